@@ -1,0 +1,161 @@
+"""ORACLE -- test infrastructure only.
+
+CPU restatement of the reference's host-side algorithms for the KV block
+extract/insert path (see kvx_oracle.c for the file:line each C function
+follows). Only tests/, ``__graft_entry__.smoke()`` and the CPU-baseline leg
+of ``bench.py`` import this package, and only as the checker or the timed
+CPU baseline. The product library never calls it.
+
+Parity status of each function (what pins it):
+  validate / coalesce / offsets_impl / build_coalesced_copy_spec:
+      brute force (expanding runs reproduces the 1-block list) and the
+      reference tests' known answers (tests/golden/reference_cases.json).
+  transfer (D2h/H2d byte semantics), read_block / write_block,
+  extract / insert:
+      numpy fancy indexing (pool[:, ids]) as an independent library routine,
+      round trips, untouched-block checks and the reference's e2e known
+      answers (shift copy, partial chunks, auto-allocate).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libkvx_oracle.so")
+_lib = None
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_u8pp = ctypes.POINTER(ctypes.c_void_p)
+
+
+def build():
+    """Compiles the C oracle with gcc (CPU only)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        l = ctypes.CDLL(_LIB_PATH)
+        l.oracle_validate.argtypes = [_i64p, ctypes.c_int64, _i64p, ctypes.c_int64,
+                                      _i64p, ctypes.c_int64]
+        for fn in (l.oracle_coalesce, l.oracle_build_coalesced_copy_spec):
+            fn.restype = ctypes.c_int64
+        l.oracle_coalesce.argtypes = [_i64p, _i64p, _i64p, ctypes.c_int64,
+                                      _i64p, _i64p, _i64p]
+        l.oracle_build_coalesced_copy_spec.argtypes = [_i64p, _i64p, ctypes.c_int64,
+                                                       _i64p, _i64p, _i64p]
+        l.oracle_offsets_impl.restype = ctypes.c_int64
+        l.oracle_offsets_impl.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int,
+                                          _i64p, _i64p, _i64p]
+        l.oracle_transfer.argtypes = [ctypes.c_int, _u8pp, _i64p, _u8pp, _i64p,
+                                      _i64p, _i64p, ctypes.c_int64,
+                                      _i64p, ctypes.c_int64, _i64p, ctypes.c_int64,
+                                      _i64p, ctypes.c_int64]
+        l.oracle_read_block.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int, ctypes.c_void_p]
+        l.oracle_write_block.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_int64]
+        for fn in (l.oracle_extract, l.oracle_insert):
+            fn.argtypes = [_u8pp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                           _i64p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                           ctypes.c_int]
+        _lib = l
+    return _lib
+
+
+def _arr(a):
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.int64))
+    return a, a.ctypes.data_as(_i64p)
+
+
+def validate(src, dst, sizes):
+    s, sp = _arr(src)
+    d, dp = _arr(dst)
+    z, zp = _arr(sizes)
+    return lib().oracle_validate(sp, len(s), dp, len(d), zp, len(z))
+
+
+def _runs(fn, ids):
+    n = len(ids)
+    outs = [np.zeros(max(n, 1), np.int64) for _ in range(3)]
+    ptrs = [o.ctypes.data_as(_i64p) for o in outs]
+    m = fn(*ptrs)
+    return [o[:m].tolist() for o in outs]
+
+
+def coalesce(src, dst, sizes):
+    s, sp = _arr(src)
+    d, dp = _arr(dst)
+    z, zp = _arr(sizes)
+    return _runs(lambda *p: lib().oracle_coalesce(sp, dp, zp, len(s), *p), s)
+
+
+def offsets_impl(ids, source_is_compact):
+    a, ap = _arr(ids)
+    return _runs(lambda *p: lib().oracle_offsets_impl(ap, len(a), int(source_is_compact), *p), a)
+
+
+def build_coalesced_copy_spec(src_ids, dst_ids):
+    s, sp = _arr(src_ids)
+    d, dp = _arr(dst_ids)
+    if len(s) != len(d):
+        raise ValueError("src and dst block lists must have same length")
+    return _runs(lambda *p: lib().oracle_build_coalesced_copy_spec(sp, dp, len(s), *p), s)
+
+
+def _ptrs(bufs):
+    arr = (ctypes.c_void_p * len(bufs))(*[b.ctypes.data if b is not None else None
+                                          for b in bufs])
+    return ctypes.cast(arr, _u8pp), arr
+
+
+def transfer(d2h, dev, host, block_bytes, phys_bytes, src, dst, sizes):
+    """D2h (d2h=True) / H2d between lists of uint8 numpy buffers; returns code."""
+    dp, keep1 = _ptrs(dev)
+    hp, keep2 = _ptrs(host)
+    db, dbp = _arr([d.nbytes for d in dev])
+    hb, hbp = _arr([h.nbytes if h is not None else 0 for h in host])
+    bb, bbp = _arr(block_bytes)
+    pb, pbp = _arr(phys_bytes)
+    s, sp = _arr(src)
+    d, dpp = _arr(dst)
+    z, zp = _arr(sizes)
+    return lib().oracle_transfer(int(bool(d2h)), dp, dbp, hp, hbp, bbp, pbp, len(dev),
+                                 sp, len(s), dpp, len(d), zp, len(z))
+
+
+def read_block(host, block_bytes, block_id):
+    out = np.zeros(block_bytes, np.uint8)
+    rc = lib().oracle_read_block(host.ctypes.data, host.nbytes, block_bytes, block_id,
+                                 out.ctypes.data)
+    return rc, out
+
+
+def write_block(host, block_bytes, block_id, payload):
+    payload = np.ascontiguousarray(payload, dtype=np.uint8)
+    return lib().oracle_write_block(host.ctypes.data, host.nbytes, block_bytes, block_id,
+                                    payload.ctypes.data, payload.nbytes)
+
+
+def extract(pools, block_bytes, ids, order=0, nthreads=1, staging=None):
+    """Packs blocks `ids` of every pool into staging; returns (code, staging)."""
+    pp, keep = _ptrs(pools)
+    a, ap = _arr(ids)
+    if staging is None:
+        staging = np.zeros(len(pools) * len(a) * block_bytes, np.uint8)
+    rc = lib().oracle_extract(pp, len(pools), pools[0].nbytes, block_bytes, ap, len(a),
+                              staging.ctypes.data, order, nthreads)
+    return rc, staging
+
+
+def insert(pools, block_bytes, ids, staging, order=0, nthreads=1):
+    pp, keep = _ptrs(pools)
+    a, ap = _arr(ids)
+    staging = np.ascontiguousarray(staging, dtype=np.uint8)
+    return lib().oracle_insert(pp, len(pools), pools[0].nbytes, block_bytes, ap, len(a),
+                               staging.ctypes.data, order, nthreads)

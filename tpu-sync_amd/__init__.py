@@ -1,0 +1,16 @@
+"""MI355X-native KV block extract/insert and pinned-host offload/reload.
+
+Import name ``tpu_sync_amd``; the package lives in the ``tpu-sync_amd``
+directory. The compute path is libkvx.so (host C++ + gfx950 HIP kernels);
+this package is a thin ctypes layer that only passes pointers.
+"""
+from . import _capi
+from ._capi import KvxError
+from .kv_cache_manager import KVCacheManager, LogicalBlockManager, RaidenFuture
+
+__all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError",
+           "library_path"]
+
+
+def library_path() -> str:
+    return _capi.LIB_PATH

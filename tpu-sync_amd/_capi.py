@@ -1,0 +1,161 @@
+"""ctypes binding of libkvx.so (the C-ABI declared in include/kvx.h).
+
+Only pointers and sizes cross this boundary: device tensors are passed as
+``tensor.data_ptr()``, streams as ``stream.cuda_stream``. The library must
+have been built (``make -C tpu-sync_amd/csrc``); importing this module
+without it raises, there is no fallback path.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libkvx.so")
+
+STATUS_NAMES = {
+    0: "OK", 1: "CANCELLED", 2: "UNKNOWN", 3: "INVALID_ARGUMENT",
+    4: "DEADLINE_EXCEEDED", 5: "NOT_FOUND", 6: "ALREADY_EXISTS",
+    7: "PERMISSION_DENIED", 8: "RESOURCE_EXHAUSTED", 9: "FAILED_PRECONDITION",
+    10: "ABORTED", 11: "OUT_OF_RANGE", 12: "UNIMPLEMENTED", 13: "INTERNAL",
+    14: "UNAVAILABLE", 15: "DATA_LOSS",
+}
+
+HOST_MALLOC, HOST_PINNED, HOST_SHM = 0, 1, 2
+LAYER_MAJOR, BLOCK_MAJOR = 0, 1
+
+
+class KvxError(RuntimeError):
+    """A non-OK status from libkvx; ``code`` is the absl::StatusCode number."""
+
+    def __init__(self, code, message, where=""):
+        self.code = code
+        self.status = STATUS_NAMES.get(code, str(code))
+        prefix = f"{where} failed: " if where else ""
+        super().__init__(f"{prefix}{message}")
+
+
+class ManagerConfig(ctypes.Structure):
+    _fields_ = [
+        ("device", ctypes.c_int32),
+        ("host_alloc", ctypes.c_int32),
+        ("num_layers", ctypes.c_int64),
+        ("num_shards", ctypes.c_int64),
+        ("device_ptrs", ctypes.POINTER(ctypes.c_uint64)),
+        ("device_bytes", ctypes.POINTER(ctypes.c_int64)),
+        ("major_dim", ctypes.c_int64),
+        ("slice_byte_size", ctypes.c_int64),
+        ("host_blocks", ctypes.c_int64),
+        ("staging_chunk_bytes", ctypes.c_int64),
+        ("staging_chunks", ctypes.c_int64),
+        ("direct_min_bytes", ctypes.c_int64),
+        ("shm_key", ctypes.c_char_p),
+        ("shm_server_name", ctypes.c_char_p),
+        ("model_uid", ctypes.c_char_p),
+        ("profile_kernels", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_i32, _i64, _u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
+_vp, _i64p, _i32p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_int = ctypes.c_int
+
+# name: (restype, argtypes)
+PROTOTYPES = {
+    "kvx_last_error": (ctypes.c_char_p, []),
+    "kvx_version": (ctypes.c_char_p, []),
+    "kvx_manager_create": (_int, [ctypes.POINTER(ManagerConfig), ctypes.POINTER(_vp)]),
+    "kvx_manager_destroy": (None, [_vp]),
+    "kvx_manager_d2h": (_int, [_vp, _i64p, _i64, _i64p, _i64, _i64p, _i64, _i64, _i64,
+                               _i64, _vp, ctypes.POINTER(_vp)]),
+    "kvx_manager_h2d": (_int, [_vp, _i64p, _i64, _i64p, _i64, _i64p, _i64, _i64, _i64,
+                               _i64, _vp, ctypes.POINTER(_vp)]),
+    "kvx_manager_d2h_auto_allocate": (_int, [_vp, _i64p, _i64, _i64p, _i64, _i32p, _i64,
+                                             _i64p, _vp, ctypes.POINTER(_vp)]),
+    "kvx_manager_gather": (_int, [_vp, _i64p, _i64, _u64, _i64, _i32, _i64, _i64, _vp,
+                                  ctypes.POINTER(_vp)]),
+    "kvx_manager_scatter": (_int, [_vp, _i64p, _i64, _u64, _i64, _i32, _i64, _i64, _vp,
+                                   ctypes.POINTER(_vp)]),
+    "kvx_manager_configure_host_staging_slots": (_int, [_vp, _i64, _i64]),
+    "kvx_manager_host_span": (_int, [_vp, _i64, _i64, _i64, _i64, _u64p, _i64p, _i64p]),
+    "kvx_manager_block_host_ptr": (_int, [_vp, _i64, _i64, _i32, _u64p]),
+    "kvx_manager_read_block": (_int, [_vp, _i64, _i32, _i64, _vp, _i64]),
+    "kvx_manager_write_block": (_int, [_vp, _i64, _i32, _i64, _vp, _i64]),
+    "kvx_manager_num_layers": (_i64, [_vp]),
+    "kvx_manager_num_shards": (_i64, [_vp]),
+    "kvx_manager_major_dim": (_i64, [_vp]),
+    "kvx_manager_host_blocks": (_i64, [_vp]),
+    "kvx_manager_bytes_per_block": (_i64, [_vp]),
+    "kvx_manager_layer_block_byte_size": (_i64, [_vp, _i64]),
+    "kvx_manager_num_block_arrays": (_i64, [_vp]),
+    "kvx_manager_block_bytes": (_i64, [_vp, _i64]),
+    "kvx_manager_block_array_host_ptr": (_u64, [_vp, _i64, _i64]),
+    "kvx_manager_block_array_host_size": (_i64, [_vp, _i64, _i64]),
+    "kvx_manager_allocated_host_bytes": (_i64, [_vp]),
+    "kvx_manager_wait_for_pending_work": (_int, [_vp]),
+    "kvx_manager_engine_stats": (_int, [_vp, _i64p]),
+    "kvx_manager_kernel_times": (_int, [_vp, _i32, _i32, _i64p,
+                                        ctypes.POINTER(ctypes.c_double), _i64p]),
+    "kvx_future_is_ready": (_int, [_vp]),
+    "kvx_future_poll_error": (_int, [_vp]),
+    "kvx_future_await": (_int, [_vp]),
+    "kvx_future_wait_on_stream": (_int, [_vp, _vp]),
+    "kvx_future_release": (None, [_vp]),
+    "kvx_block_manager_create": (_int, [_i32, ctypes.POINTER(_vp)]),
+    "kvx_block_manager_destroy": (None, [_vp]),
+    "kvx_manager_host_block_manager": (_vp, [_vp]),
+    "kvx_block_manager_allocate": (_int, [_vp, _i32, _i32, _i32p]),
+    "kvx_block_manager_allocate_target": (_int, [_vp, _i32p, _i64]),
+    "kvx_block_manager_unlock": (_int, [_vp, _i32p, _i64]),
+    "kvx_block_manager_deallocate": (_int, [_vp, _i32p, _i64]),
+    "kvx_block_manager_access": (_int, [_vp, _i32]),
+    "kvx_block_manager_is_allocated": (_i32, [_vp, _i32]),
+    "kvx_block_manager_is_locked": (_i32, [_vp, _i32]),
+    "kvx_block_manager_total_blocks": (_i32, [_vp]),
+    "kvx_block_manager_num_free": (_i32, [_vp]),
+    "kvx_block_manager_num_allocated": (_i32, [_vp]),
+    "kvx_block_manager_num_locked": (_i32, [_vp]),
+    "kvx_gather_blocks": (_int, [_u64, _i64, _i64, _i64, _u64, _i64, _u64, _i32, _u64, _vp]),
+    "kvx_scatter_blocks": (_int, [_u64, _i64, _i64, _i64, _u64, _i64, _u64, _i32, _u64, _vp]),
+}
+
+_lib = None
+
+
+def load():
+    """Loads libkvx.so once and declares every prototype."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `make -C tpu-sync_amd/csrc` "
+            "(or __graft_entry__.build()); there is no CPU fallback")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error():
+    return load().kvx_last_error().decode(errors="replace")
+
+
+def check(code, where=""):
+    if code != 0:
+        raise KvxError(code, last_error(), where)
+
+
+def i64_array(values):
+    vals = [int(v) for v in values]
+    arr = (ctypes.c_int64 * max(len(vals), 1))(*vals)
+    return arr, len(vals)
+
+
+def i32_array(values):
+    vals = [int(v) for v in values]
+    arr = (ctypes.c_int32 * max(len(vals), 1))(*vals)
+    return arr, len(vals)

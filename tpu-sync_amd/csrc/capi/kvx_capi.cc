@@ -1,0 +1,539 @@
+// extern "C" layer over the C++ manager, futures and block allocator.
+// Each entry point validates its arguments, calls the C++ object and turns
+// a Status into its code plus a thread-local message.
+#include "../../../include/kvx.h"
+
+#include <cstring>
+#include <memory>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "../host/copy_future.h"
+#include "../host/kv_cache_manager.h"
+#include "../host/logical_block_manager.h"
+#include "../kernels/block_copy.h"
+
+struct kvx_block_manager {
+  kvx::LogicalBlockManager* lbm = nullptr;
+  std::unique_ptr<kvx::LogicalBlockManager> owned;
+  std::mutex* mu = nullptr;  // the owning manager's lock, if any
+};
+
+struct kvx_manager {
+  std::unique_ptr<kvx::KVCacheManager> impl;
+  kvx_block_manager lbm_view;  // borrowed view of the manager's allocator
+};
+
+struct kvx_future {
+  kvx::CopyFuture f;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int Fail(const kvx::Status& s) {
+  g_last_error = s.message();
+  return static_cast<int>(s.code());
+}
+
+int Fail(int code, const char* msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int Done(const kvx::Status& s) {
+  if (!s.ok()) return Fail(s);
+  return KVX_OK;
+}
+
+std::vector<int64_t> Vec(const int64_t* p, int64_t n) {
+  if (p == nullptr || n <= 0) return {};
+  return std::vector<int64_t>(p, p + n);
+}
+
+std::optional<int64_t> Opt(int64_t v) {
+  return v < 0 ? std::nullopt : std::optional<int64_t>(v);
+}
+
+std::optional<size_t> OptIdx(int64_t v) {
+  return v < 0 ? std::nullopt : std::optional<size_t>(static_cast<size_t>(v));
+}
+
+bool BadArray(const void* p, int64_t n) { return n < 0 || (n > 0 && p == nullptr); }
+
+int EmitFuture(kvx::StatusOr<kvx::CopyFuture> r, kvx_future** out) {
+  if (!r.ok()) return Fail(r.status());
+  *out = new kvx_future{std::move(r).value()};
+  return KVX_OK;
+}
+
+struct LbmLock {
+  explicit LbmLock(kvx_block_manager* b) : mu(b->mu) {
+    if (mu) mu->lock();
+  }
+  ~LbmLock() {
+    if (mu) mu->unlock();
+  }
+  std::mutex* mu;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* kvx_last_error(void) { return g_last_error.c_str(); }
+
+const char* kvx_version(void) { return "kvx 0.1.0 gfx950"; }
+
+int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
+  if (cfg == nullptr || out == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null config or output");
+  }
+  *out = nullptr;
+  kvx::ManagerConfig c;
+  c.device = cfg->device;
+  c.num_layers = cfg->num_layers;
+  c.num_shards = cfg->num_shards;
+  const int64_t nstor = cfg->num_layers * cfg->num_shards;
+  if (cfg->num_layers < 0 || cfg->num_shards < 0) {
+    return Fail(KVX_INVALID_ARGUMENT, "num_layers and num_shards must be non-negative");
+  }
+  if (cfg->device_ptrs != nullptr) {
+    if (cfg->device_bytes == nullptr) {
+      return Fail(KVX_INVALID_ARGUMENT, "device_bytes is required with device_ptrs");
+    }
+    c.device_ptrs.assign(cfg->device_ptrs, cfg->device_ptrs + nstor);
+    c.device_bytes.assign(cfg->device_bytes, cfg->device_bytes + nstor);
+  }
+  c.major_dim = cfg->major_dim;
+  c.slice_byte_size = cfg->slice_byte_size;
+  c.host_blocks = cfg->host_blocks;
+  if (cfg->host_alloc < 0 || cfg->host_alloc > 2) {
+    return Fail(KVX_INVALID_ARGUMENT, "unknown host_alloc kind");
+  }
+  c.host_alloc = static_cast<kvx::HostAllocKind>(cfg->host_alloc);
+  if (cfg->shm_key) c.shm_key = cfg->shm_key;
+  if (cfg->shm_server_name) c.shm_server_name = cfg->shm_server_name;
+  if (cfg->model_uid) c.model_uid = cfg->model_uid;
+  if (cfg->staging_chunk_bytes > 0) c.engine.staging_chunk_bytes = cfg->staging_chunk_bytes;
+  if (cfg->staging_chunks > 0) c.engine.staging_chunks = static_cast<int>(cfg->staging_chunks);
+  if (cfg->direct_min_bytes > 0) c.engine.direct_min_bytes = cfg->direct_min_bytes;
+  c.engine.profile_kernels = cfg->profile_kernels != 0;
+  auto r = kvx::KVCacheManager::Create(std::move(c));
+  if (!r.ok()) return Fail(r.status());
+  auto* m = new kvx_manager;
+  m->impl = std::move(r).value();
+  m->lbm_view.lbm = m->impl->host_block_manager();
+  m->lbm_view.mu = &m->impl->host_block_mutex();
+  *out = m;
+  return KVX_OK;
+}
+
+void kvx_manager_destroy(kvx_manager* m) { delete m; }
+
+static int Transfer(bool d2h, kvx_manager* m, const int64_t* src, int64_t n_src,
+                    const int64_t* dst, int64_t n_dst, const int64_t* sizes,
+                    int64_t n_sizes, int64_t slot_idx, int64_t layer_idx,
+                    int64_t shard_idx, void* stream, kvx_future** out) {
+  if (m == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  if (BadArray(src, n_src) || BadArray(dst, n_dst) || BadArray(sizes, n_sizes)) {
+    return Fail(KVX_INVALID_ARGUMENT, "null array with a positive length");
+  }
+  auto s = Vec(src, n_src);
+  auto d = Vec(dst, n_dst);
+  auto z = Vec(sizes, n_sizes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto r = d2h ? m->impl->D2h(s, d, z, Opt(slot_idx), OptIdx(layer_idx),
+                              OptIdx(shard_idx), st)
+               : m->impl->H2d(s, d, z, Opt(slot_idx), OptIdx(layer_idx),
+                              OptIdx(shard_idx), st);
+  return EmitFuture(std::move(r), out);
+}
+
+int kvx_manager_d2h(kvx_manager* m, const int64_t* src, int64_t n_src,
+                    const int64_t* dst, int64_t n_dst, const int64_t* sizes,
+                    int64_t n_sizes, int64_t slot_idx, int64_t layer_idx,
+                    int64_t shard_idx, void* stream, kvx_future** out) {
+  return Transfer(true, m, src, n_src, dst, n_dst, sizes, n_sizes, slot_idx,
+                  layer_idx, shard_idx, stream, out);
+}
+
+int kvx_manager_h2d(kvx_manager* m, const int64_t* src, int64_t n_src,
+                    const int64_t* dst, int64_t n_dst, const int64_t* sizes,
+                    int64_t n_sizes, int64_t slot_idx, int64_t layer_idx,
+                    int64_t shard_idx, void* stream, kvx_future** out) {
+  return Transfer(false, m, src, n_src, dst, n_dst, sizes, n_sizes, slot_idx,
+                  layer_idx, shard_idx, stream, out);
+}
+
+int kvx_manager_d2h_auto_allocate(kvx_manager* m, const int64_t* src,
+                                  int64_t n_src, const int64_t* sizes,
+                                  int64_t n_sizes, int32_t* out_ids,
+                                  int64_t out_capacity, int64_t* out_num_ids,
+                                  void* stream, kvx_future** out) {
+  if (m == nullptr || out == nullptr || out_num_ids == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  }
+  if (BadArray(src, n_src) || BadArray(sizes, n_sizes)) {
+    return Fail(KVX_INVALID_ARGUMENT, "null array with a positive length");
+  }
+  int64_t total = 0;
+  for (int64_t i = 0; i < n_sizes; ++i) total += sizes[i] > 0 ? sizes[i] : 0;
+  if (out_capacity < total || (total > 0 && out_ids == nullptr)) {
+    return Fail(KVX_INVALID_ARGUMENT, "out_ids capacity smaller than sum(sizes)");
+  }
+  auto r = m->impl->D2hAutoAllocate(Vec(src, n_src), Vec(sizes, n_sizes),
+                                    static_cast<hipStream_t>(stream));
+  if (!r.ok()) return Fail(r.status());
+  auto& ids = r->first;
+  for (size_t i = 0; i < ids.size(); ++i) out_ids[i] = ids[i];
+  *out_num_ids = static_cast<int64_t>(ids.size());
+  *out = new kvx_future{std::move(r->second)};
+  return KVX_OK;
+}
+
+static int DeviceCopy(bool gather, kvx_manager* m, const int64_t* ids,
+                      int64_t n, uint64_t staging, int64_t staging_bytes,
+                      int32_t order, int64_t layer_idx, int64_t shard_idx,
+                      void* stream, kvx_future** out) {
+  if (m == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  if (BadArray(ids, n)) return Fail(KVX_INVALID_ARGUMENT, "null ids with a positive length");
+  if (order != KVX_LAYER_MAJOR && order != KVX_BLOCK_MAJOR) {
+    return Fail(KVX_INVALID_ARGUMENT, "unknown staging order");
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto v = Vec(ids, n);
+  auto r = gather ? m->impl->Gather(v, staging, staging_bytes, order == KVX_BLOCK_MAJOR,
+                                    OptIdx(layer_idx), OptIdx(shard_idx), st)
+                  : m->impl->Scatter(v, staging, staging_bytes, order == KVX_BLOCK_MAJOR,
+                                     OptIdx(layer_idx), OptIdx(shard_idx), st);
+  return EmitFuture(std::move(r), out);
+}
+
+int kvx_manager_gather(kvx_manager* m, const int64_t* ids, int64_t n,
+                       uint64_t staging, int64_t staging_bytes, int32_t order,
+                       int64_t layer_idx, int64_t shard_idx, void* stream,
+                       kvx_future** out) {
+  return DeviceCopy(true, m, ids, n, staging, staging_bytes, order, layer_idx,
+                    shard_idx, stream, out);
+}
+
+int kvx_manager_scatter(kvx_manager* m, const int64_t* ids, int64_t n,
+                        uint64_t staging, int64_t staging_bytes, int32_t order,
+                        int64_t layer_idx, int64_t shard_idx, void* stream,
+                        kvx_future** out) {
+  return DeviceCopy(false, m, ids, n, staging, staging_bytes, order, layer_idx,
+                    shard_idx, stream, out);
+}
+
+int kvx_manager_configure_host_staging_slots(kvx_manager* m, int64_t num_slots,
+                                             int64_t max_major_per_slot) {
+  if (m == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager");
+  return Done(m->impl->ConfigureHostStagingSlots(num_slots, max_major_per_slot));
+}
+
+int kvx_manager_host_span(kvx_manager* m, int64_t layer_idx, int64_t shard_idx,
+                          int64_t slot_idx, int64_t num_major,
+                          uint64_t* out_ptr, int64_t* out_nbytes,
+                          int64_t* out_base_major) {
+  if (m == nullptr || out_ptr == nullptr || out_nbytes == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  }
+  if (layer_idx < 0 || shard_idx < 0) {
+    return Fail(KVX_OUT_OF_RANGE, "HostSpan layer or shard index out of range");
+  }
+  auto r = m->impl->HostSpan(static_cast<size_t>(layer_idx),
+                             static_cast<size_t>(shard_idx), slot_idx, num_major);
+  if (!r.ok()) return Fail(r.status());
+  *out_ptr = reinterpret_cast<uint64_t>(r->ptr);
+  *out_nbytes = static_cast<int64_t>(r->nbytes);
+  if (out_base_major) *out_base_major = r->base_major;
+  return KVX_OK;
+}
+
+int kvx_manager_block_host_ptr(kvx_manager* m, int64_t layer_idx,
+                               int64_t shard_idx, int32_t block_id,
+                               uint64_t* out_ptr) {
+  if (m == nullptr || out_ptr == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  if (layer_idx < 0 || shard_idx < 0) {
+    return Fail(KVX_OUT_OF_RANGE, "layer or shard index out of range");
+  }
+  auto r = m->impl->GetBlockHostPointerValue(static_cast<size_t>(layer_idx),
+                                             static_cast<size_t>(shard_idx), block_id);
+  if (!r.ok()) return Fail(r.status());
+  *out_ptr = static_cast<uint64_t>(r.value());
+  return KVX_OK;
+}
+
+int kvx_manager_read_block(kvx_manager* m, int64_t layer_idx, int32_t block_id,
+                           int64_t shard_idx, void* buf, int64_t len) {
+  if (m == nullptr || buf == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or buffer");
+  if (layer_idx < 0 || shard_idx < 0) {
+    return Fail(KVX_OUT_OF_RANGE, "layer or shard index out of range");
+  }
+  auto r = m->impl->ReadBlockBytes(static_cast<size_t>(layer_idx), block_id,
+                                   static_cast<size_t>(shard_idx));
+  if (!r.ok()) return Fail(r.status());
+  if (static_cast<int64_t>(r->size()) != len) {
+    return Fail(KVX_INVALID_ARGUMENT, "buffer length must equal the block size");
+  }
+  std::memcpy(buf, r->data(), r->size());
+  return KVX_OK;
+}
+
+int kvx_manager_write_block(kvx_manager* m, int64_t layer_idx,
+                            int32_t block_id, int64_t shard_idx,
+                            const void* buf, int64_t len) {
+  if (m == nullptr || (buf == nullptr && len > 0)) {
+    return Fail(KVX_INVALID_ARGUMENT, "null manager or buffer");
+  }
+  if (layer_idx < 0 || shard_idx < 0 || len < 0) {
+    return Fail(KVX_OUT_OF_RANGE, "layer or shard index out of range");
+  }
+  return Done(m->impl->WriteBlockBytes(static_cast<size_t>(layer_idx), block_id,
+                                       buf, static_cast<size_t>(len),
+                                       static_cast<size_t>(shard_idx)));
+}
+
+int64_t kvx_manager_num_layers(const kvx_manager* m) {
+  return m ? static_cast<int64_t>(m->impl->num_layers()) : -1;
+}
+int64_t kvx_manager_num_shards(const kvx_manager* m) {
+  return m ? static_cast<int64_t>(m->impl->num_shards()) : -1;
+}
+int64_t kvx_manager_major_dim(const kvx_manager* m) {
+  return m ? m->impl->major_dim() : -1;
+}
+int64_t kvx_manager_host_blocks(const kvx_manager* m) {
+  return m ? m->impl->host_blocks() : -1;
+}
+int64_t kvx_manager_bytes_per_block(const kvx_manager* m) {
+  return m ? static_cast<int64_t>(m->impl->bytes_per_block()) : -1;
+}
+int64_t kvx_manager_layer_block_byte_size(const kvx_manager* m, int64_t layer_idx) {
+  if (m == nullptr || layer_idx < 0) return -1;
+  return m->impl->LayerBlockByteSize(static_cast<size_t>(layer_idx));
+}
+int64_t kvx_manager_num_block_arrays(const kvx_manager* m) {
+  return m ? static_cast<int64_t>(m->impl->num_block_arrays()) : -1;
+}
+int64_t kvx_manager_block_bytes(const kvx_manager* m, int64_t block_array_idx) {
+  if (m == nullptr || block_array_idx < 0) return -1;
+  return static_cast<int64_t>(m->impl->block_bytes(static_cast<size_t>(block_array_idx)));
+}
+uint64_t kvx_manager_block_array_host_ptr(kvx_manager* m, int64_t block_array_idx,
+                                          int64_t shard_idx) {
+  if (m == nullptr || block_array_idx < 0 || shard_idx < 0) return 0;
+  return reinterpret_cast<uint64_t>(m->impl->GetBlockArrayHostPointer(
+      static_cast<size_t>(block_array_idx), static_cast<size_t>(shard_idx)));
+}
+int64_t kvx_manager_block_array_host_size(kvx_manager* m, int64_t block_array_idx,
+                                          int64_t shard_idx) {
+  if (m == nullptr || block_array_idx < 0 || shard_idx < 0) return 0;
+  return static_cast<int64_t>(m->impl->GetBlockArrayHostSize(
+      static_cast<size_t>(block_array_idx), static_cast<size_t>(shard_idx)));
+}
+int64_t kvx_manager_allocated_host_bytes(const kvx_manager* m) {
+  return m ? static_cast<int64_t>(m->impl->GetAllocatedHostDramBytes()) : -1;
+}
+int kvx_manager_wait_for_pending_work(kvx_manager* m) {
+  if (m == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager");
+  return Done(m->impl->WaitForPendingWork());
+}
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out5) {
+  if (m == nullptr || out5 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  if (m->impl->engine() == nullptr) {
+    return Fail(KVX_FAILED_PRECONDITION, "CPU-only manager has no transfer engine");
+  }
+  kvx::EngineStats s = m->impl->engine()->stats();
+  out5[0] = s.direct_copies;
+  out5[1] = s.staged_copies;
+  out5[2] = s.memcpy_calls;
+  out5[3] = s.kernel_launches;
+  out5[4] = s.chunks;
+  return KVX_OK;
+}
+
+int kvx_manager_kernel_times(kvx_manager* m, int32_t gather, int32_t reset,
+                             int64_t* out_launches, double* out_total_ms,
+                             int64_t* out_bytes) {
+  if (m == nullptr || out_launches == nullptr || out_total_ms == nullptr ||
+      out_bytes == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  }
+  if (m->impl->engine() == nullptr) {
+    return Fail(KVX_FAILED_PRECONDITION, "CPU-only manager has no transfer engine");
+  }
+  auto r = m->impl->engine()->ProfiledKernelTimes(gather != 0, reset != 0);
+  if (!r.ok()) return Fail(r.status());
+  *out_launches = r->launches;
+  *out_total_ms = r->total_ms;
+  *out_bytes = r->bytes;
+  return KVX_OK;
+}
+
+int kvx_future_is_ready(kvx_future* f) { return f && f->f.IsReady() ? 1 : 0; }
+int kvx_future_poll_error(kvx_future* f) {
+  if (f == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null future");
+  return Done(f->f.PollError());
+}
+int kvx_future_await(kvx_future* f) {
+  if (f == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null future");
+  return Done(f->f.Await());
+}
+int kvx_future_wait_on_stream(kvx_future* f, void* stream) {
+  if (f == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null future");
+  return Done(f->f.WaitOnStream(static_cast<hipStream_t>(stream)));
+}
+void kvx_future_release(kvx_future* f) { delete f; }
+
+int kvx_block_manager_create(int32_t num_blocks, kvx_block_manager** out) {
+  if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
+  if (num_blocks < 0) return Fail(KVX_INVALID_ARGUMENT, "num_blocks must be non-negative");
+  auto* b = new kvx_block_manager;
+  b->owned = std::make_unique<kvx::LogicalBlockManager>(num_blocks);
+  b->lbm = b->owned.get();
+  *out = b;
+  return KVX_OK;
+}
+
+void kvx_block_manager_destroy(kvx_block_manager* b) {
+  if (b != nullptr && b->owned) delete b;
+}
+
+kvx_block_manager* kvx_manager_host_block_manager(kvx_manager* m) {
+  return m == nullptr ? nullptr : &m->lbm_view;
+}
+
+static std::vector<int> Ids(const int32_t* ids, int64_t n) {
+  if (ids == nullptr || n <= 0) return {};
+  return std::vector<int>(ids, ids + n);
+}
+
+int kvx_block_manager_allocate(kvx_block_manager* b, int32_t n, int32_t lock,
+                               int32_t* out_ids) {
+  if (b == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null block manager");
+  LbmLock l(b);
+  auto r = b->lbm->Allocate(n, lock != 0);
+  if (!r.ok()) return Fail(r.status());
+  if (out_ids == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
+  for (size_t i = 0; i < r->size(); ++i) out_ids[i] = (*r)[i];
+  return KVX_OK;
+}
+int kvx_block_manager_allocate_target(kvx_block_manager* b, const int32_t* ids,
+                                      int64_t n) {
+  if (b == nullptr || BadArray(ids, n)) return Fail(KVX_INVALID_ARGUMENT, "null argument");
+  LbmLock l(b);
+  return Done(b->lbm->AllocateTarget(Ids(ids, n)));
+}
+int kvx_block_manager_unlock(kvx_block_manager* b, const int32_t* ids, int64_t n) {
+  if (b == nullptr || BadArray(ids, n)) return Fail(KVX_INVALID_ARGUMENT, "null argument");
+  LbmLock l(b);
+  return Done(b->lbm->Unlock(Ids(ids, n)));
+}
+int kvx_block_manager_deallocate(kvx_block_manager* b, const int32_t* ids,
+                                 int64_t n) {
+  if (b == nullptr || BadArray(ids, n)) return Fail(KVX_INVALID_ARGUMENT, "null argument");
+  LbmLock l(b);
+  return Done(b->lbm->Deallocate(Ids(ids, n)));
+}
+int kvx_block_manager_access(kvx_block_manager* b, int32_t id) {
+  if (b == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null block manager");
+  LbmLock l(b);
+  return Done(b->lbm->AccessBlock(id));
+}
+int32_t kvx_block_manager_is_allocated(kvx_block_manager* b, int32_t id) {
+  if (b == nullptr) return 0;
+  LbmLock l(b);
+  return b->lbm->IsAllocated(id) ? 1 : 0;
+}
+int32_t kvx_block_manager_is_locked(kvx_block_manager* b, int32_t id) {
+  if (b == nullptr) return 0;
+  LbmLock l(b);
+  return b->lbm->IsLocked(id) ? 1 : 0;
+}
+int32_t kvx_block_manager_total_blocks(kvx_block_manager* b) {
+  if (b == nullptr) return -1;
+  LbmLock l(b);
+  return b->lbm->total_blocks();
+}
+int32_t kvx_block_manager_num_free(kvx_block_manager* b) {
+  if (b == nullptr) return -1;
+  LbmLock l(b);
+  return b->lbm->num_free_blocks();
+}
+int32_t kvx_block_manager_num_allocated(kvx_block_manager* b) {
+  if (b == nullptr) return -1;
+  LbmLock l(b);
+  return b->lbm->num_allocated_blocks();
+}
+int32_t kvx_block_manager_num_locked(kvx_block_manager* b) {
+  if (b == nullptr) return -1;
+  LbmLock l(b);
+  return b->lbm->num_locked_blocks();
+}
+
+static int RawCopy(bool gather, uint64_t storage_table, int64_t num_storages,
+                   int64_t block_bytes, int64_t pool_blocks, uint64_t ids,
+                   int64_t n, uint64_t staging, int32_t order, uint64_t error,
+                   void* stream) {
+  if (storage_table == 0 || ids == 0 || staging == 0) {
+    return Fail(KVX_INVALID_ARGUMENT, "null device pointer");
+  }
+  if (num_storages <= 0 || n <= 0 || block_bytes <= 0 || pool_blocks <= 0) {
+    return Fail(KVX_INVALID_ARGUMENT, "sizes must be positive");
+  }
+  if (order != KVX_LAYER_MAJOR && order != KVX_BLOCK_MAJOR) {
+    return Fail(KVX_INVALID_ARGUMENT, "unknown staging order");
+  }
+  if (num_storages * n > UINT32_MAX || n > INT32_MAX) {
+    return Fail(KVX_INVALID_ARGUMENT, "too many blocks for one launch");
+  }
+  kvx::CopyLaunch l;
+  l.npieces = 1;
+  l.ids = reinterpret_cast<const int64_t*>(ids);
+  l.n = n;
+  l.error = reinterpret_cast<int32_t*>(error);
+  kvx::CopyPiece& p = l.pieces[0];
+  p.storages = storage_table;
+  p.staging = staging;
+  p.stride_w = order == KVX_BLOCK_MAJOR ? block_bytes : n * block_bytes;
+  p.stride_i = order == KVX_BLOCK_MAJOR ? num_storages * block_bytes : block_bytes;
+  p.f0 = 0;
+  p.nblocks = num_storages * n;
+  p.block_bytes = block_bytes;
+  p.pool_blocks = pool_blocks;
+  // The storage bases are device data the host cannot inspect; the vector
+  // width follows block_bytes and staging. gfx950 global memory accepts
+  // unaligned vector accesses, so a base that is not 16-byte aligned is slower
+  // but still copied exactly.
+  const int vec = kvx::LaunchVectorBytes(l, 0);
+  hipError_t e = kvx::LaunchBlockCopy(
+      l, gather ? kvx::CopyDir::kGather : kvx::CopyDir::kScatter, vec,
+      static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    g_last_error = std::string("kernel launch failed: ") + hipGetErrorString(e);
+    return e == hipErrorInvalidValue ? KVX_INVALID_ARGUMENT : KVX_INTERNAL;
+  }
+  return KVX_OK;
+}
+
+int kvx_gather_blocks(uint64_t storage_table, int64_t num_storages,
+                      int64_t block_bytes, int64_t pool_blocks, uint64_t ids,
+                      int64_t n, uint64_t staging, int32_t order, uint64_t error,
+                      void* stream) {
+  return RawCopy(true, storage_table, num_storages, block_bytes, pool_blocks,
+                 ids, n, staging, order, error, stream);
+}
+
+int kvx_scatter_blocks(uint64_t storage_table, int64_t num_storages,
+                       int64_t block_bytes, int64_t pool_blocks, uint64_t ids,
+                       int64_t n, uint64_t staging, int32_t order,
+                       uint64_t error, void* stream) {
+  return RawCopy(false, storage_table, num_storages, block_bytes, pool_blocks,
+                 ids, n, staging, order, error, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+#include "copy_future.h"
+
+#include <thread>
+
+#include "hip_util.h"
+
+namespace kvx {
+
+CopyFuture::State::~State() {
+  for (hipEvent_t e : events) {
+    if (e != nullptr) (void)hipEventDestroy(e);
+  }
+}
+
+CopyFuture::CopyFuture(Status status) : state_(std::make_shared<State>()) {
+  state_->status = std::move(status);
+  state_->done = true;
+}
+
+CopyFuture CopyFuture::FromEvents(std::vector<hipEvent_t> events,
+                                  std::vector<std::shared_ptr<void>> keep_alive) {
+  CopyFuture f;
+  f.state_->events = std::move(events);
+  f.state_->keep_alive = std::move(keep_alive);
+  f.state_->done = f.state_->events.empty();
+  return f;
+}
+
+CopyFuture CopyFuture::Join(const std::vector<CopyFuture>& futures) {
+  CopyFuture f;
+  f.state_->done = false;
+  for (const CopyFuture& c : futures) {
+    if (c.state_) f.state_->children.push_back(c.state_);
+  }
+  return f;
+}
+
+bool CopyFuture::StateReady(const State& s) {
+  {
+    std::lock_guard<std::mutex> l(s.mu);
+    if (s.done) return true;
+  }
+  for (const auto& c : s.children) {
+    if (!StateReady(*c)) return false;
+  }
+  for (hipEvent_t e : s.events) {
+    hipError_t q = hipEventQuery(e);
+    if (q == hipErrorNotReady) return false;
+  }
+  return true;
+}
+
+Status CopyFuture::StatePoll(const State& s) {
+  {
+    std::lock_guard<std::mutex> l(s.mu);
+    if (!s.status.ok()) return s.status;
+    if (s.done) return OkStatus();
+  }
+  for (const auto& c : s.children) {
+    Status st = StatePoll(*c);
+    if (!st.ok()) return st;
+  }
+  for (hipEvent_t e : s.events) {
+    hipError_t q = hipEventQuery(e);
+    if (q != hipSuccess && q != hipErrorNotReady) {
+      return HipStatus(q, "copy completion event");
+    }
+  }
+  return OkStatus();
+}
+
+Status CopyFuture::StateAwait(State& s) {
+  {
+    std::lock_guard<std::mutex> l(s.mu);
+    if (s.done) return s.status;
+  }
+  Status result = OkStatus();
+  for (const auto& c : s.children) {
+    Status st = StateAwait(*c);
+    if (result.ok() && !st.ok()) result = st;
+  }
+  for (hipEvent_t e : s.events) {
+    Status st = HipStatus(hipEventSynchronize(e), "copy completion event");
+    if (result.ok() && !st.ok()) result = st;
+  }
+  std::lock_guard<std::mutex> l(s.mu);
+  if (!s.done) {
+    if (s.status.ok()) s.status = result;
+    s.done = true;
+    s.keep_alive.clear();
+  }
+  return s.status;
+}
+
+bool CopyFuture::IsReady() const { return StateReady(*state_); }
+
+Status CopyFuture::PollError() const { return StatePoll(*state_); }
+
+Status CopyFuture::Await() const { return StateAwait(*state_); }
+
+Status CopyFuture::WaitOnStream(hipStream_t stream) const {
+  std::vector<const State*> stack{state_.get()};
+  while (!stack.empty()) {
+    const State* s = stack.back();
+    stack.pop_back();
+    for (const auto& c : s->children) stack.push_back(c.get());
+    for (hipEvent_t e : s->events) {
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(stream, e, 0));
+    }
+  }
+  return OkStatus();
+}
+
+void CopyFuture::OnReady(std::function<void(Status)> cb) const {
+  if (StateReady(*state_)) {
+    cb(Await());
+    return;
+  }
+  std::shared_ptr<State> s = state_;
+  std::thread([s, cb = std::move(cb)]() { cb(StateAwait(*s)); }).detach();
+}
+
+}  // namespace kvx

@@ -1,0 +1,515 @@
+#include "kv_cache_manager.h"
+
+#include <algorithm>
+#include <cstring>
+#include <limits>
+#include <string>
+
+#include "hip_util.h"
+
+namespace kvx {
+
+Status ValidateOffsetsAndSizes(const std::vector<int64_t>& src_offsets,
+                               const std::vector<int64_t>& dst_offsets,
+                               const std::vector<int64_t>& sizes) {
+  if (!dst_offsets.empty() && src_offsets.size() != dst_offsets.size()) {
+    return InvalidArgumentError(
+        "src_offsets, dst_offsets, and sizes must have the same length");
+  }
+  if (!sizes.empty() && src_offsets.size() != sizes.size()) {
+    return InvalidArgumentError(
+        "src_offsets, dst_offsets, and sizes must have the same length");
+  }
+  for (const std::vector<int64_t>* v : {&src_offsets, &dst_offsets, &sizes}) {
+    for (int64_t x : *v) {
+      if (x < 0) {
+        return InvalidArgumentError("copy offsets and sizes must be non-negative");
+      }
+    }
+  }
+  return OkStatus();
+}
+
+void CoalesceMajorDimCopies(const std::vector<int64_t>& src_offsets,
+                            const std::vector<int64_t>& dst_offsets,
+                            const std::vector<int64_t>& sizes,
+                            std::vector<int64_t>& out_src,
+                            std::vector<int64_t>& out_dst,
+                            std::vector<int64_t>& out_sizes) {
+  out_src.clear();
+  out_dst.clear();
+  out_sizes.clear();
+  for (size_t i = 0; i < src_offsets.size(); ++i) {
+    const bool extends = !out_src.empty() &&
+                         src_offsets[i] == out_src.back() + out_sizes.back() &&
+                         dst_offsets[i] == out_dst.back() + out_sizes.back();
+    if (extends) {
+      out_sizes.back() += sizes[i];
+    } else {
+      out_src.push_back(src_offsets[i]);
+      out_dst.push_back(dst_offsets[i]);
+      out_sizes.push_back(sizes[i]);
+    }
+  }
+}
+
+namespace {
+
+// a * b + c <= limit without overflow, for non-negative operands.
+bool RangeFits(int64_t a, int64_t b, int64_t c, int64_t limit) {
+  int64_t prod = 0;
+  int64_t sum = 0;
+  if (__builtin_mul_overflow(a, b, &prod)) return false;
+  if (__builtin_add_overflow(prod, c, &sum)) return false;
+  return sum <= limit;
+}
+
+}  // namespace
+
+StatusOr<std::unique_ptr<KVCacheManager>> KVCacheManager::Create(
+    ManagerConfig cfg) {
+  std::unique_ptr<KVCacheManager> m(new KVCacheManager(std::move(cfg)));
+  KVX_RETURN_IF_ERROR(m->Init());
+  return m;
+}
+
+Status KVCacheManager::Init() {
+  num_layers_ = cfg_.num_layers;
+  num_shards_ = cfg_.num_shards;
+  if (num_layers_ < 0 || num_shards_ < 0) {
+    return InvalidArgumentError("num_layers and num_shards must be non-negative");
+  }
+  if (cfg_.host_blocks < 0 || cfg_.host_blocks > std::numeric_limits<int>::max()) {
+    return InvalidArgumentError("host_blocks out of range");
+  }
+  host_blocks_ = cfg_.host_blocks;
+  const bool device_backed = !cfg_.device_ptrs.empty();
+  const size_t nstor = static_cast<size_t>(num_layers_ * num_shards_);
+  major_dim_ = cfg_.major_dim;
+  layer_block_bytes_.assign(num_layers_, 0);
+  layer_physical_bytes_.assign(num_layers_, 0);
+  storages_.assign(nstor, StorageInfo{});
+
+  if (device_backed) {
+    if (cfg_.device_ptrs.size() != nstor || cfg_.device_bytes.size() != nstor) {
+      return InvalidArgumentError(
+          "device_ptrs and device_bytes need num_layers * num_shards entries");
+    }
+    if (major_dim_ <= 0) return InvalidArgumentError("major_dim must be positive");
+    for (int64_t l = 0; l < num_layers_; ++l) {
+      // The layer's on-device size is the size of its first shard
+      // (kv_cache_manager_base.cc:287-296).
+      const int64_t phys = cfg_.device_bytes[l * num_shards_];
+      layer_physical_bytes_[l] = phys;
+      layer_block_bytes_[l] = phys / major_dim_;
+      for (int64_t s = 0; s < num_shards_; ++s) {
+        const size_t k = l * num_shards_ + s;
+        if (cfg_.device_bytes[k] < phys) {
+          return InvalidArgumentError(
+              "Device buffer shard size smaller than physical size");
+        }
+        if (cfg_.device_ptrs[k] == 0) {
+          return InvalidArgumentError("null device pointer");
+        }
+        storages_[k].dev = cfg_.device_ptrs[k];
+        storages_[k].dev_bytes = cfg_.device_bytes[k];
+      }
+    }
+    slice_byte_size_ = cfg_.slice_byte_size > 0
+                           ? cfg_.slice_byte_size
+                           : (num_layers_ > 0 ? layer_block_bytes_[0] : 0);
+  } else {
+    slice_byte_size_ = cfg_.slice_byte_size;
+    if (slice_byte_size_ < 0) return InvalidArgumentError("slice_byte_size < 0");
+    for (int64_t l = 0; l < num_layers_; ++l) layer_block_bytes_[l] = slice_byte_size_;
+  }
+
+  lbm_ = std::make_unique<LogicalBlockManager>(static_cast<int>(host_blocks_));
+
+  int64_t alloc_size = 0;
+  if (!RangeFits(host_blocks_, slice_byte_size_, 0,
+                 std::numeric_limits<int64_t>::max())) {
+    return InvalidArgumentError("host mirror size overflows");
+  }
+  alloc_size = host_blocks_ * slice_byte_size_;
+  for (size_t k = 0; k < nstor; ++k) {
+    StatusOr<HostBufferAllocation> a = Status();
+    switch (cfg_.host_alloc) {
+      case HostAllocKind::kMalloc:
+        a = AllocateMallocHost(static_cast<size_t>(alloc_size));
+        break;
+      case HostAllocKind::kPinned:
+        a = device_backed ? AllocatePinnedHost(static_cast<size_t>(alloc_size), cfg_.device)
+                          : AllocateMallocHost(static_cast<size_t>(alloc_size));
+        break;
+      default:
+        return UnimplementedError("host allocator kind not supported");
+    }
+    if (!a.ok()) return a.status();
+    if (alloc_size > 0 && a->ptr == nullptr) {
+      return InternalError("Host allocator returned null buffer for size: " +
+                           std::to_string(alloc_size));
+    }
+    storages_[k].host = a->ptr;
+    storages_[k].host_bytes = static_cast<int64_t>(a->size);
+    storages_[k].host_owner = a->owner;
+    allocated_host_bytes_ += a->size;
+  }
+
+  if (device_backed) {
+    EngineOptions eo = cfg_.engine;
+    eo.device = cfg_.device;
+    KVX_ASSIGN_OR_RETURN(engine_, TransferEngine::Create(eo));
+  }
+  return OkStatus();
+}
+
+KVCacheManager::~KVCacheManager() { (void)WaitForPendingWork(); }
+
+Status KVCacheManager::WaitForPendingWork() {
+  if (!engine_) return OkStatus();
+  // The engine's streams are private: waiting on them leaves unrelated
+  // framework work on the device alone.
+  return engine_->Synchronize();
+}
+
+StatusOr<std::vector<KVCacheManager::Work>> KVCacheManager::SelectWorks(
+    std::optional<size_t> layer_idx, std::optional<size_t> shard_idx) const {
+  if (layer_idx.has_value() && *layer_idx >= static_cast<size_t>(num_layers_)) {
+    return OutOfRangeError("layer or shard index out of range");
+  }
+  if (shard_idx.has_value() && *shard_idx >= static_cast<size_t>(num_shards_)) {
+    return OutOfRangeError("layer or shard index out of range");
+  }
+  std::vector<Work> works;
+  for (int64_t l = 0; l < num_layers_; ++l) {
+    if (layer_idx.has_value() && *layer_idx != static_cast<size_t>(l)) continue;
+    for (int64_t s = 0; s < num_shards_; ++s) {
+      if (shard_idx.has_value() && *shard_idx != static_cast<size_t>(s)) continue;
+      works.push_back(Work{static_cast<size_t>(l), static_cast<size_t>(s)});
+    }
+  }
+  return works;
+}
+
+StatusOr<CopyFuture> KVCacheManager::Transfer(
+    Direction dir, const std::vector<int64_t>& src,
+    const std::vector<int64_t>& dst, const std::vector<int64_t>& sizes_in,
+    std::optional<int64_t> slot_idx, std::optional<size_t> layer_idx,
+    std::optional<size_t> shard_idx, hipStream_t dep) {
+  const bool d2h = dir == Direction::kD2H;
+  if (!engine_) {
+    return FailedPreconditionError(
+        d2h ? "D2h requires a device-backed KVCacheManagerBase"
+            : "H2d requires a device-backed KVCacheManagerBase");
+  }
+  KVX_RETURN_IF_ERROR(ValidateOffsetsAndSizes(src, dst, sizes_in));
+  // The reference coalesces src against dst and sizes element-wise; a list
+  // with sources but without destinations has nothing to pair them with.
+  if (!src.empty() && dst.empty()) {
+    return InvalidArgumentError(
+        "src_offsets, dst_offsets, and sizes must have the same length");
+  }
+  std::vector<int64_t> sizes = sizes_in;
+  if (sizes.empty()) sizes.assign(src.size(), 1);
+  KVX_ASSIGN_OR_RETURN(std::vector<Work> works, SelectWorks(layer_idx, shard_idx));
+  std::vector<int64_t> src_c, dst_c, sizes_c;
+  CoalesceMajorDimCopies(src, dst, sizes, src_c, dst_c, sizes_c);
+  const bool is_partial = !src_c.empty();
+
+  std::vector<StorageView> views;
+  std::vector<int64_t> full_bytes;
+  views.reserve(works.size());
+  for (const Work& w : works) {
+    const StorageInfo& si = storage(w.layer, w.shard);
+    uint8_t* host = si.host;
+    int64_t host_size = si.host_bytes;
+    if (slot_idx.has_value()) {
+      KVX_ASSIGN_OR_RETURN(KVCacheHostSpan span,
+                           HostSpan(w.layer, w.shard, *slot_idx,
+                                    staging_max_major_per_slot_));
+      host = span.ptr;
+      host_size = static_cast<int64_t>(span.nbytes);
+    }
+    const int64_t B = layer_block_bytes(w.layer);
+    const int64_t phys = layer_physical_bytes_[w.layer];
+    if (!is_partial) {
+      if (host == nullptr) {
+        return FailedPreconditionError(d2h ? "Destination host pointer is null"
+                                           : "Source host pointer is null");
+      }
+      if (phys > host_size) {
+        return d2h ? OutOfRangeError("Copy range exceeds destination host buffer size")
+                   : InvalidArgumentError("Source host buffer is too small");
+      }
+      full_bytes.push_back(phys);
+    } else {
+      for (size_t j = 0; j < src_c.size(); ++j) {
+        const int64_t dev_off = d2h ? src_c[j] : dst_c[j];
+        const int64_t host_off = d2h ? dst_c[j] : src_c[j];
+        if (d2h) {
+          if (!RangeFits(dev_off + sizes_c[j], B, 0, si.dev_bytes)) {
+            return InvalidArgumentError("Copy range exceeds source device buffer size");
+          }
+          if (!RangeFits(host_off + sizes_c[j], B, 0, host_size)) {
+            return InvalidArgumentError("Copy range exceeds destination host buffer size");
+          }
+        } else {
+          if (!RangeFits(host_off + sizes_c[j], B, 0, host_size)) {
+            return InvalidArgumentError("Copy range exceeds source host buffer size");
+          }
+          if (!RangeFits(dev_off + sizes_c[j], B, 0, si.dev_bytes)) {
+            return InvalidArgumentError(
+                "Copy range exceeds destination device buffer size");
+          }
+        }
+      }
+    }
+    views.push_back(StorageView{si.dev, si.dev_bytes, host, host_size, B});
+  }
+  if (!is_partial) return engine_->CopyFull(dir, views, full_bytes, dep);
+  return engine_->Copy(dir, views, src_c, dst_c, sizes_c, dep);
+}
+
+StatusOr<CopyFuture> KVCacheManager::D2h(const std::vector<int64_t>& src,
+                                         const std::vector<int64_t>& dst,
+                                         const std::vector<int64_t>& sizes,
+                                         std::optional<int64_t> slot_idx,
+                                         std::optional<size_t> layer_idx,
+                                         std::optional<size_t> shard_idx,
+                                         hipStream_t dep) {
+  return Transfer(Direction::kD2H, src, dst, sizes, slot_idx, layer_idx,
+                  shard_idx, dep);
+}
+
+StatusOr<CopyFuture> KVCacheManager::H2d(const std::vector<int64_t>& src,
+                                         const std::vector<int64_t>& dst,
+                                         const std::vector<int64_t>& sizes,
+                                         std::optional<int64_t> slot_idx,
+                                         std::optional<size_t> layer_idx,
+                                         std::optional<size_t> shard_idx,
+                                         hipStream_t dep) {
+  return Transfer(Direction::kH2D, src, dst, sizes, slot_idx, layer_idx,
+                  shard_idx, dep);
+}
+
+StatusOr<std::pair<std::vector<int>, CopyFuture>>
+KVCacheManager::D2hAutoAllocate(const std::vector<int64_t>& src,
+                                const std::vector<int64_t>& sizes,
+                                hipStream_t dep) {
+  // kv_cache_manager_base.cc:1093-1140: allocate sum(sizes) locked host ids,
+  // then copy block src[j]+k to the k-th id allocated for chunk j.
+  if (src.size() != sizes.size()) {
+    return InvalidArgumentError("Lengths of offset and size lists must match");
+  }
+  int64_t total = 0;
+  for (int64_t s : sizes) total += s;
+  if (total > std::numeric_limits<int>::max() || total < 0) {
+    return InvalidArgumentError("Requested blocks out of range");
+  }
+  std::vector<int> ids;
+  {
+    std::lock_guard<std::mutex> l(lbm_mu_);
+    KVX_ASSIGN_OR_RETURN(ids, lbm_->Allocate(static_cast<int>(total), /*lock=*/true));
+  }
+  std::vector<int64_t> fsrc, fdst, fsz;
+  fsrc.reserve(total);
+  fdst.reserve(total);
+  fsz.reserve(total);
+  size_t next = 0;
+  for (size_t j = 0; j < src.size(); ++j) {
+    for (int64_t k = 0; k < sizes[j]; ++k) {
+      fsrc.push_back(src[j] + k);
+      fdst.push_back(ids[next++]);
+      fsz.push_back(1);
+    }
+  }
+  KVX_ASSIGN_OR_RETURN(CopyFuture f, D2h(fsrc, fdst, fsz, std::nullopt,
+                                         std::nullopt, std::nullopt, dep));
+  return std::make_pair(std::move(ids), std::move(f));
+}
+
+StatusOr<CopyFuture> KVCacheManager::DeviceCopy(
+    bool gather, const std::vector<int64_t>& ids, uint64_t staging,
+    int64_t staging_bytes, bool block_major, std::optional<size_t> layer_idx,
+    std::optional<size_t> shard_idx, hipStream_t stream) {
+  if (!engine_) {
+    return FailedPreconditionError(
+        "Gather/Scatter requires a device-backed KVCacheManagerBase");
+  }
+  KVX_ASSIGN_OR_RETURN(std::vector<Work> works, SelectWorks(layer_idx, shard_idx));
+  std::vector<StorageView> views;
+  int64_t need = 0;
+  for (const Work& w : works) {
+    const StorageInfo& si = storage(w.layer, w.shard);
+    const int64_t B = layer_block_bytes(w.layer);
+    for (int64_t id : ids) {
+      if (id < 0) return InvalidArgumentError("block ids must be non-negative");
+      if (!RangeFits(id + 1, B, 0, si.dev_bytes)) {
+        return OutOfRangeError("block id exceeds device buffer");
+      }
+    }
+    views.push_back(StorageView{si.dev, si.dev_bytes, nullptr, 0, B});
+    need += B * static_cast<int64_t>(ids.size());
+  }
+  if (!gather) {
+    // Two staging slots naming one device block would race in the scatter.
+    std::vector<int64_t> sorted = ids;
+    std::sort(sorted.begin(), sorted.end());
+    if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) {
+      return InvalidArgumentError("scatter block ids must be unique");
+    }
+  }
+  if (staging == 0 && need > 0) return InvalidArgumentError("null staging buffer");
+  if (staging_bytes < need) {
+    return InvalidArgumentError("staging buffer too small: need " +
+                                std::to_string(need) + " bytes");
+  }
+  return engine_->DeviceCopy(gather, views, ids, staging, block_major, stream);
+}
+
+StatusOr<CopyFuture> KVCacheManager::Gather(const std::vector<int64_t>& ids,
+                                            uint64_t staging,
+                                            int64_t staging_bytes,
+                                            bool block_major,
+                                            std::optional<size_t> layer_idx,
+                                            std::optional<size_t> shard_idx,
+                                            hipStream_t stream) {
+  return DeviceCopy(true, ids, staging, staging_bytes, block_major, layer_idx,
+                    shard_idx, stream);
+}
+
+StatusOr<CopyFuture> KVCacheManager::Scatter(const std::vector<int64_t>& ids,
+                                             uint64_t staging,
+                                             int64_t staging_bytes,
+                                             bool block_major,
+                                             std::optional<size_t> layer_idx,
+                                             std::optional<size_t> shard_idx,
+                                             hipStream_t stream) {
+  return DeviceCopy(false, ids, staging, staging_bytes, block_major, layer_idx,
+                    shard_idx, stream);
+}
+
+Status KVCacheManager::ConfigureHostStagingSlots(int64_t num_slots,
+                                                 int64_t max_major_per_slot) {
+  if (num_slots <= 0) return InvalidArgumentError("num_slots must be positive");
+  if (max_major_per_slot <= 0) {
+    return InvalidArgumentError("max_major_per_slot must be positive");
+  }
+  staging_num_slots_ = num_slots;
+  staging_max_major_per_slot_ = max_major_per_slot;
+  return OkStatus();
+}
+
+StatusOr<KVCacheHostSpan> KVCacheManager::HostSpan(size_t layer_idx,
+                                                   size_t shard_idx,
+                                                   int64_t slot_idx,
+                                                   int64_t num_major) {
+  // kv_cache_manager_base.cc:1434-1466.
+  if (staging_num_slots_ <= 0 || staging_max_major_per_slot_ <= 0) {
+    return FailedPreconditionError("Host staging slots have not been configured");
+  }
+  if (slot_idx < 0 || slot_idx >= staging_num_slots_) {
+    return OutOfRangeError("slot_idx out of range");
+  }
+  if (num_major < 0 || num_major > staging_max_major_per_slot_) {
+    return OutOfRangeError("num_major out of range");
+  }
+  if (layer_idx >= static_cast<size_t>(num_layers_) ||
+      shard_idx >= static_cast<size_t>(num_shards_)) {
+    return OutOfRangeError("HostSpan layer or shard index out of range");
+  }
+  const int64_t B = layer_block_bytes(layer_idx);
+  const int64_t base_major = slot_idx * staging_max_major_per_slot_;
+  const size_t byte_offset = static_cast<size_t>(base_major) * B;
+  const size_t nbytes = static_cast<size_t>(num_major) * B;
+  const StorageInfo& si = storage(layer_idx, shard_idx);
+  if (byte_offset + nbytes > static_cast<size_t>(si.host_bytes)) {
+    return OutOfRangeError("HostSpan exceeds host staging buffer");
+  }
+  KVCacheHostSpan span;
+  span.ptr = si.host + byte_offset;
+  span.nbytes = nbytes;
+  span.slot_idx = slot_idx;
+  span.base_major = base_major;
+  span.num_major = num_major;
+  span.layer_idx = layer_idx;
+  span.shard_idx = shard_idx;
+  return span;
+}
+
+uint8_t* KVCacheManager::GetHostPointer(size_t layer_idx, size_t shard_idx) {
+  // Shard ids wrap modulo the local shard count
+  // (tpu_sync/core/raiden_manager_base.cc:202-230).
+  if (layer_idx >= static_cast<size_t>(num_layers_) || num_shards_ == 0) {
+    return nullptr;
+  }
+  return storage(layer_idx, shard_idx % num_shards_).host;
+}
+
+size_t KVCacheManager::GetHostSize(size_t layer_idx, size_t shard_idx) {
+  if (layer_idx >= static_cast<size_t>(num_layers_) || num_shards_ == 0) return 0;
+  return static_cast<size_t>(storage(layer_idx, shard_idx % num_shards_).host_bytes);
+}
+
+int64_t KVCacheManager::LayerBlockByteSize(size_t layer_idx) const {
+  if (layer_idx >= static_cast<size_t>(num_layers_)) return -1;
+  return layer_block_bytes_[layer_idx];
+}
+
+size_t KVCacheManager::block_bytes(size_t block_array_idx) const {
+  const int64_t per_layer = LayerBlockByteSize(block_array_idx);
+  if (per_layer > 0) return static_cast<size_t>(per_layer);
+  return bytes_per_block();
+}
+
+uint8_t* KVCacheManager::GetBlockArrayHostPointer(size_t block_array_idx,
+                                                  size_t shard_idx) {
+  return GetHostPointer(block_array_idx, shard_idx);
+}
+
+size_t KVCacheManager::GetBlockArrayHostSize(size_t block_array_idx,
+                                             size_t shard_idx) {
+  return GetHostSize(block_array_idx, shard_idx);
+}
+
+StatusOr<uintptr_t> KVCacheManager::GetBlockHostPointerValue(size_t layer_idx,
+                                                             size_t shard_idx,
+                                                             int block_id) {
+  if (block_id < 0) return InvalidArgumentError("block_id must be non-negative");
+  const size_t bb = block_bytes(layer_idx);
+  const size_t host_size = GetHostSize(layer_idx, shard_idx);
+  uint8_t* base = GetHostPointer(layer_idx, shard_idx);
+  if (base == nullptr) return OutOfRangeError("layer or shard index out of range");
+  const size_t block = static_cast<size_t>(block_id);
+  if (bb == 0 || block > host_size / bb || block * bb + bb > host_size) {
+    return OutOfRangeError("block range exceeds host buffer");
+  }
+  return reinterpret_cast<uintptr_t>(base + block * bb);
+}
+
+StatusOr<std::string> KVCacheManager::ReadBlockBytes(size_t layer_idx,
+                                                     int block_id,
+                                                     size_t shard_idx) {
+  KVX_ASSIGN_OR_RETURN(uintptr_t p,
+                       GetBlockHostPointerValue(layer_idx, shard_idx, block_id));
+  return std::string(reinterpret_cast<const char*>(p), block_bytes(layer_idx));
+}
+
+Status KVCacheManager::WriteBlockBytes(size_t layer_idx, int block_id,
+                                       const void* payload, size_t payload_size,
+                                       size_t shard_idx) {
+  if (block_id < 0) return InvalidArgumentError("block_id must be non-negative");
+  const size_t bb = block_bytes(layer_idx);
+  if (payload_size != bb) {
+    return InvalidArgumentError("payload size must equal block size: got " +
+                                std::to_string(payload_size) + ", expected " +
+                                std::to_string(bb));
+  }
+  KVX_ASSIGN_OR_RETURN(uintptr_t p,
+                       GetBlockHostPointerValue(layer_idx, shard_idx, block_id));
+  std::memcpy(reinterpret_cast<void*>(p), payload, bb);
+  return OkStatus();
+}
+
+}  // namespace kvx

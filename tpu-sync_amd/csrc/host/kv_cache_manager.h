@@ -1,0 +1,210 @@
+// Paged KV manager for one MI355X: the counterpart of the reference's
+// KVCacheManagerBase (tpu_sync/kv_cache/kv_cache_manager_base.h:111-599).
+//
+// It wraps per-(layer, shard) device buffers of shape [major_dim][...]
+// (borrowed; the caller keeps them alive) and owns a host mirror with the
+// same per-(layer, shard) layout, [host_blocks][block bytes]. D2h/H2d move
+// whole blocks addressed by major-dimension offsets between the two and
+// return a CopyFuture; an empty spec copies the whole layer. Offsets are
+// validated and coalesced exactly as the reference does
+// (kv_cache_manager_base.cc:72-141) and every range is checked before any
+// copy is issued. Device data moves through TransferEngine (gather/scatter
+// kernels + pipelined hipMemcpyAsync) instead of one DMA per run.
+#ifndef KVX_HOST_KV_CACHE_MANAGER_H_
+#define KVX_HOST_KV_CACHE_MANAGER_H_
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <optional>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "copy_future.h"
+#include "host_allocator.h"
+#include "logical_block_manager.h"
+#include "status.h"
+#include "transfer_engine.h"
+
+namespace kvx {
+
+struct ManagerConfig {
+  int device = 0;
+  int64_t num_layers = 0;
+  int64_t num_shards = 1;
+  // Device base address of each (layer, shard) buffer, index
+  // layer * num_shards + shard. Empty: a CPU-only manager (host mirror only),
+  // like the reference's CPU-only constructor (kv_cache_manager_base.cc:374-450).
+  std::vector<uint64_t> device_ptrs;
+  std::vector<int64_t> device_bytes;  // bytes of each device buffer
+  int64_t major_dim = 0;              // blocks along the major dimension
+  // Bytes per block; required for a CPU-only manager, otherwise derived from
+  // layer 0 (device bytes / major_dim) when 0.
+  int64_t slice_byte_size = 0;
+  int64_t host_blocks = 64;
+  HostAllocKind host_alloc = HostAllocKind::kPinned;
+  // Used when host_alloc == kShm.
+  std::string shm_key;
+  std::string shm_server_name;
+  std::string model_uid;
+  EngineOptions engine;
+};
+
+// A contiguous host range of one (layer, shard) staging slot
+// (kv_cache_manager_base.h KVCacheHostSpan).
+struct KVCacheHostSpan {
+  uint8_t* ptr = nullptr;
+  size_t nbytes = 0;
+  int64_t slot_idx = -1;
+  int64_t base_major = 0;
+  int64_t num_major = 0;
+  size_t layer_idx = 0;
+  size_t shard_idx = 0;
+};
+
+class KVCacheManager {
+ public:
+  static StatusOr<std::unique_ptr<KVCacheManager>> Create(ManagerConfig cfg);
+  ~KVCacheManager();
+
+  StatusOr<CopyFuture> D2h(const std::vector<int64_t>& src_offsets_major_dim,
+                           const std::vector<int64_t>& dst_offsets_major_dim,
+                           const std::vector<int64_t>& copy_sizes_major_dim,
+                           std::optional<int64_t> slot_idx = std::nullopt,
+                           std::optional<size_t> layer_idx = std::nullopt,
+                           std::optional<size_t> shard_idx = std::nullopt,
+                           hipStream_t dep = nullptr);
+  StatusOr<CopyFuture> H2d(const std::vector<int64_t>& src_offsets_major_dim,
+                           const std::vector<int64_t>& dst_offsets_major_dim,
+                           const std::vector<int64_t>& copy_sizes_major_dim,
+                           std::optional<int64_t> slot_idx = std::nullopt,
+                           std::optional<size_t> layer_idx = std::nullopt,
+                           std::optional<size_t> shard_idx = std::nullopt,
+                           hipStream_t dep = nullptr);
+  StatusOr<std::pair<std::vector<int>, CopyFuture>> D2hAutoAllocate(
+      const std::vector<int64_t>& src_offsets_major_dim,
+      const std::vector<int64_t>& copy_sizes_major_dim,
+      hipStream_t dep = nullptr);
+
+  // Device-side extract/insert: gathers blocks `ids` of the selected
+  // storages into a device staging buffer (or scatters them back). Staging
+  // is layer-major [storage][n][block] or block-major [n][storage][block];
+  // storages are (layer, shard) in layer-major order, optionally restricted
+  // to one layer and/or one shard.
+  StatusOr<CopyFuture> Gather(const std::vector<int64_t>& ids, uint64_t staging,
+                              int64_t staging_bytes, bool block_major,
+                              std::optional<size_t> layer_idx,
+                              std::optional<size_t> shard_idx,
+                              hipStream_t stream);
+  StatusOr<CopyFuture> Scatter(const std::vector<int64_t>& ids,
+                               uint64_t staging, int64_t staging_bytes,
+                               bool block_major,
+                               std::optional<size_t> layer_idx,
+                               std::optional<size_t> shard_idx,
+                               hipStream_t stream);
+
+  Status ConfigureHostStagingSlots(int64_t num_slots,
+                                   int64_t max_major_per_slot);
+  StatusOr<KVCacheHostSpan> HostSpan(size_t layer_idx, size_t shard_idx,
+                                     int64_t slot_idx, int64_t num_major);
+
+  // Host block accessors (kv_cache_manager_base.cc:1468-1552,
+  // tpu_sync/frameworks/torch/kv_cache_manager.cc:224-267).
+  StatusOr<uintptr_t> GetBlockHostPointerValue(size_t layer_idx,
+                                               size_t shard_idx, int block_id);
+  StatusOr<std::string> ReadBlockBytes(size_t layer_idx, int block_id,
+                                       size_t shard_idx);
+  Status WriteBlockBytes(size_t layer_idx, int block_id, const void* payload,
+                         size_t payload_size, size_t shard_idx);
+  uint8_t* GetHostPointer(size_t layer_idx, size_t shard_idx);
+  size_t GetHostSize(size_t layer_idx, size_t shard_idx);
+
+  LogicalBlockManager* host_block_manager() const { return lbm_.get(); }
+  std::mutex& host_block_mutex() { return lbm_mu_; }
+  size_t bytes_per_block() const { return static_cast<size_t>(slice_byte_size_); }
+  size_t num_block_arrays() const { return static_cast<size_t>(num_layers_); }
+  size_t block_bytes(size_t block_array_idx) const;
+  uint8_t* GetBlockArrayHostPointer(size_t block_array_idx, size_t shard_idx);
+  size_t GetBlockArrayHostSize(size_t block_array_idx, size_t shard_idx);
+  int64_t LayerBlockByteSize(size_t layer_idx) const;
+  size_t GetAllocatedHostDramBytes() const { return allocated_host_bytes_; }
+
+  size_t num_layers() const { return static_cast<size_t>(num_layers_); }
+  size_t num_shards() const { return static_cast<size_t>(num_shards_); }
+  int64_t major_dim() const { return major_dim_; }
+  int64_t host_blocks() const { return host_blocks_; }
+  bool device_backed() const { return engine_ != nullptr; }
+  int device() const { return cfg_.device; }
+  TransferEngine* engine() { return engine_.get(); }
+  Status WaitForPendingWork();
+
+ private:
+  struct StorageInfo {
+    uint64_t dev = 0;
+    int64_t dev_bytes = 0;
+    uint8_t* host = nullptr;
+    int64_t host_bytes = 0;
+    std::shared_ptr<void> host_owner;
+  };
+  explicit KVCacheManager(ManagerConfig cfg) : cfg_(std::move(cfg)) {}
+  Status Init();
+  int64_t layer_block_bytes(size_t layer) const { return layer_block_bytes_[layer]; }
+  StorageInfo& storage(size_t layer, size_t shard) {
+    return storages_[layer * num_shards_ + shard];
+  }
+  struct Work {
+    size_t layer;
+    size_t shard;
+  };
+  StatusOr<std::vector<Work>> SelectWorks(std::optional<size_t> layer_idx,
+                                          std::optional<size_t> shard_idx) const;
+  StatusOr<CopyFuture> Transfer(Direction dir,
+                                const std::vector<int64_t>& src,
+                                const std::vector<int64_t>& dst,
+                                const std::vector<int64_t>& sizes,
+                                std::optional<int64_t> slot_idx,
+                                std::optional<size_t> layer_idx,
+                                std::optional<size_t> shard_idx,
+                                hipStream_t dep);
+  StatusOr<CopyFuture> DeviceCopy(bool gather, const std::vector<int64_t>& ids,
+                                  uint64_t staging, int64_t staging_bytes,
+                                  bool block_major,
+                                  std::optional<size_t> layer_idx,
+                                  std::optional<size_t> shard_idx,
+                                  hipStream_t stream);
+
+  ManagerConfig cfg_;
+  int64_t num_layers_ = 0;
+  int64_t num_shards_ = 0;
+  int64_t major_dim_ = 0;
+  int64_t slice_byte_size_ = 0;
+  int64_t host_blocks_ = 0;
+  std::vector<int64_t> layer_block_bytes_;
+  std::vector<int64_t> layer_physical_bytes_;
+  std::vector<StorageInfo> storages_;
+  size_t allocated_host_bytes_ = 0;
+  int64_t staging_num_slots_ = 0;
+  int64_t staging_max_major_per_slot_ = 0;
+  std::unique_ptr<LogicalBlockManager> lbm_;
+  std::mutex lbm_mu_;
+  std::unique_ptr<TransferEngine> engine_;
+};
+
+// The reference's offset validation (kv_cache_manager_base.cc:72-102) and
+// run coalescing (kv_cache_manager_base.cc:121-141), exposed for tests.
+Status ValidateOffsetsAndSizes(const std::vector<int64_t>& src_offsets,
+                               const std::vector<int64_t>& dst_offsets,
+                               const std::vector<int64_t>& sizes);
+void CoalesceMajorDimCopies(const std::vector<int64_t>& src_offsets,
+                            const std::vector<int64_t>& dst_offsets,
+                            const std::vector<int64_t>& sizes,
+                            std::vector<int64_t>& out_src,
+                            std::vector<int64_t>& out_dst,
+                            std::vector<int64_t>& out_sizes);
+
+}  // namespace kvx
+
+#endif  // KVX_HOST_KV_CACHE_MANAGER_H_

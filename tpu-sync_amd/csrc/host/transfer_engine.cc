@@ -1,0 +1,608 @@
+#include "transfer_engine.h"
+
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+
+#include "../kernels/block_copy.h"
+#include "hip_util.h"
+
+namespace kvx {
+namespace {
+
+constexpr int64_t kArgAlign = 256;
+
+int64_t AlignUp(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// A run of compact indices whose host ids are consecutive.
+struct HostRun {
+  int64_t i0;
+  int64_t len;
+  int64_t host0;
+};
+
+// One piece of a staging chunk: flat blocks [f0, f0 + nb) of one group,
+// placed at byte offset buf_off of the chunk buffer.
+struct PiecePlan {
+  int group;
+  int64_t f0;
+  int64_t nb;
+  int64_t buf_off;
+};
+
+}  // namespace
+
+StatusOr<std::unique_ptr<TransferEngine>> TransferEngine::Create(
+    const EngineOptions& opts) {
+  if (opts.staging_chunk_bytes <= 0 || opts.staging_chunks <= 0 ||
+      opts.arg_ring_bytes <= 0) {
+    return InvalidArgumentError("engine sizes must be positive");
+  }
+  std::unique_ptr<TransferEngine> e(new TransferEngine(opts));
+  KVX_RETURN_IF_ERROR(e->Init());
+  return e;
+}
+
+Status TransferEngine::Init() {
+  DeviceGuard g(opts_.device);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  KVX_HIP_RETURN_IF_ERROR(
+      hipStreamCreateWithFlags(&gather_stream_, hipStreamNonBlocking));
+  KVX_HIP_RETURN_IF_ERROR(
+      hipStreamCreateWithFlags(&d2h_stream_, hipStreamNonBlocking));
+  KVX_HIP_RETURN_IF_ERROR(
+      hipStreamCreateWithFlags(&h2d_stream_, hipStreamNonBlocking));
+  KVX_HIP_RETURN_IF_ERROR(
+      hipStreamCreateWithFlags(&scatter_stream_, hipStreamNonBlocking));
+  for (Ring* r : {&out_ring_, &in_ring_}) {
+    for (int k = 0; k < opts_.staging_chunks; ++k) {
+      void* p = nullptr;
+      KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, opts_.staging_chunk_bytes));
+      r->bufs.push_back(reinterpret_cast<uint64_t>(p));
+      KVX_ASSIGN_OR_RETURN(hipEvent_t ready, NewEvent());
+      KVX_ASSIGN_OR_RETURN(hipEvent_t free_ev, NewEvent());
+      r->ready.push_back(ready);
+      r->free.push_back(free_ev);
+      r->used.push_back(false);
+    }
+  }
+  return GrowArgRing(opts_.arg_ring_bytes);
+}
+
+TransferEngine::~TransferEngine() {
+  DeviceGuard g(opts_.device);
+  for (hipStream_t s :
+       {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
+    if (s != nullptr) (void)hipStreamSynchronize(s);
+  }
+  for (ArgSlice& s : arg_inflight_) (void)hipEventDestroy(s.done);
+  arg_inflight_.clear();
+  for (KernelSample& s : samples_) {
+    (void)hipEventDestroy(s.start);
+    (void)hipEventDestroy(s.stop);
+  }
+  samples_.clear();
+  for (Ring* r : {&out_ring_, &in_ring_}) {
+    for (uint64_t b : r->bufs) (void)hipFree(reinterpret_cast<void*>(b));
+    for (hipEvent_t e : r->ready) (void)hipEventDestroy(e);
+    for (hipEvent_t e : r->free) (void)hipEventDestroy(e);
+  }
+  if (arg_host_ != nullptr) (void)hipHostFree(arg_host_);
+  if (arg_dev_ != 0) (void)hipFree(reinterpret_cast<void*>(arg_dev_));
+  for (hipStream_t s :
+       {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
+    if (s != nullptr) (void)hipStreamDestroy(s);
+  }
+}
+
+EngineStats TransferEngine::stats() const {
+  std::lock_guard<std::mutex> l(const_cast<std::mutex&>(mu_));
+  return stats_;
+}
+
+Status TransferEngine::Synchronize() {
+  DeviceGuard g(opts_.device);
+  for (hipStream_t s :
+       {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
+    KVX_HIP_RETURN_IF_ERROR(hipStreamSynchronize(s));
+  }
+  return OkStatus();
+}
+
+Status TransferEngine::LaunchCopy(const CopyLaunch& l, bool gather, int vec,
+                                  hipStream_t stream) {
+  KernelSample s;
+  if (opts_.profile_kernels) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.start));
+    KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.stop));
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.start, stream));
+  }
+  KVX_HIP_RETURN_IF_ERROR(LaunchBlockCopy(
+      l, gather ? CopyDir::kGather : CopyDir::kScatter, vec, stream));
+  ++stats_.kernel_launches;
+  if (opts_.profile_kernels) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.stop, stream));
+    for (int k = 0; k < l.npieces; ++k) {
+      s.bytes += 2 * l.pieces[k].nblocks * l.pieces[k].block_bytes;
+    }
+    s.gather = gather;
+    samples_.push_back(s);
+  }
+  return OkStatus();
+}
+
+StatusOr<KernelTimes> TransferEngine::ProfiledKernelTimes(bool gather,
+                                                          bool reset) {
+  std::lock_guard<std::mutex> l(mu_);
+  KernelTimes t;
+  for (const KernelSample& s : samples_) {
+    if (s.gather != gather) continue;
+    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(s.stop));
+    float ms = 0;
+    KVX_HIP_RETURN_IF_ERROR(hipEventElapsedTime(&ms, s.start, s.stop));
+    ++t.launches;
+    t.total_ms += ms;
+    t.bytes += s.bytes;
+  }
+  if (reset) {
+    std::vector<KernelSample> keep;
+    for (KernelSample& s : samples_) {
+      if (s.gather == gather) {
+        (void)hipEventDestroy(s.start);
+        (void)hipEventDestroy(s.stop);
+      } else {
+        keep.push_back(s);
+      }
+    }
+    samples_.swap(keep);
+  }
+  return t;
+}
+
+StatusOr<hipEvent_t> TransferEngine::NewEvent() {
+  hipEvent_t e = nullptr;
+  KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  return e;
+}
+
+Status TransferEngine::GrowArgRing(int64_t bytes) {
+  for (ArgSlice& s : arg_inflight_) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(s.done));
+    (void)hipEventDestroy(s.done);
+  }
+  arg_inflight_.clear();
+  if (arg_host_ != nullptr) (void)hipHostFree(arg_host_);
+  if (arg_dev_ != 0) (void)hipFree(reinterpret_cast<void*>(arg_dev_));
+  arg_host_ = nullptr;
+  arg_dev_ = 0;
+  const int64_t size = AlignUp(std::max(bytes, arg_bytes_ * 2), kArgAlign);
+  void* h = nullptr;
+  void* d = nullptr;
+  KVX_HIP_RETURN_IF_ERROR(hipHostMalloc(&h, size, hipHostMallocDefault));
+  KVX_HIP_RETURN_IF_ERROR(hipMalloc(&d, size));
+  arg_host_ = static_cast<uint8_t*>(h);
+  arg_dev_ = reinterpret_cast<uint64_t>(d);
+  arg_bytes_ = size;
+  arg_head_ = 0;
+  return OkStatus();
+}
+
+StatusOr<int64_t> TransferEngine::ArgAlloc(int64_t bytes) {
+  bytes = AlignUp(std::max<int64_t>(bytes, 1), kArgAlign);
+  if (bytes > arg_bytes_) KVX_RETURN_IF_ERROR(GrowArgRing(bytes));
+  int64_t start = arg_head_;
+  if (start + bytes > arg_bytes_) start = 0;
+  const int64_t end = start + bytes;
+  // Retire finished slices; wait for any unfinished one that overlaps.
+  for (auto it = arg_inflight_.begin(); it != arg_inflight_.end();) {
+    const bool overlap = it->begin < end && start < it->end;
+    hipError_t q = hipEventQuery(it->done);
+    if (q == hipErrorNotReady && overlap) {
+      KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(it->done));
+      q = hipSuccess;
+    }
+    if (q == hipErrorNotReady) {
+      ++it;
+      continue;
+    }
+    (void)hipEventDestroy(it->done);
+    it = arg_inflight_.erase(it);
+  }
+  arg_head_ = end;
+  return start;
+}
+
+Status TransferEngine::ArgCommit(int64_t begin, int64_t end,
+                                 hipStream_t stream) {
+  KVX_ASSIGN_OR_RETURN(hipEvent_t ev, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ev, stream));
+  arg_inflight_.push_back(ArgSlice{begin, end, ev});
+  return OkStatus();
+}
+
+std::vector<TransferEngine::Group> TransferEngine::MakeGroups(
+    const std::vector<StorageView>& s) {
+  std::vector<Group> groups;
+  for (size_t w = 0; w < s.size(); ++w) {
+    const int64_t pool = s[w].block_bytes > 0 ? s[w].dev_bytes / s[w].block_bytes : 0;
+    Group* g = nullptr;
+    for (Group& c : groups) {
+      if (c.block_bytes == s[w].block_bytes) g = &c;
+    }
+    if (g == nullptr) {
+      groups.push_back(Group{});
+      g = &groups.back();
+      g->block_bytes = s[w].block_bytes;
+      g->pool_blocks = pool;
+    }
+    g->pool_blocks = std::min(g->pool_blocks, pool);
+    g->members.push_back(static_cast<int>(w));
+  }
+  return groups;
+}
+
+Status TransferEngine::WaitDep(hipStream_t dep, hipStream_t on) {
+  if (dep == nullptr) return OkStatus();
+  KVX_ASSIGN_OR_RETURN(hipEvent_t ev, NewEvent());
+  Status st = HipStatus(hipEventRecord(ev, dep), "hipEventRecord(dep)");
+  if (st.ok()) st = HipStatus(hipStreamWaitEvent(on, ev, 0), "hipStreamWaitEvent");
+  (void)hipEventDestroy(ev);
+  return st;
+}
+
+StatusOr<CopyFuture> TransferEngine::Copy(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& src, const std::vector<int64_t>& dst,
+    const std::vector<int64_t>& sizes, hipStream_t dep) {
+  if (src.size() != dst.size() || src.size() != sizes.size()) {
+    return InvalidArgumentError("src, dst and sizes must have the same length");
+  }
+  int64_t total = 0;
+  int64_t min_run = INT64_MAX;
+  for (int64_t s : sizes) {
+    total += s;
+    if (s > 0) min_run = std::min(min_run, s);
+  }
+  if (total == 0 || storages.empty()) return CopyFuture();
+  int64_t min_block = INT64_MAX;
+  for (const StorageView& s : storages) min_block = std::min(min_block, s.block_bytes);
+  if (min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) {
+    return CopyDirect(dir, storages, src, dst, sizes, dep);
+  }
+  return CopyStaged(dir, storages, src, dst, sizes, dep);
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyDirect(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& src, const std::vector<int64_t>& dst,
+    const std::vector<int64_t>& sizes, hipStream_t dep) {
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(opts_.device);
+  hipStream_t cs = dir == Direction::kD2H ? d2h_stream_ : h2d_stream_;
+  KVX_RETURN_IF_ERROR(WaitDep(dep, cs));
+  for (const StorageView& s : storages) {
+    const int64_t B = s.block_bytes;
+    for (size_t r = 0; r < sizes.size(); ++r) {
+      if (sizes[r] == 0) continue;
+      const size_t bytes = static_cast<size_t>(sizes[r] * B);
+      if (dir == Direction::kD2H) {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(
+            s.host + dst[r] * B, reinterpret_cast<void*>(s.dev + src[r] * B),
+            bytes, hipMemcpyDeviceToHost, cs));
+      } else {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(
+            reinterpret_cast<void*>(s.dev + dst[r] * B), s.host + src[r] * B,
+            bytes, hipMemcpyHostToDevice, cs));
+      }
+      ++stats_.memcpy_calls;
+    }
+  }
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, cs));
+  ++stats_.direct_copies;
+  return CopyFuture::FromEvents({done}, {});
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyFull(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& bytes, hipStream_t dep) {
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(opts_.device);
+  hipStream_t cs = dir == Direction::kD2H ? d2h_stream_ : h2d_stream_;
+  KVX_RETURN_IF_ERROR(WaitDep(dep, cs));
+  for (size_t w = 0; w < storages.size(); ++w) {
+    const StorageView& s = storages[w];
+    if (bytes[w] == 0) continue;
+    if (dir == Direction::kD2H) {
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(s.host,
+                                             reinterpret_cast<void*>(s.dev),
+                                             bytes[w], hipMemcpyDeviceToHost, cs));
+    } else {
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(s.dev),
+                                             s.host, bytes[w],
+                                             hipMemcpyHostToDevice, cs));
+    }
+    ++stats_.memcpy_calls;
+  }
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, cs));
+  ++stats_.direct_copies;
+  return CopyFuture::FromEvents({done}, {});
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyStaged(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& src, const std::vector<int64_t>& dst,
+    const std::vector<int64_t>& sizes, hipStream_t dep) {
+  const bool d2h = dir == Direction::kD2H;
+  // 1. Expand runs into (device id, host id) pairs.
+  int64_t N = 0;
+  for (int64_t s : sizes) N += s;
+  std::vector<int64_t> dev_id(N), host_id(N);
+  {
+    int64_t k = 0;
+    for (size_t r = 0; r < sizes.size(); ++r) {
+      for (int64_t j = 0; j < sizes[r]; ++j, ++k) {
+        dev_id[k] = d2h ? src[r] + j : dst[r] + j;
+        host_id[k] = d2h ? dst[r] + j : src[r] + j;
+      }
+    }
+  }
+  // 2. One writer per destination block: the last pair naming it wins, as
+  // when the copies are issued in order.
+  const std::vector<int64_t>& dest = d2h ? host_id : dev_id;
+  std::vector<int64_t> order(N);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t a, int64_t b) { return dest[a] < dest[b]; });
+  std::vector<int64_t> kept;
+  kept.reserve(N);
+  for (int64_t k = 0; k < N; ++k) {
+    if (k + 1 < N && dest[order[k + 1]] == dest[order[k]]) continue;
+    kept.push_back(order[k]);
+  }
+  // 3. Compact order: by host id, so every host run is contiguous in staging.
+  if (!d2h) {
+    std::stable_sort(kept.begin(), kept.end(), [&](int64_t a, int64_t b) {
+      return host_id[a] < host_id[b];
+    });
+  }
+  const int64_t n = static_cast<int64_t>(kept.size());
+  std::vector<int64_t> cdev(n), chost(n);
+  for (int64_t i = 0; i < n; ++i) {
+    cdev[i] = dev_id[kept[i]];
+    chost[i] = host_id[kept[i]];
+  }
+  std::vector<HostRun> runs;
+  for (int64_t i = 0; i < n;) {
+    int64_t e = i + 1;
+    while (e < n && chost[e] == chost[e - 1] + 1) ++e;
+    runs.push_back(HostRun{i, e - i, chost[i]});
+    i = e;
+  }
+  if (n > INT32_MAX) return InvalidArgumentError("too many blocks in one copy");
+
+  std::vector<Group> groups = MakeGroups(storages);
+  for (const Group& gr : groups) {
+    if (gr.block_bytes > opts_.staging_chunk_bytes) {
+      return InvalidArgumentError("block larger than a staging chunk");
+    }
+    if (static_cast<int64_t>(gr.members.size()) * n > UINT32_MAX) {
+      return InvalidArgumentError("copy too large for one plan");
+    }
+  }
+
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard dg(opts_.device);
+  hipStream_t ks = d2h ? gather_stream_ : scatter_stream_;
+  hipStream_t cs = d2h ? d2h_stream_ : h2d_stream_;
+  Ring& ring = d2h ? out_ring_ : in_ring_;
+
+  // 4. Arguments: compact device ids, then one base-address table per group.
+  int64_t arg_bytes = AlignUp(n * 8, kArgAlign);
+  std::vector<int64_t> table_off(groups.size());
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    table_off[gi] = arg_bytes;
+    arg_bytes += AlignUp(static_cast<int64_t>(groups[gi].members.size()) * 8, kArgAlign);
+  }
+  KVX_ASSIGN_OR_RETURN(int64_t aoff, ArgAlloc(arg_bytes));
+  std::memcpy(arg_host_ + aoff, cdev.data(), n * 8);
+  uint64_t align_acc = 0;
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    uint64_t* t = reinterpret_cast<uint64_t*>(arg_host_ + aoff + table_off[gi]);
+    for (size_t m = 0; m < groups[gi].members.size(); ++m) {
+      t[m] = storages[groups[gi].members[m]].dev;
+      align_acc |= t[m];
+    }
+    groups[gi].table_dev = arg_dev_ + aoff + table_off[gi];
+  }
+  KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(arg_dev_ + aoff),
+                                         arg_host_ + aoff, arg_bytes,
+                                         hipMemcpyHostToDevice, ks));
+  KVX_RETURN_IF_ERROR(WaitDep(dep, ks));
+  const int64_t* ids_dev = reinterpret_cast<const int64_t*>(arg_dev_ + aoff);
+
+  // 5. Chunk plan over the layer-major staging layout of all groups.
+  const int64_t cap = opts_.staging_chunk_bytes;
+  std::vector<std::vector<PiecePlan>> chunks;
+  {
+    std::vector<PiecePlan> cur;
+    int64_t used = 0;
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+      const int64_t B = groups[gi].block_bytes;
+      const int64_t F = static_cast<int64_t>(groups[gi].members.size()) * n;
+      int64_t f = 0;
+      while (f < F) {
+        int64_t fit = (cap - used) / B;
+        if (fit == 0) {
+          chunks.push_back(std::move(cur));
+          cur.clear();
+          used = 0;
+          continue;
+        }
+        const int64_t take = std::min(fit, F - f);
+        cur.push_back(PiecePlan{static_cast<int>(gi), f, take, used});
+        used += take * B;
+        f += take;
+      }
+    }
+    if (!cur.empty()) chunks.push_back(std::move(cur));
+  }
+
+  auto issue_memcpys = [&](const PiecePlan& p, uint64_t buf) -> Status {
+    const Group& gr = groups[p.group];
+    const int64_t B = gr.block_bytes;
+    const int64_t wlo = p.f0 / n;
+    const int64_t whi = (p.f0 + p.nb - 1) / n;
+    for (int64_t w = wlo; w <= whi; ++w) {
+      const StorageView& s = storages[gr.members[w]];
+      const int64_t ilo = std::max<int64_t>(p.f0 - w * n, 0);
+      const int64_t ihi = std::min<int64_t>(p.f0 + p.nb - w * n, n);
+      // First run that ends after ilo.
+      auto it = std::upper_bound(runs.begin(), runs.end(), ilo,
+                                 [](int64_t v, const HostRun& r) { return v < r.i0; });
+      if (it != runs.begin()) --it;
+      for (; it != runs.end() && it->i0 < ihi; ++it) {
+        const int64_t a = std::max(it->i0, ilo);
+        const int64_t b = std::min(it->i0 + it->len, ihi);
+        if (a >= b) continue;
+        uint8_t* host = s.host + (it->host0 + (a - it->i0)) * B;
+        void* stg = reinterpret_cast<void*>(buf + p.buf_off + (w * n + a - p.f0) * B);
+        const size_t bytes = static_cast<size_t>((b - a) * B);
+        if (d2h) {
+          KVX_HIP_RETURN_IF_ERROR(
+              hipMemcpyAsync(host, stg, bytes, hipMemcpyDeviceToHost, cs));
+        } else {
+          KVX_HIP_RETURN_IF_ERROR(
+              hipMemcpyAsync(stg, host, bytes, hipMemcpyHostToDevice, cs));
+        }
+        ++stats_.memcpy_calls;
+      }
+    }
+    return OkStatus();
+  };
+
+  auto launch = [&](const std::vector<PiecePlan>& ps, uint64_t buf) -> Status {
+    for (size_t p0 = 0; p0 < ps.size(); p0 += kMaxPieces) {
+      CopyLaunch cl;
+      cl.ids = ids_dev;
+      cl.n = n;
+      uint64_t acc = align_acc | buf;
+      for (size_t k = p0; k < ps.size() && k < p0 + kMaxPieces; ++k) {
+        const PiecePlan& p = ps[k];
+        const Group& gr = groups[p.group];
+        CopyPiece& c = cl.pieces[cl.npieces++];
+        c.storages = gr.table_dev;
+        c.staging = buf + static_cast<uint64_t>(p.buf_off) -
+                    static_cast<uint64_t>(p.f0) * static_cast<uint64_t>(gr.block_bytes);
+        c.stride_w = n * gr.block_bytes;
+        c.stride_i = gr.block_bytes;
+        c.f0 = p.f0;
+        c.nblocks = p.nb;
+        c.block_bytes = gr.block_bytes;
+        c.pool_blocks = gr.pool_blocks;
+        acc |= static_cast<uint64_t>(p.buf_off);
+      }
+      const int vec = LaunchVectorBytes(cl, acc);
+      KVX_RETURN_IF_ERROR(LaunchCopy(cl, d2h, vec, ks));
+    }
+    return OkStatus();
+  };
+
+  // 6. Pipeline the chunks through the staging ring.
+  for (const std::vector<PiecePlan>& ch : chunks) {
+    const size_t k = ring.next;
+    ring.next = (ring.next + 1) % ring.bufs.size();
+    const uint64_t buf = ring.bufs[k];
+    if (d2h) {
+      if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.free[k], 0));
+      KVX_RETURN_IF_ERROR(launch(ch, buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], ks));
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.ready[k], 0));
+      for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], cs));
+    } else {
+      if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.free[k], 0));
+      for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], cs));
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.ready[k], 0));
+      KVX_RETURN_IF_ERROR(launch(ch, buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], ks));
+    }
+    ring.used[k] = true;
+    ++stats_.chunks;
+  }
+  KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, ks));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, d2h ? cs : ks));
+  ++stats_.staged_copies;
+  return CopyFuture::FromEvents({done}, {});
+}
+
+StatusOr<CopyFuture> TransferEngine::DeviceCopy(
+    bool gather, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& ids, uint64_t staging, bool block_major,
+    hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(ids.size());
+  if (n == 0 || storages.empty()) return CopyFuture();
+  std::vector<Group> groups = MakeGroups(storages);
+  if (block_major && groups.size() != 1) {
+    return InvalidArgumentError("block-major staging needs one block size");
+  }
+  for (const Group& gr : groups) {
+    if (static_cast<int64_t>(gr.members.size()) * n > UINT32_MAX) {
+      return InvalidArgumentError("copy too large for one launch");
+    }
+  }
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard dg(opts_.device);
+  int64_t arg_bytes = AlignUp(n * 8, kArgAlign);
+  std::vector<int64_t> table_off(groups.size());
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    table_off[gi] = arg_bytes;
+    arg_bytes += AlignUp(static_cast<int64_t>(groups[gi].members.size()) * 8, kArgAlign);
+  }
+  KVX_ASSIGN_OR_RETURN(int64_t aoff, ArgAlloc(arg_bytes));
+  std::memcpy(arg_host_ + aoff, ids.data(), n * 8);
+  uint64_t acc = staging;
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    uint64_t* t = reinterpret_cast<uint64_t*>(arg_host_ + aoff + table_off[gi]);
+    for (size_t m = 0; m < groups[gi].members.size(); ++m) {
+      t[m] = storages[groups[gi].members[m]].dev;
+      acc |= t[m];
+    }
+    groups[gi].table_dev = arg_dev_ + aoff + table_off[gi];
+  }
+  KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(arg_dev_ + aoff),
+                                         arg_host_ + aoff, arg_bytes,
+                                         hipMemcpyHostToDevice, stream));
+  int64_t off = 0;
+  for (size_t g0 = 0; g0 < groups.size(); g0 += kMaxPieces) {
+    CopyLaunch cl;
+    cl.ids = reinterpret_cast<const int64_t*>(arg_dev_ + aoff);
+    cl.n = n;
+    for (size_t gi = g0; gi < groups.size() && gi < g0 + kMaxPieces; ++gi) {
+      const Group& gr = groups[gi];
+      const int64_t W = static_cast<int64_t>(gr.members.size());
+      CopyPiece& c = cl.pieces[cl.npieces++];
+      c.storages = gr.table_dev;
+      c.staging = staging + static_cast<uint64_t>(off);
+      c.stride_w = block_major ? gr.block_bytes : n * gr.block_bytes;
+      c.stride_i = block_major ? W * gr.block_bytes : gr.block_bytes;
+      c.f0 = 0;
+      c.nblocks = W * n;
+      c.block_bytes = gr.block_bytes;
+      c.pool_blocks = gr.pool_blocks;
+      acc |= static_cast<uint64_t>(off);
+      off += W * n * gr.block_bytes;
+    }
+    const int vec = LaunchVectorBytes(cl, acc);
+    KVX_RETURN_IF_ERROR(LaunchCopy(cl, gather, vec, stream));
+  }
+  KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, stream));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
+  return CopyFuture::FromEvents({done}, {});
+}
+
+}  // namespace kvx

@@ -1,0 +1,194 @@
+// Block transfer engine: moves whole blocks between paged device storages
+// and host mirrors on one GPU.
+//
+// The reference issues one raw DMA per (layer, shard, run)
+// (tpu_sync/kv_cache/kv_cache_manager_base.cc:1944-2124 ->
+// tpu_sync/core/raw_transfer_core.h:638-692). Here a copy is planned as:
+//   * direct: every run is large, so one hipMemcpyAsync per (storage, run)
+//     between the device storage and the host mirror;
+//   * staged (scattered device ids): the gather kernel packs the blocks of a
+//     chunk of storages into a device staging buffer in host-id order, then a
+//     few large hipMemcpyAsync move each host run; reload is the mirror image
+//     (H2D into staging, then the scatter kernel).
+// Staged copies are pipelined over a ring of staging buffers: the kernel
+// stream and the copy stream hand chunks to each other with events, so the
+// gather of chunk c+1 overlaps the DMA of chunk c and nothing blocks the
+// host. D2H and H2D use separate stream pairs and rings, so an offload and a
+// reload can run at the same time in both PCIe directions.
+#ifndef KVX_HOST_TRANSFER_ENGINE_H_
+#define KVX_HOST_TRANSFER_ENGINE_H_
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <deque>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+#include "copy_future.h"
+#include "status.h"
+
+namespace kvx {
+
+struct CopyLaunch;
+
+// One storage as seen by one copy: a device buffer of pool blocks and the
+// host region (a mirror or a staging-slot span) the copy reads or writes.
+struct StorageView {
+  uint64_t dev = 0;
+  int64_t dev_bytes = 0;
+  uint8_t* host = nullptr;
+  int64_t host_bytes = 0;
+  int64_t block_bytes = 0;
+};
+
+enum class Direction : int { kD2H = 0, kH2D = 1 };
+
+struct EngineOptions {
+  int device = 0;
+  int64_t staging_chunk_bytes = 64ll << 20;
+  int staging_chunks = 4;
+  int64_t arg_ring_bytes = 8ll << 20;
+  // A run moves directly (no staging) only when every run of the copy is at
+  // least this many bytes.
+  int64_t direct_min_bytes = 4ll << 20;
+  // Bracket every kernel launch with timing events on its stream.
+  bool profile_kernels = false;
+};
+
+// Accumulated duration of the profiled launches of one kernel direction.
+struct KernelTimes {
+  int64_t launches = 0;
+  double total_ms = 0;
+  int64_t bytes = 0;  // algorithmic HBM bytes: 2 x bytes moved
+};
+
+// Counters of what the engine issued (for tests and the benchmark).
+struct EngineStats {
+  int64_t direct_copies = 0;
+  int64_t staged_copies = 0;
+  int64_t memcpy_calls = 0;
+  int64_t kernel_launches = 0;
+  int64_t chunks = 0;
+};
+
+class TransferEngine {
+ public:
+  static StatusOr<std::unique_ptr<TransferEngine>> Create(
+      const EngineOptions& opts);
+  ~TransferEngine();
+
+  // Copies runs of whole blocks for every storage in `storages`:
+  // D2H: device block src[r]+k -> host block dst[r]+k;
+  // H2D: host block src[r]+k -> device block dst[r]+k, for k < sizes[r].
+  // Offsets are in blocks of each storage's own block size. The caller has
+  // validated every range. If `dep` is non-null the copy is ordered after
+  // the work already enqueued on it.
+  StatusOr<CopyFuture> Copy(Direction dir,
+                            const std::vector<StorageView>& storages,
+                            const std::vector<int64_t>& src,
+                            const std::vector<int64_t>& dst,
+                            const std::vector<int64_t>& sizes,
+                            hipStream_t dep);
+
+  // Whole-buffer copy of `bytes` per storage (the reference's empty-spec
+  // full-layer copy).
+  StatusOr<CopyFuture> CopyFull(Direction dir,
+                                const std::vector<StorageView>& storages,
+                                const std::vector<int64_t>& bytes,
+                                hipStream_t dep);
+
+  // Device-only gather/scatter between the storages and a caller buffer
+  // laid out layer-major [storage][n][block] (block_major=false) or
+  // block-major [n][storage][block]. Runs on `stream`.
+  StatusOr<CopyFuture> DeviceCopy(bool gather,
+                                  const std::vector<StorageView>& storages,
+                                  const std::vector<int64_t>& ids,
+                                  uint64_t staging, bool block_major,
+                                  hipStream_t stream);
+
+  // Device-side scale/payload groups for one launch: storages that share a
+  // block size form one piece of the kernel (see block_copy.h).
+  int device() const { return opts_.device; }
+  EngineStats stats() const;
+  // Blocks until everything enqueued on the engine's streams has finished.
+  Status Synchronize();
+  // Sums the profiled launches of gather (or scatter) kernels recorded so
+  // far; waits for them to finish. `reset` drops the samples.
+  StatusOr<KernelTimes> ProfiledKernelTimes(bool gather, bool reset);
+
+ private:
+  struct Group {
+    int64_t block_bytes = 0;
+    int64_t pool_blocks = 0;
+    std::vector<int> members;  // indices into the storages vector
+    uint64_t table_dev = 0;    // device address of the base-address table
+  };
+  struct Ring {
+    std::vector<uint64_t> bufs;
+    std::vector<hipEvent_t> ready;
+    std::vector<hipEvent_t> free;
+    std::vector<bool> used;
+    size_t next = 0;
+  };
+  struct ArgSlice {
+    int64_t begin = 0;
+    int64_t end = 0;
+    hipEvent_t done = nullptr;
+  };
+
+  explicit TransferEngine(const EngineOptions& opts) : opts_(opts) {}
+  Status Init();
+  // Reserves `bytes` of the pinned/device argument ring; waits on the host
+  // only if the region is still read by an earlier, unfinished copy.
+  StatusOr<int64_t> ArgAlloc(int64_t bytes);
+  Status ArgCommit(int64_t begin, int64_t end, hipStream_t stream);
+  Status GrowArgRing(int64_t bytes);
+  static std::vector<Group> MakeGroups(const std::vector<StorageView>& s);
+  Status WaitDep(hipStream_t dep, hipStream_t on);
+  StatusOr<CopyFuture> CopyDirect(Direction dir,
+                                  const std::vector<StorageView>& storages,
+                                  const std::vector<int64_t>& src,
+                                  const std::vector<int64_t>& dst,
+                                  const std::vector<int64_t>& sizes,
+                                  hipStream_t dep);
+  StatusOr<CopyFuture> CopyStaged(Direction dir,
+                                  const std::vector<StorageView>& storages,
+                                  const std::vector<int64_t>& src,
+                                  const std::vector<int64_t>& dst,
+                                  const std::vector<int64_t>& sizes,
+                                  hipStream_t dep);
+  StatusOr<hipEvent_t> NewEvent();
+  // Launches one block-copy kernel, bracketed by timing events when
+  // profiling is on.
+  Status LaunchCopy(const CopyLaunch& l, bool gather, int vec,
+                    hipStream_t stream);
+
+  struct KernelSample {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+    int64_t bytes = 0;
+    bool gather = true;
+  };
+
+  EngineOptions opts_;
+  std::vector<KernelSample> samples_;
+  std::mutex mu_;
+  hipStream_t gather_stream_ = nullptr;   // D2H: kernels
+  hipStream_t d2h_stream_ = nullptr;      // D2H: DMA
+  hipStream_t h2d_stream_ = nullptr;      // H2D: DMA
+  hipStream_t scatter_stream_ = nullptr;  // H2D: kernels
+  Ring out_ring_;
+  Ring in_ring_;
+  uint8_t* arg_host_ = nullptr;
+  uint64_t arg_dev_ = 0;
+  int64_t arg_bytes_ = 0;
+  int64_t arg_head_ = 0;
+  std::deque<ArgSlice> arg_inflight_;
+  EngineStats stats_;
+};
+
+}  // namespace kvx
+
+#endif  // KVX_HOST_TRANSFER_ENGINE_H_

@@ -1,0 +1,267 @@
+// Paged-KV block gather/scatter for gfx950 (MI355X).
+//
+// Pure data movement, bound by HBM bandwidth: no MFMA, no LDS on the data
+// itself. Blocks of >= 8 KiB get one 256-lane workgroup each (four wave64s);
+// every lane keeps kUnroll independent 16-byte loads in flight before it
+// stores, which is what saturates HBM on a streaming copy. The block id and
+// the storage base are workgroup-uniform, so the compiler reads them with
+// scalar loads into SGPRs: the id table is read once per block, broadcast
+// through SGPRs instead of an LDS round trip and barrier. Small blocks (side
+// tables such as per-head fp8 scales) are packed many to a workgroup so that
+// every lane still moves one vector.
+//
+// Loads and stores are non-temporal: a gathered block is read once and the
+// staging copy is next read by the DMA engine, so neither should displace
+// L2/MALL lines.
+//
+// Bad block ids (outside [0, pool_blocks)) are skipped and reported through
+// an optional device flag; no lane ever forms an address from one.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "block_copy.h"
+
+namespace kvx {
+namespace {
+
+constexpr int kThreads = 256;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Explicit address spaces: data goes through global_load/global_store (not
+// flat), and workgroup-uniform table reads through the constant address
+// space so they become scalar loads.
+#define KVX_GLOBAL __attribute__((address_space(1)))
+#define KVX_CONST __attribute__((address_space(4)))
+
+template <typename T>
+__device__ __forceinline__ KVX_GLOBAL T* gptr(uint64_t addr) {
+  return (KVX_GLOBAL T*)addr;
+}
+
+template <typename T>
+__device__ __forceinline__ T uniform_load(uint64_t table, uint32_t idx) {
+  return ((const KVX_CONST T*)table)[idx];
+}
+
+struct KPiece {
+  uint64_t storages;
+  uint64_t staging;
+  int64_t stride_w;
+  int64_t stride_i;
+  int64_t pool_blocks;
+  uint32_t f0;
+  uint32_t nblocks;
+  uint32_t elems;     // vectors per block
+  uint32_t bpw;       // blocks per workgroup
+  uint32_t wg_begin;  // first workgroup of the piece
+  uint32_t pad;
+};
+
+struct KParams {
+  KPiece p[kMaxPieces];
+  const int64_t* ids;
+  int32_t* error;
+  uint32_t n;
+  int32_t npieces;
+};
+
+template <typename V>
+__device__ __forceinline__ V ld_nt(const KVX_GLOBAL V* p) {
+  return __builtin_nontemporal_load(p);
+}
+
+template <typename V>
+__device__ __forceinline__ void st_nt(V v, KVX_GLOBAL V* p) {
+  __builtin_nontemporal_store(v, p);
+}
+
+// Whole-block copy by all lanes of the workgroup.
+template <typename V, int kUnroll>
+__device__ __forceinline__ void copy_whole_block(const KVX_GLOBAL V* __restrict__ src,
+                                                 KVX_GLOBAL V* __restrict__ dst,
+                                                 uint32_t elems) {
+  uint32_t k = threadIdx.x;
+  for (; k + (kUnroll - 1) * kThreads < elems; k += kUnroll * kThreads) {
+    V r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) r[u] = ld_nt(src + k + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) st_nt(r[u], dst + k + u * kThreads);
+  }
+  for (; k < elems; k += kThreads) st_nt(ld_nt(src + k), dst + k);
+}
+
+__device__ __forceinline__ KPiece select_piece(const KParams& P, uint32_t wg) {
+  // Pieces are sorted by wg_begin; the choice is workgroup-uniform. Each
+  // candidate is copied by a constant index so the kernel argument block is
+  // read in place rather than spilled to scratch.
+  KPiece p = P.p[0];
+  if (P.npieces > 1 && wg >= P.p[1].wg_begin) p = P.p[1];
+  if (P.npieces > 2 && wg >= P.p[2].wg_begin) p = P.p[2];
+  if (P.npieces > 3 && wg >= P.p[3].wg_begin) p = P.p[3];
+  return p;
+}
+
+template <typename V, bool kGather, int kUnroll>
+__global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
+  const uint32_t wg = blockIdx.x;
+  const KPiece p = select_piece(P, wg);
+  const uint32_t b0 = (wg - p.wg_begin) * p.bpw;
+  const uint32_t n = P.n;
+
+  if (p.bpw == 1) {
+    const uint32_t f = p.f0 + b0;
+    const uint32_t w = f / n;
+    const uint32_t i = f - w * n;
+    const int64_t id = uniform_load<int64_t>(reinterpret_cast<uint64_t>(P.ids), i);
+    if (static_cast<uint64_t>(id) >= static_cast<uint64_t>(p.pool_blocks)) {
+      if (threadIdx.x == 0 && P.error != nullptr) atomicOr(P.error, 1);
+      return;
+    }
+    const uint64_t base = uniform_load<uint64_t>(p.storages, w);
+    KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(id) * p.elems;
+    KVX_GLOBAL V* stg = gptr<V>(p.staging + w * static_cast<uint64_t>(p.stride_w) +
+                                i * static_cast<uint64_t>(p.stride_i));
+    if (kGather) {
+      copy_whole_block<V, kUnroll>(pool, stg, p.elems);
+    } else {
+      copy_whole_block<V, kUnroll>(stg, pool, p.elems);
+    }
+    return;
+  }
+
+  // Many small blocks per workgroup: lane e moves vector (e % elems) of
+  // block (e / elems).
+  const uint32_t left = p.nblocks - b0;
+  const uint32_t nb = left < p.bpw ? left : p.bpw;
+  const uint32_t total = nb * p.elems;
+  for (uint32_t e = threadIdx.x; e < total; e += kThreads) {
+    const uint32_t b = e / p.elems;
+    const uint32_t sub = e - b * p.elems;
+    const uint32_t f = p.f0 + b0 + b;
+    const uint32_t w = f / n;
+    const uint32_t i = f - w * n;
+    const int64_t id = gptr<const int64_t>(reinterpret_cast<uint64_t>(P.ids))[i];
+    if (static_cast<uint64_t>(id) >= static_cast<uint64_t>(p.pool_blocks)) {
+      if (P.error != nullptr) atomicOr(P.error, 1);
+      continue;
+    }
+    const uint64_t base = gptr<const uint64_t>(p.storages)[w];
+    KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(id) * p.elems + sub;
+    KVX_GLOBAL V* stg = gptr<V>(p.staging + w * static_cast<uint64_t>(p.stride_w) +
+                                i * static_cast<uint64_t>(p.stride_i)) +
+                        sub;
+    if (kGather) {
+      st_nt(ld_nt(pool), stg);
+    } else {
+      st_nt(ld_nt(stg), pool);
+    }
+  }
+}
+
+// Blocks per workgroup: one for blocks of >= 2 vectors per lane, otherwise
+// enough blocks to give each lane about 8 vectors.
+uint32_t BlocksPerWorkgroup(uint64_t elems) {
+  if (elems >= 2 * kThreads) return 1;
+  uint64_t bpw = (8 * kThreads) / (elems == 0 ? 1 : elems);
+  return static_cast<uint32_t>(bpw < 1 ? 1 : bpw);
+}
+
+bool BuildParams(const CopyLaunch& l, int vec_bytes, KParams* P,
+                 uint32_t* grid) {
+  if (l.npieces < 1 || l.npieces > kMaxPieces || l.ids == nullptr ||
+      l.n <= 0 || l.n > INT32_MAX || vec_bytes <= 0) {
+    return false;
+  }
+  *P = KParams{};
+  P->ids = l.ids;
+  P->error = l.error;
+  P->n = static_cast<uint32_t>(l.n);
+  P->npieces = l.npieces;
+  uint64_t wg = 0;
+  for (int k = 0; k < l.npieces; ++k) {
+    const CopyPiece& c = l.pieces[k];
+    if (c.storages == 0 || c.nblocks <= 0 || c.f0 < 0 || c.block_bytes <= 0 ||
+        c.block_bytes % vec_bytes != 0 || c.pool_blocks <= 0) {
+      return false;
+    }
+    if (static_cast<uint64_t>(c.f0) + static_cast<uint64_t>(c.nblocks) >
+        UINT32_MAX) {
+      return false;
+    }
+    const uint64_t elems = static_cast<uint64_t>(c.block_bytes) / vec_bytes;
+    if (elems > UINT32_MAX) return false;
+    const uint32_t bpw = BlocksPerWorkgroup(elems);
+    if (static_cast<uint64_t>(bpw) * elems > UINT32_MAX) return false;
+    KPiece& kp = P->p[k];
+    kp.storages = c.storages;
+    kp.staging = c.staging;
+    kp.stride_w = c.stride_w;
+    kp.stride_i = c.stride_i;
+    kp.pool_blocks = c.pool_blocks;
+    kp.f0 = static_cast<uint32_t>(c.f0);
+    kp.nblocks = static_cast<uint32_t>(c.nblocks);
+    kp.elems = static_cast<uint32_t>(elems);
+    kp.bpw = bpw;
+    kp.wg_begin = static_cast<uint32_t>(wg);
+    wg += (static_cast<uint64_t>(c.nblocks) + bpw - 1) / bpw;
+    if (wg > INT32_MAX) return false;
+  }
+  *grid = static_cast<uint32_t>(wg);
+  return true;
+}
+
+template <typename V, int kUnroll>
+hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir,
+                  hipStream_t stream) {
+  if (dir == CopyDir::kGather) {
+    hipLaunchKernelGGL((block_copy_kernel<V, true, kUnroll>), dim3(grid),
+                       dim3(kThreads), 0, stream, P);
+  } else {
+    hipLaunchKernelGGL((block_copy_kernel<V, false, kUnroll>), dim3(grid),
+                       dim3(kThreads), 0, stream, P);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int LaunchVectorBytes(const CopyLaunch& l, uint64_t extra_align) {
+  uint64_t acc = extra_align;
+  for (int k = 0; k < l.npieces && k < kMaxPieces; ++k) {
+    const CopyPiece& c = l.pieces[k];
+    acc |= static_cast<uint64_t>(c.block_bytes) | c.staging |
+           static_cast<uint64_t>(c.stride_w) | static_cast<uint64_t>(c.stride_i);
+  }
+  if ((acc & 15) == 0) return 16;
+  if ((acc & 3) == 0) return 4;
+  return 1;
+}
+
+int64_t BlockCopyWorkgroups(const CopyLaunch& l, int vec_bytes) {
+  KParams P;
+  uint32_t grid = 0;
+  if (!BuildParams(l, vec_bytes, &P, &grid)) return -1;
+  return grid;
+}
+
+hipError_t LaunchBlockCopy(const CopyLaunch& l, CopyDir dir, int vec_bytes,
+                           hipStream_t stream) {
+  KParams P;
+  uint32_t grid = 0;
+  if (!BuildParams(l, vec_bytes, &P, &grid)) return hipErrorInvalidValue;
+  switch (vec_bytes) {
+    case 16:
+      return Launch<u32x4, 8>(P, grid, dir, stream);
+    case 4:
+      return Launch<uint32_t, 8>(P, grid, dir, stream);
+    case 1:
+      return Launch<uint8_t, 8>(P, grid, dir, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace kvx

@@ -1,0 +1,435 @@
+"""PyTorch-facing KV cache manager over libkvx (MI355X).
+
+Mirrors the reference's Python surface
+(tpu_sync/api/torch/kv_cache_manager.py:55-439 and the nanobind module
+tpu_sync/frameworks/torch/tpu_raiden_torch_module.cc:339-395): ``d2h`` /
+``h2d`` by major-dimension block offsets returning a future with
+``Await`` / ``IsReady`` / ``PollError``, ``d2h_auto_allocate``,
+``read_block_bytes`` / ``write_block_bytes`` and the CPU-only constructor
+``create_host_only_for_testing``. Errors raise ``RuntimeError`` subclasses
+whose text follows the reference's "KVCacheManager D2h failed: <msg>".
+
+This module only passes pointers: device tensors by ``data_ptr()`` and
+streams by ``cuda_stream``. All copying happens in libkvx.
+"""
+import ctypes
+from typing import Any, List, Optional, Sequence, Tuple
+
+from . import _capi
+
+
+class RaidenFuture:
+    """Async completion of one copy (tpu_sync/core/raiden_future.h:25-36)."""
+
+    def __init__(self, handle, keep_alive=None, where=""):
+        self._h = handle
+        self._keep = keep_alive
+        self._where = where
+
+    def Await(self) -> None:
+        """Blocks until the copy finished; raises on failure."""
+        _capi.check(_capi.load().kvx_future_await(self._h), self._where)
+
+    def IsReady(self) -> bool:
+        return bool(_capi.load().kvx_future_is_ready(self._h))
+
+    def PollError(self) -> None:
+        """Non-blocking: raises if the copy already failed."""
+        _capi.check(_capi.load().kvx_future_poll_error(self._h), self._where)
+
+    def wait_on_stream(self, stream=None) -> None:
+        """Orders `stream` (default: torch's current stream) after the copy."""
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream()
+        _capi.check(_capi.load().kvx_future_wait_on_stream(
+            self._h, ctypes.c_void_p(_stream_ptr(stream))), self._where)
+
+    # Pythonic aliases.
+    await_ = Await
+    is_ready = IsReady
+    poll_error = PollError
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h and _capi._lib is not None:
+            _capi._lib.kvx_future_release(h)
+
+
+def _stream_ptr(stream) -> int:
+    if stream is None:
+        return 0
+    if isinstance(stream, int):
+        return stream
+    return int(getattr(stream, "cuda_stream", stream))
+
+
+def _flatten_caches(kv_caches) -> Tuple[List[List[Any]], int]:
+    layers = []
+    for entry in kv_caches:
+        shards = list(entry) if isinstance(entry, (list, tuple)) else [entry]
+        layers.append(shards)
+    num_shards = len(layers[0]) if layers else 0
+    if any(len(s) != num_shards for s in layers):
+        raise RuntimeError("Number of shards mismatch across layers")
+    return layers, num_shards
+
+
+class LogicalBlockManager:
+    """Host block allocator (tpu_sync/kv_cache/logical_block_manager.h:35-93)."""
+
+    def __init__(self, num_blocks: int = 0, _handle=None, _owner=None):
+        lib = _capi.load()
+        if _handle is not None:
+            self._h, self._owned, self._owner = _handle, False, _owner
+        else:
+            h = ctypes.c_void_p()
+            _capi.check(lib.kvx_block_manager_create(num_blocks, ctypes.byref(h)))
+            self._h, self._owned, self._owner = h, True, None
+
+    def allocate(self, num_blocks: int, lock: bool = False) -> List[int]:
+        out = (ctypes.c_int32 * max(num_blocks, 1))()
+        _capi.check(_capi.load().kvx_block_manager_allocate(self._h, num_blocks,
+                                                            int(lock), out))
+        return list(out[:num_blocks])
+
+    def _ids_call(self, fn, ids):
+        arr, n = _capi.i32_array(ids)
+        _capi.check(fn(self._h, arr, n))
+
+    def allocate_target(self, ids: Sequence[int]) -> None:
+        self._ids_call(_capi.load().kvx_block_manager_allocate_target, ids)
+
+    def unlock(self, ids: Sequence[int]) -> None:
+        self._ids_call(_capi.load().kvx_block_manager_unlock, ids)
+
+    def deallocate(self, ids: Sequence[int]) -> None:
+        self._ids_call(_capi.load().kvx_block_manager_deallocate, ids)
+
+    def access_block(self, block_id: int) -> None:
+        _capi.check(_capi.load().kvx_block_manager_access(self._h, block_id))
+
+    def is_allocated(self, block_id: int) -> bool:
+        return bool(_capi.load().kvx_block_manager_is_allocated(self._h, block_id))
+
+    def is_locked(self, block_id: int) -> bool:
+        return bool(_capi.load().kvx_block_manager_is_locked(self._h, block_id))
+
+    @property
+    def total_blocks(self) -> int:
+        return _capi.load().kvx_block_manager_total_blocks(self._h)
+
+    @property
+    def num_free_blocks(self) -> int:
+        return _capi.load().kvx_block_manager_num_free(self._h)
+
+    @property
+    def num_allocated_blocks(self) -> int:
+        return _capi.load().kvx_block_manager_num_allocated(self._h)
+
+    @property
+    def num_locked_blocks(self) -> int:
+        return _capi.load().kvx_block_manager_num_locked(self._h)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and getattr(self, "_owned", False) and _capi._lib is not None:
+            _capi._lib.kvx_block_manager_destroy(h)
+            self._h = None
+
+
+class KVCacheManager:
+    """Paged KV cache manager on one MI355X.
+
+    Args:
+      kv_caches: one contiguous device tensor per layer (K and V buffers count
+        as separate layers), or a list of per-shard tensors per layer. Every
+        tensor's first dimension is the block (major) dimension.
+      host_blocks_to_allocate: host mirror blocks per (layer, shard).
+      max_blocks / num_slots: alternatively, a staging-slot layout; the host
+        mirror then holds max_blocks * num_slots blocks.
+      host_alloc: "pinned" (hipHostMalloc, default), "malloc" or "shm".
+      staging_chunk_bytes / staging_chunks: device staging ring per direction.
+      The remaining reference arguments (ports, controller address, worker
+      id, timeout, parallelism, unsafe_skip_buffer_lock) configure its
+      networking and control plane, which this single-GPU build does not
+      have; they are accepted and ignored.
+    """
+
+    def __init__(self, kv_caches: List[Any], local_control_port: int = 0,
+                 max_blocks: Optional[int] = None, num_slots: Optional[int] = None,
+                 timeout_s: float = 120.0, unsafe_skip_buffer_lock: bool = True,
+                 host_blocks_to_allocate: Optional[int] = None, parallelism: int = 4,
+                 node_id: int = 0, listener_port: Optional[int] = None,
+                 raiden_worker_port: int = 0,
+                 raiden_controller_address: Optional[str] = None,
+                 worker_id: Optional[str] = None, *, host_alloc: str = "pinned",
+                 staging_chunk_bytes: int = 0, staging_chunks: int = 0,
+                 direct_min_bytes: int = 0, shm_key: Optional[str] = None,
+                 shm_server_name: Optional[str] = None,
+                 model_uid: Optional[str] = None, profile_kernels: bool = False):
+        if host_blocks_to_allocate is None:
+            if max_blocks is None or num_slots is None:
+                raise ValueError("Must specify either (max_blocks, num_slots) or"
+                                 " host_blocks_to_allocate.")
+            host_blocks_to_allocate = max_blocks * num_slots
+        layers, num_shards = _flatten_caches(kv_caches)
+        ptrs, sizes = [], []
+        major_dim = 0
+        device = 0
+        for shards in layers:
+            for t in shards:
+                if not t.is_contiguous():
+                    raise RuntimeError("kv cache tensors must be contiguous")
+                ptrs.append(t.data_ptr())
+                sizes.append(t.numel() * t.element_size())
+                device = t.device.index or 0
+        if layers:
+            major_dim = int(layers[0][0].shape[0])
+        self._tensors = layers  # borrowed device buffers stay alive
+        self._init(device, len(layers), num_shards, ptrs, sizes, major_dim, 0,
+                   host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
+                   staging_chunks, direct_min_bytes, shm_key, shm_server_name,
+                   model_uid, profile_kernels)
+        self.node_id = node_id
+        if max_blocks is not None and num_slots is not None:
+            self.configure_host_staging_slots(num_slots, max_blocks)
+
+    def _init(self, device, num_layers, num_shards, ptrs, sizes, major_dim,
+              slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
+              direct_min_bytes, shm_key, shm_server_name, model_uid,
+              profile_kernels=False):
+        lib = _capi.load()
+        kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
+                 "shm": _capi.HOST_SHM}
+        cfg = _capi.ManagerConfig()
+        cfg.device = device
+        cfg.host_alloc = kinds[host_alloc]
+        cfg.num_layers = num_layers
+        cfg.num_shards = num_shards
+        if ptrs:
+            self._ptr_arr = (ctypes.c_uint64 * len(ptrs))(*ptrs)
+            self._size_arr = (ctypes.c_int64 * len(sizes))(*sizes)
+            cfg.device_ptrs = self._ptr_arr
+            cfg.device_bytes = self._size_arr
+        cfg.major_dim = major_dim
+        cfg.slice_byte_size = slice_byte_size
+        cfg.host_blocks = host_blocks
+        cfg.staging_chunk_bytes = chunk_bytes
+        cfg.staging_chunks = chunks
+        cfg.direct_min_bytes = direct_min_bytes
+        cfg.shm_key = shm_key.encode() if shm_key else None
+        cfg.shm_server_name = shm_server_name.encode() if shm_server_name else None
+        cfg.model_uid = model_uid.encode() if model_uid else None
+        cfg.profile_kernels = int(bool(profile_kernels))
+        h = ctypes.c_void_p()
+        _capi.check(lib.kvx_manager_create(ctypes.byref(cfg), ctypes.byref(h)),
+                    "KVCacheManager create")
+        self._h = h
+
+    @classmethod
+    def create_host_only_for_testing(cls, *, num_layers: int, num_shards: int = 1,
+                                     slice_byte_size: int, node_id: int = 0,
+                                     local_port: Optional[int] = None,
+                                     host_blocks: int, parallelism: int = 4,
+                                     host_alloc: str = "malloc") -> "KVCacheManager":
+        """CPU-only manager backed by library-owned host memory."""
+        obj = cls.__new__(cls)
+        obj._tensors = []
+        obj._init(0, num_layers, num_shards, [], [], 0, slice_byte_size, host_blocks,
+                  host_alloc, 0, 0, 0, None, None, None)
+        obj.node_id = node_id
+        return obj
+
+    # -- copies -------------------------------------------------------------
+    def _transfer(self, fn, where, src, dst, sizes, slot_idx, layer_idx, shard_idx,
+                  stream):
+        s, ns = _capi.i64_array(src)
+        d, nd = _capi.i64_array(dst)
+        z, nz = _capi.i64_array(sizes if sizes is not None else [])
+        out = ctypes.c_void_p()
+        _capi.check(fn(self._h, s, ns, d, nd, z, nz,
+                       -1 if slot_idx is None else slot_idx,
+                       -1 if layer_idx is None else layer_idx,
+                       -1 if shard_idx is None else shard_idx,
+                       ctypes.c_void_p(_stream_ptr(stream)), ctypes.byref(out)), where)
+        return RaidenFuture(out, self, where)
+
+    def d2h(self, src_offsets: Sequence[int] = (), dst_offsets: Sequence[int] = (),
+            copy_sizes: Optional[Sequence[int]] = None, *, slot_idx=None,
+            layer_idx=None, shard_idx=None, stream=None,
+            src_offsets_major_dim=None, dst_offsets_major_dim=None,
+            copy_sizes_major_dim=None) -> RaidenFuture:
+        """Device-to-host copy of whole blocks (defaults to 1 block per entry)."""
+        src = src_offsets_major_dim if src_offsets_major_dim is not None else src_offsets
+        dst = dst_offsets_major_dim if dst_offsets_major_dim is not None else dst_offsets
+        sizes = copy_sizes_major_dim if copy_sizes_major_dim is not None else copy_sizes
+        if sizes is None:
+            sizes = [1] * len(src)
+        return self._transfer(_capi.load().kvx_manager_d2h, "KVCacheManager D2h", src,
+                              dst, sizes, slot_idx, layer_idx, shard_idx, stream)
+
+    def h2d(self, src_offsets: Sequence[int] = (), dst_offsets: Sequence[int] = (),
+            copy_sizes: Optional[Sequence[int]] = None, *, slot_idx=None,
+            layer_idx=None, shard_idx=None, stream=None,
+            src_offsets_major_dim=None, dst_offsets_major_dim=None,
+            copy_sizes_major_dim=None) -> RaidenFuture:
+        """Host-to-device copy of whole blocks (defaults to 1 block per entry)."""
+        src = src_offsets_major_dim if src_offsets_major_dim is not None else src_offsets
+        dst = dst_offsets_major_dim if dst_offsets_major_dim is not None else dst_offsets
+        sizes = copy_sizes_major_dim if copy_sizes_major_dim is not None else copy_sizes
+        if sizes is None:
+            sizes = [1] * len(src)
+        return self._transfer(_capi.load().kvx_manager_h2d, "KVCacheManager H2d", src,
+                              dst, sizes, slot_idx, layer_idx, shard_idx, stream)
+
+    # Reference spellings.
+    D2h = d2h
+    H2d = h2d
+
+    def d2h_auto_allocate(self, src_offsets_major_dim: Sequence[int] = (),
+                          copy_sizes_major_dim: Sequence[int] = (), *, stream=None
+                          ) -> Tuple[List[int], RaidenFuture]:
+        s, ns = _capi.i64_array(src_offsets_major_dim)
+        z, nz = _capi.i64_array(copy_sizes_major_dim)
+        total = sum(max(int(v), 0) for v in copy_sizes_major_dim)
+        ids = (ctypes.c_int32 * max(total, 1))()
+        n_out = ctypes.c_int64()
+        out = ctypes.c_void_p()
+        where = "KVCacheManager D2hAutoAllocate"
+        _capi.check(_capi.load().kvx_manager_d2h_auto_allocate(
+            self._h, s, ns, z, nz, ids, total, ctypes.byref(n_out),
+            ctypes.c_void_p(_stream_ptr(stream)), ctypes.byref(out)), where)
+        return list(ids[:n_out.value]), RaidenFuture(out, self, where)
+
+    D2hAutoAllocate = d2h_auto_allocate
+
+    def _device_copy(self, fn, where, block_ids, staging, order, layer_idx, shard_idx,
+                     stream):
+        ids, n = _capi.i64_array(block_ids)
+        nbytes = staging.numel() * staging.element_size()
+        out = ctypes.c_void_p()
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream(staging.device)
+        _capi.check(fn(self._h, ids, n, staging.data_ptr(), nbytes, order,
+                       -1 if layer_idx is None else layer_idx,
+                       -1 if shard_idx is None else shard_idx,
+                       ctypes.c_void_p(_stream_ptr(stream)), ctypes.byref(out)), where)
+        return RaidenFuture(out, (self, staging), where)
+
+    def gather(self, block_ids: Sequence[int], staging, *, block_major: bool = False,
+               layer_idx=None, shard_idx=None, stream=None) -> RaidenFuture:
+        """Extracts blocks into a contiguous device staging tensor (one kernel)."""
+        order = _capi.BLOCK_MAJOR if block_major else _capi.LAYER_MAJOR
+        return self._device_copy(_capi.load().kvx_manager_gather, "KVCacheManager gather",
+                                 block_ids, staging, order, layer_idx, shard_idx, stream)
+
+    def scatter(self, block_ids: Sequence[int], staging, *, block_major: bool = False,
+                layer_idx=None, shard_idx=None, stream=None) -> RaidenFuture:
+        """Inserts a contiguous device staging tensor into the paged pool."""
+        order = _capi.BLOCK_MAJOR if block_major else _capi.LAYER_MAJOR
+        return self._device_copy(_capi.load().kvx_manager_scatter, "KVCacheManager scatter",
+                                 block_ids, staging, order, layer_idx, shard_idx, stream)
+
+    # -- staging slots and host blocks --------------------------------------
+    def configure_host_staging_slots(self, num_slots: int, max_major_per_slot: int) -> None:
+        _capi.check(_capi.load().kvx_manager_configure_host_staging_slots(
+            self._h, num_slots, max_major_per_slot))
+
+    def host_span(self, layer_idx: int, shard_idx: int, slot_idx: int,
+                  num_major: int) -> Tuple[int, int, int]:
+        """(host address, nbytes, base_major) of a staging-slot span."""
+        ptr, nbytes, base = ctypes.c_uint64(), ctypes.c_int64(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_host_span(
+            self._h, layer_idx, shard_idx, slot_idx, num_major, ctypes.byref(ptr),
+            ctypes.byref(nbytes), ctypes.byref(base)))
+        return ptr.value, nbytes.value, base.value
+
+    def get_block_host_pointer(self, layer_idx: int, shard_idx: int, block_id: int) -> int:
+        ptr = ctypes.c_uint64()
+        _capi.check(_capi.load().kvx_manager_block_host_ptr(
+            self._h, layer_idx, shard_idx, block_id, ctypes.byref(ptr)))
+        return ptr.value
+
+    def read_block_bytes(self, layer_idx: int, block_id: int, shard_idx: int = 0) -> bytes:
+        n = self.block_bytes(layer_idx)
+        buf = ctypes.create_string_buffer(max(n, 1))
+        _capi.check(_capi.load().kvx_manager_read_block(self._h, layer_idx, block_id,
+                                                        shard_idx, buf, n))
+        return buf.raw[:n]
+
+    def write_block_bytes(self, layer_idx: int, block_id: int, payload: bytes,
+                          shard_idx: int = 0) -> None:
+        payload = bytes(payload)
+        _capi.check(_capi.load().kvx_manager_write_block(
+            self._h, layer_idx, block_id, shard_idx, payload, len(payload)))
+
+    def host_view(self, layer_idx: int, shard_idx: int = 0):
+        """numpy uint8 view of one (layer, shard) host mirror (no copy)."""
+        import numpy as np
+        lib = _capi.load()
+        ptr = lib.kvx_manager_block_array_host_ptr(self._h, layer_idx, shard_idx)
+        size = lib.kvx_manager_block_array_host_size(self._h, layer_idx, shard_idx)
+        if not ptr or size <= 0:
+            return np.zeros(0, np.uint8)
+        return np.ctypeslib.as_array((ctypes.c_uint8 * size).from_address(ptr))
+
+    # -- geometry ----------------------------------------------------------
+    @property
+    def num_layers(self) -> int:
+        return _capi.load().kvx_manager_num_layers(self._h)
+
+    @property
+    def num_shards(self) -> int:
+        return _capi.load().kvx_manager_num_shards(self._h)
+
+    @property
+    def host_blocks(self) -> int:
+        return _capi.load().kvx_manager_host_blocks(self._h)
+
+    def bytes_per_block(self) -> int:
+        return _capi.load().kvx_manager_bytes_per_block(self._h)
+
+    def block_bytes(self, block_array_idx: int) -> int:
+        return _capi.load().kvx_manager_block_bytes(self._h, block_array_idx)
+
+    def layer_block_byte_size(self, layer_idx: int) -> int:
+        return _capi.load().kvx_manager_layer_block_byte_size(self._h, layer_idx)
+
+    def num_block_arrays(self) -> int:
+        return _capi.load().kvx_manager_num_block_arrays(self._h)
+
+    def get_allocated_host_dram_bytes(self) -> int:
+        return _capi.load().kvx_manager_allocated_host_bytes(self._h)
+
+    def host_block_manager(self) -> LogicalBlockManager:
+        h = _capi.load().kvx_manager_host_block_manager(self._h)
+        return LogicalBlockManager(_handle=ctypes.c_void_p(h), _owner=self)
+
+    def wait_for_pending_work(self) -> None:
+        _capi.check(_capi.load().kvx_manager_wait_for_pending_work(self._h))
+
+    def engine_stats(self) -> dict:
+        out = (ctypes.c_int64 * 5)()
+        _capi.check(_capi.load().kvx_manager_engine_stats(self._h, out))
+        keys = ("direct_copies", "staged_copies", "memcpy_calls", "kernel_launches",
+                "chunks")
+        return dict(zip(keys, list(out)))
+
+    def kernel_times(self, gather: bool = True, reset: bool = False) -> dict:
+        """Profiled launches of the gather (or scatter) kernel: count, total ms
+        (HIP events on the kernel's stream) and algorithmic HBM bytes."""
+        n, ms, nbytes = ctypes.c_int64(), ctypes.c_double(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_kernel_times(
+            self._h, int(gather), int(reset), ctypes.byref(n), ctypes.byref(ms),
+            ctypes.byref(nbytes)))
+        return {"launches": n.value, "total_ms": ms.value, "bytes": nbytes.value}
+
+    def close(self) -> None:
+        h, self._h = getattr(self, "_h", None), None
+        if h and _capi._lib is not None:
+            _capi._lib.kvx_manager_destroy(h)
+
+    def __del__(self):
+        self.close()
