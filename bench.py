@@ -25,6 +25,16 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
 
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and, in a
+# second run, WRITE_SIZE (KiB per dispatch), each divided by the factor the
+# same counter reads for a plain 1 GiB device copy in the same runs (FETCH
+# 0.500, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
+# (kernel, algorithmic bytes per launch).
+MEASURED_TRAFFIC = {
+    ("gather", 2 * 512 * 64 * 32768): int((524347.8 / 0.50002 + 1048579.75 / 1.0) * 1024),
+    ("scatter", 2 * 512 * 64 * 32768): int((524345.6 / 0.50002 + 1048598.8 / 1.0) * 1024),
+}
+
 WORKLOADS = {
     "llama3-8b-kv": dict(layers=32, kv_heads=8, head_dim=128, block_tokens=16,
                          dtype="bf16", dtype_bytes=2, pool_blocks=16384, batch=512),
@@ -47,7 +57,52 @@ def parse_args():
                    help="minimum seconds per CPU-baseline leg (0 skips it)")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the one-direction and PCIe-peak measurements")
+    p.add_argument("--rocpd-summary", metavar="DB",
+                   help="print per-kernel (name, grid) duration statistics of a "
+                        "rocprofv3 results database and exit")
     return p.parse_args()
+
+
+def rocpd_summary(db_path):
+    """Kernel durations grouped by (kernel, grid size) and memory copies by
+    direction, from a rocprofv3 --kernel-trace results database."""
+    import sqlite3
+    con = sqlite3.connect(db_path)
+    cur = con.cursor()
+    print(f"{'kernel':<72} {'grid':>9} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}")
+    q = ("select name, grid_x, count(*), avg(end - start), min(end - start), "
+         "max(end - start), sum(end - start) from kernels group by name, grid_x "
+         "order by sum(end - start) desc")
+    for name, grid, cnt, avg, mn, mx, _ in cur.execute(q):
+        short = (name.replace("void ", "").replace("(anonymous namespace)::", "")
+                 .replace("unsigned int __vector(4)", "u32x4"))
+        if ">(" in short:
+            short = short[:short.index(">(") + 1]
+        short = short if len(short) <= 72 else short[:69] + "..."
+        print(f"{short:<72} {grid:>9} {cnt:>6} {avg / 1e3:>9.2f} {mn / 1e3:>9.2f} {mx / 1e3:>9.2f}")
+    q = ("select p.name, k.grid_x, p.counter_name, count(*), avg(p.counter_value), "
+         "min(p.counter_value), max(p.counter_value) from pmc_events p left join kernels k "
+         "on p.dispatch_id = k.dispatch_id group by p.name, k.grid_x, p.counter_name")
+    rows = list(cur.execute(q))
+    if rows:
+        print(f"\n{'kernel (pmc)':<60} {'grid':>9} {'counter':>11} {'calls':>6} "
+              f"{'avg':>13} {'min':>13} {'max':>13}")
+        for name, grid, counter, cnt, avg, mn, mx in rows:
+            short = (name.replace("void ", "").replace("(anonymous namespace)::", "")
+                     .replace("unsigned int __vector(4)", "u32x4"))
+            if ">(" in short:
+                short = short[:short.index(">(") + 1]
+            short = short if len(short) <= 60 else short[:57] + "..."
+            print(f"{short:<60} {grid or 0:>9} {counter:>11} {cnt:>6} {avg:>13.1f} "
+                  f"{mn:>13.1f} {mx:>13.1f}")
+    q = ("select name, count(*), sum(size), avg(end - start), sum(end - start) "
+         "from memory_copies group by name")
+    rows = list(cur.execute(q))
+    if rows:
+        print(f"\n{'memory copy':<32} {'calls':>6} {'GB':>9} {'avg_us':>9} {'GB/s':>9}")
+        for name, cnt, size, avg, tot in rows:
+            print(f"{name:<32} {cnt:>6} {size / 1e9:>9.3f} {avg / 1e3:>9.2f} "
+                  f"{size / tot if tot else 0:>9.2f}")
 
 
 def timed_events(torch, fn, reps, stream):
@@ -138,6 +193,9 @@ def cpu_baseline(oracle, S, bb, n, min_seconds):
 
 def main():
     args = parse_args()
+    if args.rocpd_summary:
+        rocpd_summary(args.rocpd_summary)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU; this build has no "
                                    "multi-GPU path (--gpus must be 1)"}))
@@ -205,21 +263,64 @@ def main():
     ks = mgr.kernel_times(False, reset=True)
     log(f"offload+reload: {value:.2f} GB/s, {elapsed / args.steps * 1e3:.2f} ms/step")
 
-    def kernel_roofline(kt):
+    def pipeline_kernel(kt, name):
         if kt["launches"] == 0:
             return None
         avg_s = kt["total_ms"] / kt["launches"] / 1e3
         per_launch = kt["bytes"] / kt["launches"]
-        ach = per_launch / avg_s / 1e9
-        return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "block_copy_kernel (gather)", "launches": kt["launches"],
-                "avg_launch_us": round(avg_s * 1e6, 2), "bytes_per_launch": int(per_launch)}
+        return {"kernel": f"block_copy_kernel ({name}) per staging chunk in the pipeline",
+                "achieved_gbps": round(per_launch / avg_s / 1e9, 1),
+                "launches": kt["launches"], "avg_launch_us": round(avg_s * 1e6, 2),
+                "bytes_per_launch": int(per_launch)}
 
-    roof = kernel_roofline(kg)
-    scatter_roof = kernel_roofline(ks)
-    if scatter_roof:
-        scatter_roof["kernel"] = "block_copy_kernel (scatter)"
+    pipe_gather = pipeline_kernel(kg, "gather")
+    pipe_scatter = pipeline_kernel(ks, "scatter")
+
+    # The gather/scatter kernels alone: one launch moves the whole batch
+    # (n blocks x S storages, 2 * n * S * B algorithmic HBM bytes) between the
+    # pool and a device staging buffer, on a stream of its own, timed with
+    # HIP events on that stream. Inside the offload pipeline the same kernel
+    # shares the CUs with the runtime's D2H blit kernels, so its pipeline
+    # launches are reported separately.
+    log("timing the gather/scatter kernels alone")
+    staging = torch.empty(n * S * bb, dtype=torch.uint8, device=dev)
+    ks_stream = torch.cuda.Stream(dev)
+    ids_fixed, free_fixed = batch()
+    iso = {}
+    for name, fn, ids_ in (("gather", mgr.gather, ids_fixed), ("scatter", mgr.scatter, free_fixed)):
+        for _ in range(2):
+            fn(ids_, staging, stream=ks_stream).Await()
+        # The engine brackets each launch with HIP events on ks_stream (the
+        # stream the kernel runs on); the id-table upload before it is not
+        # inside the bracket.
+        mgr.kernel_times(name == "gather", reset=True)
+        futs = [fn(ids_, staging, stream=ks_stream) for _ in range(args.steps)]
+        for f in futs:
+            f.Await()
+        kt = mgr.kernel_times(name == "gather", reset=True)
+        avg_s = kt["total_ms"] / kt["launches"] / 1e3
+        per_launch = kt["bytes"] / kt["launches"]
+        assert per_launch == 2 * n * S * bb
+        ach = per_launch / avg_s / 1e9
+        iso[name] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                     "traffic": MEASURED_TRAFFIC.get((name, per_launch)),
+                     "kernel": f"block_copy_kernel ({name}), {n} ids x {S} storages per launch",
+                     "launches": kt["launches"], "avg_launch_us": round(avg_s * 1e6, 2),
+                     "bytes_per_launch": int(per_launch)}
+        log(f"{name} alone: {ach:.0f} GB/s ({ach / HBM_PEAK_GBPS:.1%} of HBM peak)")
+    # A plain device copy of the same byte count: the measured copy ceiling,
+    # and the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters.
+    copy_dst = torch.empty_like(staging)
+    t_copy = timed_events(torch, lambda: copy_dst.copy_(staging), max(3, args.steps // 4),
+                          ks_stream)
+    hbm_copy_gbps = 2 * staging.numel() / t_copy / 1e9
+    log(f"plain device copy of {staging.numel() >> 20} MiB: {hbm_copy_gbps:.0f} GB/s")
+    del staging, copy_dst
+    mgr.kernel_times(True, reset=True)
+    mgr.kernel_times(False, reset=True)
+    roof = iso["gather"]
+    scatter_roof = iso["scatter"]
 
     extras = {}
     if not args.no_extras:
@@ -278,6 +379,10 @@ def main():
         "blocks_per_s": round(args.steps * 2 * n / elapsed, 1),
         "roofline": roof,
         "scatter_roofline": scatter_roof,
+        "pipeline_gather": pipe_gather,
+        "pipeline_scatter": pipe_scatter,
+        "hbm_copy_same_bytes_gbps": round(hbm_copy_gbps, 1),
+        "gather_frac_of_measured_copy": round(roof["achieved"] / hbm_copy_gbps, 4),
         "cpu_baseline": cpu,
         **extras,
     }
