@@ -4,10 +4,13 @@
 Workload (default): Llama-3-8B-shaped paged KV cache -- 32 layers with K and
 V in separate buffers (64 storages), 8 KV heads, head_dim 128, 16-token
 blocks, bf16, a pool of 16384 blocks (32 GiB of HBM). One step offloads a
-batch of 512 random blocks (gather kernel + D2H into a pinned host slot) and
-reloads the previous batch from the other host slot (H2D + scatter kernel
-into 512 random free blocks); the two run at the same time in the two PCIe
-directions. value = KV payload bytes offloaded + reloaded per second.
+batch of 512 random blocks into a pinned host slot and reloads the previous
+batch from the other host slot into 512 random free blocks; the two run at
+the same time in the two PCIe directions. value = KV payload bytes
+offloaded + reloaded per second. The headline mode (auto) moves short runs
+with one zero-copy kernel (pool <-> pinned host over PCIe); the staged mode
+(gather kernel + hipMemcpyAsync through a device staging ring, and H2D +
+scatter) is measured in the same run.
 
 Printed as one JSON line, with the gather kernel's HBM roofline (HIP events
 on the kernel's stream over the timed region), measured pinned PCIe peaks
@@ -56,7 +59,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=5.0,
                    help="minimum seconds per CPU-baseline leg (0 skips it)")
     p.add_argument("--no-extras", action="store_true",
-                   help="skip the one-direction and PCIe-peak measurements")
+                   help="skip the per-mode, one-direction and PCIe-peak measurements")
+    p.add_argument("--mode", default="auto", choices=["auto", "staged", "zero_copy"],
+                   help="transfer mode of the headline offload/reload loop")
     p.add_argument("--rocpd-summary", metavar="DB",
                    help="print per-kernel (name, grid) duration statistics of a "
                         "rocprofv3 results database and exit")
@@ -191,6 +196,51 @@ def cpu_baseline(oracle, S, bb, n, min_seconds):
     }
 
 
+def run_duplex(torch, mgr, batch, slots, steps, warmup):
+    """Offload batch k into host slot k%2 while reloading the other slot into
+    fresh free blocks; returns the seconds the timed steps took."""
+    mgr.d2h(batch()[0], slots[1]).Await()  # the first reload reads real data
+    pending = []
+
+    def step(k):
+        for f in pending:
+            f.Await()
+        pending.clear()
+        ids, free = batch()
+        pending.append(mgr.d2h(ids, slots[k % 2]))
+        pending.append(mgr.h2d(slots[(k + 1) % 2], free))
+
+    def drain():
+        for f in pending:
+            f.Await()
+        pending.clear()
+        mgr.wait_for_pending_work()
+        torch.cuda.synchronize()
+
+    for k in range(warmup):
+        step(k)
+    drain()
+    mgr.kernel_times(True, reset=True)
+    mgr.kernel_times(False, reset=True)
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(warmup + k)
+    drain()
+    return time.perf_counter() - t0
+
+
+def one_direction(mgr, batch, slots, reps):
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        mgr.d2h(batch()[0], slots[0]).Await()
+    t_off = (time.perf_counter() - t0) / reps
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        mgr.h2d(slots[0], batch()[1]).Await()
+    t_rel = (time.perf_counter() - t0) / reps
+    return t_off, t_rel
+
+
 def main():
     args = parse_args()
     if args.rocpd_summary:
@@ -215,10 +265,15 @@ def main():
     pools = [torch.randint(-2**31, 2**31 - 1, (P, bb // 4), dtype=torch.int32, device=dev,
                            generator=gen).view(torch.uint8) for _ in range(S)]
     torch.cuda.synchronize()
-    mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=2 * n,
-                             staging_chunk_bytes=args.chunk_mib << 20,
-                             staging_chunks=args.chunks, profile_kernels=True)
-    log("manager ready")
+
+    def make_mgr(mode):
+        return pkg.KVCacheManager(pools, host_blocks_to_allocate=2 * n,
+                                  staging_chunk_bytes=args.chunk_mib << 20,
+                                  staging_chunks=args.chunks, profile_kernels=True,
+                                  transfer_mode=mode)
+
+    mgr = make_mgr(args.mode)
+    log(f"manager ready (mode {args.mode})")
     rng = np.random.default_rng(0)
     slots = [list(range(0, n)), list(range(n, 2 * n))]
 
@@ -226,61 +281,34 @@ def main():
         perm = rng.permutation(P)
         return perm[:n].tolist(), perm[n:2 * n].tolist()
 
-    # Prime slot 1 so the first reload reads offloaded data.
-    mgr.d2h(batch()[0], slots[1]).Await()
-    pending = []
-
-    def step(k):
-        for f in pending:
-            f.Await()
-        pending.clear()
-        ids, free = batch()
-        pending.append(mgr.d2h(ids, slots[k % 2]))
-        pending.append(mgr.h2d(slots[(k + 1) % 2], free))
-
-    for k in range(args.warmup):
-        step(k)
-    for f in pending:
-        f.Await()
-    pending.clear()
-    mgr.wait_for_pending_work()
-    torch.cuda.synchronize()
-    mgr.kernel_times(True, reset=True)
-    mgr.kernel_times(False, reset=True)
-    log(f"timing {args.steps} steps")
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        step(args.warmup + k)
-    for f in pending:
-        f.Await()
-    pending.clear()
-    mgr.wait_for_pending_work()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
     step_bytes = 2 * n * S * bb
+    log(f"timing {args.steps} offload+reload steps")
+    elapsed = run_duplex(torch, mgr, batch, slots, args.steps, args.warmup)
     value = args.steps * step_bytes / elapsed / 1e9
+    stats = mgr.engine_stats()
+    log(f"offload+reload: {value:.2f} GB/s, {elapsed / args.steps * 1e3:.2f} ms/step "
+        f"({stats})")
     kg = mgr.kernel_times(True, reset=True)
     ks = mgr.kernel_times(False, reset=True)
-    log(f"offload+reload: {value:.2f} GB/s, {elapsed / args.steps * 1e3:.2f} ms/step")
 
-    def pipeline_kernel(kt, name):
+    def loop_kernel(kt, name):
         if kt["launches"] == 0:
             return None
         avg_s = kt["total_ms"] / kt["launches"] / 1e3
         per_launch = kt["bytes"] / kt["launches"]
-        return {"kernel": f"block_copy_kernel ({name}) per staging chunk in the pipeline",
+        return {"kernel": f"block_copy_kernel ({name}) inside the offload/reload loop",
                 "achieved_gbps": round(per_launch / avg_s / 1e9, 1),
                 "launches": kt["launches"], "avg_launch_us": round(avg_s * 1e6, 2),
                 "bytes_per_launch": int(per_launch)}
 
-    pipe_gather = pipeline_kernel(kg, "gather")
-    pipe_scatter = pipeline_kernel(ks, "scatter")
+    loop_gather = loop_kernel(kg, "gather")
+    loop_scatter = loop_kernel(ks, "scatter")
 
     # The gather/scatter kernels alone: one launch moves the whole batch
     # (n blocks x S storages, 2 * n * S * B algorithmic HBM bytes) between the
-    # pool and a device staging buffer, on a stream of its own, timed with
-    # HIP events on that stream. Inside the offload pipeline the same kernel
-    # shares the CUs with the runtime's D2H blit kernels, so its pipeline
+    # pool and a device staging buffer, on a stream of its own. Inside the
+    # offload loop the same kernel shares the GPU with PCIe traffic (D2H blit
+    # kernels in staged mode; the zero-copy kernels are PCIe-bound), so those
     # launches are reported separately.
     log("timing the gather/scatter kernels alone")
     staging = torch.empty(n * S * bb, dtype=torch.uint8, device=dev)
@@ -319,34 +347,39 @@ def main():
     del staging, copy_dst
     mgr.kernel_times(True, reset=True)
     mgr.kernel_times(False, reset=True)
-    roof = iso["gather"]
-    scatter_roof = iso["scatter"]
 
     extras = {}
     if not args.no_extras:
+        half = n * S * bb
         reps = max(3, args.steps // 2)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            mgr.d2h(batch()[0], slots[0]).Await()
-        t_off = (time.perf_counter() - t0) / reps
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            mgr.h2d(slots[0], batch()[1]).Await()
-        t_rel = (time.perf_counter() - t0) / reps
-        mgr.kernel_times(True, reset=True)
-        mgr.kernel_times(False, reset=True)
+        modes = {}
+        for mode in ("zero_copy", "staged"):
+            m = mgr if mode == args.mode else make_mgr(mode)
+            t_off, t_rel = one_direction(m, batch, slots, reps)
+            el = elapsed if m is mgr else run_duplex(torch, m, batch, slots, args.steps,
+                                                      args.warmup)
+            modes[mode] = {"duplex_gbps": round(args.steps * step_bytes / el / 1e9, 2),
+                           "offload_gbps": round(half / t_off / 1e9, 2),
+                           "reload_gbps": round(half / t_rel / 1e9, 2)}
+            log(f"{mode}: {modes[mode]}")
+            if m is not mgr:
+                m.close()
         log("measuring pinned PCIe peaks")
         peaks = pcie_peaks(torch, dev)
-        half = n * S * bb
+        head_mode = "zero_copy" if args.mode == "auto" else args.mode
+        for mode, r in modes.items():
+            r["offload_frac_of_pcie_d2h"] = round(r["offload_gbps"] / peaks["pcie_d2h_gbps"], 4)
+            r["reload_frac_of_pcie_h2d"] = round(r["reload_gbps"] / peaks["pcie_h2d_gbps"], 4)
+            r["duplex_frac_of_pcie_bidir"] = round(r["duplex_gbps"] / peaks["pcie_bidir_gbps"], 4)
         extras = {
-            "offload_gbps": round(half / t_off / 1e9, 2),
-            "reload_gbps": round(half / t_rel / 1e9, 2),
+            "offload_gbps": modes[head_mode]["offload_gbps"],
+            "reload_gbps": modes[head_mode]["reload_gbps"],
+            "offload_frac_of_pcie_d2h": modes[head_mode]["offload_frac_of_pcie_d2h"],
+            "reload_frac_of_pcie_h2d": modes[head_mode]["reload_frac_of_pcie_h2d"],
+            "duplex_frac_of_pcie_bidir": round(value / peaks["pcie_bidir_gbps"], 4),
             **{k: round(v, 2) for k, v in peaks.items()},
+            "modes": modes,
         }
-        extras["offload_frac_of_pcie_d2h"] = round(extras["offload_gbps"] / peaks["pcie_d2h_gbps"], 4)
-        extras["reload_frac_of_pcie_h2d"] = round(extras["reload_gbps"] / peaks["pcie_h2d_gbps"], 4)
-        extras["duplex_frac_of_pcie_bidir"] = round(value / peaks["pcie_bidir_gbps"], 4)
     mgr.close()
     del pools
     torch.cuda.empty_cache()
@@ -374,15 +407,15 @@ def main():
             "layers": L, "kv_heads": w["kv_heads"], "head_dim": w["head_dim"],
             "block_tokens": w["block_tokens"], "kv_dtype": w["dtype"], "storages": S,
             "block_bytes": bb, "pool_blocks": P, "batch_blocks": n,
-            "staging_chunk_mib": args.chunk_mib,
+            "transfer_mode": args.mode, "staging_chunk_mib": args.chunk_mib,
         },
         "blocks_per_s": round(args.steps * 2 * n / elapsed, 1),
-        "roofline": roof,
-        "scatter_roofline": scatter_roof,
-        "pipeline_gather": pipe_gather,
-        "pipeline_scatter": pipe_scatter,
+        "roofline": iso["gather"],
+        "scatter_roofline": iso["scatter"],
+        "loop_gather": loop_gather,
+        "loop_scatter": loop_scatter,
         "hbm_copy_same_bytes_gbps": round(hbm_copy_gbps, 1),
-        "gather_frac_of_measured_copy": round(roof["achieved"] / hbm_copy_gbps, 4),
+        "gather_frac_of_measured_copy": round(iso["gather"]["achieved"] / hbm_copy_gbps, 4),
         "cpu_baseline": cpu,
         **extras,
     }

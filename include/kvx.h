@@ -54,6 +54,19 @@ extern "C" {
 #define KVX_HOST_PINNED 1 /* hipHostMalloc page-locked, zeroed */
 #define KVX_HOST_SHM 2    /* /dev/shm segment, survives the process */
 
+/* Transfer modes for copies whose runs are short (runs of at least
+ * direct_min_bytes always use one hipMemcpyAsync per run):
+ *   KVX_MODE_STAGED: gather kernel -> device staging ring -> hipMemcpyAsync
+ *     (and H2D -> scatter for reload), pipelined chunk by chunk;
+ *   KVX_MODE_ZERO_COPY: one kernel moves the blocks between the pool and the
+ *     pinned host mirror directly over PCIe (needs KVX_HOST_PINNED);
+ *   KVX_MODE_AUTO: staged when the host ids of a copy form long runs (an
+ *     average of 32 blocks or more) or the mirror is not pinned, zero-copy
+ *     for fragmented host ids. */
+#define KVX_MODE_AUTO 0
+#define KVX_MODE_STAGED 1
+#define KVX_MODE_ZERO_COPY 2
+
 /* Staging orders for kvx_manager_gather / kvx_manager_scatter. */
 #define KVX_LAYER_MAJOR 0 /* [storage][n][block_bytes] */
 #define KVX_BLOCK_MAJOR 1 /* [n][storage][block_bytes] */
@@ -93,7 +106,9 @@ typedef struct kvx_manager_config {
   const char* shm_server_name;  /* KVX_HOST_SHM: optional server name */
   const char* model_uid;        /* KVX_HOST_SHM: schema check on warm boot */
   int32_t profile_kernels;      /* 1: time every kernel launch with HIP events */
-  int32_t reserved;
+  int32_t transfer_mode;        /* KVX_MODE_*: how short runs cross PCIe */
+  int64_t zero_copy_workgroups; /* workgroup cap of a zero-copy launch in both
+                                   directions; 0 = 16 for D2H, 64 for H2D */
 } kvx_manager_config;
 
 int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out);
@@ -188,9 +203,10 @@ int64_t kvx_manager_block_array_host_size(kvx_manager* m, int64_t block_array_id
 int64_t kvx_manager_allocated_host_bytes(const kvx_manager* m);
 /* Blocks until every copy the manager issued has finished. */
 int kvx_manager_wait_for_pending_work(kvx_manager* m);
-/* Counters of what the transfer engine issued: out[0..4] = direct copies,
- * staged copies, hipMemcpyAsync calls, kernel launches, staging chunks. */
-int kvx_manager_engine_stats(kvx_manager* m, int64_t* out5);
+/* Counters of what the transfer engine issued: out[0..5] = direct copies,
+ * staged copies, hipMemcpyAsync calls, kernel launches, staging chunks,
+ * zero-copy copies. */
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out6);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the
  * gather (gather = 1) or scatter (gather = 0) kernels so far. Waits for the

@@ -93,11 +93,14 @@ def random_spec(rng, blocks, host_blocks, max_entries=8, max_run=3):
 
 PATHS = {
     "direct": dict(direct_min_bytes=1),
-    "staged": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2),
+    "staged": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                   transfer_mode="staged"),
+    "zero_copy": dict(direct_min_bytes=1 << 40, transfer_mode="zero_copy"),
 }
+MODES = ["staged", "zero_copy"]
 
 
-@pytest.mark.parametrize("path", ["direct", "staged"])
+@pytest.mark.parametrize("path", ["direct", "staged", "zero_copy"])
 @pytest.mark.parametrize("bb", [32768, 1024, 48, 36, 3])
 def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
     rng = np.random.default_rng(bb * 7 + len(path))
@@ -123,19 +126,23 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
     if path == "staged":
         assert stats["direct_copies"] == 0 and stats["staged_copies"] == 12
         assert stats["chunks"] > 12 or bb < 1024
+    elif path == "zero_copy":
+        assert stats["zero_copy_copies"] == 12 and stats["memcpy_calls"] == 0
     else:
-        assert stats["staged_copies"] == 0
+        assert stats["staged_copies"] == 0 and stats["zero_copy_copies"] == 0
     mgr.close()
 
 
-def test_scattered_ids_match_oracle_many_chunks(kvx, cuda):
-    """512 random single-block ids over 8 storages through a 2-chunk ring of
-    256 KiB: exercises duplicate-free host runs, chunk boundaries inside a
-    storage and ring reuse across calls."""
+@pytest.mark.parametrize("mode", MODES)
+def test_scattered_ids_match_oracle_many_chunks(kvx, cuda, mode):
+    """512 random single-block ids over 8 storages (staged: through a 2-chunk
+    ring of 256 KiB, so chunk boundaries fall inside a storage and the ring is
+    reused across calls; zero-copy: one kernel per call)."""
     rng = np.random.default_rng(21)
     layers, blocks, hb, bb = 8, 1024, 600, 4096
     host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
-    mgr = make_mgr(kvx, dev, hb, staging_chunk_bytes=256 << 10, staging_chunks=2)
+    mgr = make_mgr(kvx, dev, hb, staging_chunk_bytes=256 << 10, staging_chunks=2,
+                   transfer_mode=mode)
     mir = Mirror(host, hb)
     for rep in range(3):
         ids = rng.choice(blocks, size=512, replace=False).tolist()
@@ -151,10 +158,11 @@ def test_scattered_ids_match_oracle_many_chunks(kvx, cuda):
     mgr.close()
 
 
-def test_duplicate_destinations_last_wins(kvx, cuda):
+@pytest.mark.parametrize("mode", MODES)
+def test_duplicate_destinations_last_wins(kvx, cuda, mode):
     rng = np.random.default_rng(3)
     host, dev = dev_pools(rng, cuda, 2, 1, 16, 256)
-    mgr = make_mgr(kvx, dev, 8, direct_min_bytes=1 << 40)
+    mgr = make_mgr(kvx, dev, 8, direct_min_bytes=1 << 40, transfer_mode=mode)
     # Two device blocks to host block 5: the later entry wins, as when the
     # copies are issued in order.
     mgr.d2h([1, 9], [5, 5], [1, 1]).Await()
@@ -173,13 +181,14 @@ def test_reference_known_answers_dtypes(kvx, cuda, golden):
     fp32 and int32 byte widths, on both copy paths."""
     elems = 128 * 8 * 8 * 128
     for itemsize, dtype in [(1, "fp8"), (2, "bf16"), (4, "fp32"), (4, "int32")]:
-        for path in ("direct", "staged"):
+        for path in ("direct", "staged", "zero_copy"):
             for case in golden["transfer_cases"]:
                 L, P, H = case["layers"], case["blocks"], case["host_blocks"]
                 rng = np.random.default_rng(101)
                 host, dev = dev_pools(rng, cuda, L, 1, P, elems * itemsize)
-                mgr = make_mgr(kvx, dev, H, **(PATHS[path] if path == "direct" else
-                                               dict(direct_min_bytes=1 << 40)))
+                mgr = make_mgr(kvx, dev, H, **(PATHS[path] if path != "staged" else
+                                               dict(direct_min_bytes=1 << 40,
+                                                    transfer_mode="staged")))
                 print(f"{dtype} {path} {case['source']}", flush=True)
                 for op in case["ops"]:
                     if op["op"] == "d2h_auto_allocate":
@@ -336,9 +345,8 @@ def test_nan_denormal_bit_patterns_preserved(kvx, cuda):
                              size=int(nanmask.sum()))
     pools_np = [raw, bf.view(np.uint8).reshape(P, bb)]
     pools = [torch.from_numpy(p).to(cuda) for p in pools_np]
-    for path in ("direct", "staged"):
-        mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=P,
-                                 **(dict(direct_min_bytes=1 << 40) if path == "staged" else {}))
+    for path in ("staged", "zero_copy"):
+        mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=P, transfer_mode=path)
         ids = rng.permutation(P).tolist()
         mgr.d2h(ids, list(range(P))).Await()
         back = rng.permutation(P).tolist()
@@ -464,7 +472,8 @@ def test_concurrent_disjoint_blocks(kvx, cuda):
     mgr.close()
 
 
-def test_llama3_8b_pool_full_size_round_trip(kvx, cuda):
+@pytest.mark.parametrize("mode", MODES)
+def test_llama3_8b_pool_full_size_round_trip(kvx, cuda, mode):
     """32 layers x (K, V) x 16384 blocks x 16 tokens x 8 heads x 128 dim bf16
     (32 GiB pool): offload 512 random blocks to pinned host, reload into 512
     random free slots; bit-exact through size-independent checks (every
@@ -488,8 +497,8 @@ def test_llama3_8b_pool_full_size_round_trip(kvx, cuda):
         return p.view(torch.int32)[keep].to(torch.int64).sum()
 
     sums = [checksum(p) for p in pools]
-    mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=n)
-    print("offload 512 blocks x 64 storages", flush=True)
+    mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=n, transfer_mode=mode)
+    print(f"{mode}: offload 512 blocks x 64 storages", flush=True)
     mgr.d2h(ids.tolist(), list(range(n))).Await()
     print("reload into 512 free slots", flush=True)
     mgr.h2d(list(range(n)), free.tolist()).Await()
@@ -497,5 +506,40 @@ def test_llama3_8b_pool_full_size_round_trip(kvx, cuda):
         assert torch.equal(pools[s].index_select(0, free_t), orig[s]), s
         assert int(checksum(pools[s]).item()) == int(sums[s].item()), s
     stats = mgr.engine_stats()
-    assert stats["staged_copies"] == 2 and stats["kernel_launches"] >= 2
+    key = "staged_copies" if mode == "staged" else "zero_copy_copies"
+    assert stats[key] == 2 and stats["kernel_launches"] >= 2
+    mgr.close()
+
+
+def test_zero_copy_needs_pinned_host(kvx, cuda):
+    t = torch.zeros(4, 256, dtype=torch.uint8, device=cuda)
+    with pytest.raises(kvx.KvxError) as e:
+        kvx.KVCacheManager([t], host_blocks_to_allocate=4, host_alloc="malloc",
+                           transfer_mode="zero_copy")
+    assert e.value.code == 3
+    # A pageable mirror falls back to the staged path in auto mode.
+    mgr = kvx.KVCacheManager([t], host_blocks_to_allocate=4, host_alloc="malloc")
+    t[1].fill_(7)
+    mgr.d2h([1], [2]).Await()
+    assert (mgr.host_view(0).reshape(4, 256)[2] == 7).all()
+    assert mgr.engine_stats()["staged_copies"] == 1
+    mgr.close()
+
+
+def test_auto_mode_picks_by_host_fragmentation(kvx, cuda):
+    """Auto mode stages copies whose host ids form long runs and moves
+    fragmented ones with the zero-copy kernel; both are bit-exact."""
+    rng = np.random.default_rng(31)
+    host, dev = dev_pools(rng, cuda, 2, 1, 256, 4096)
+    mgr = make_mgr(kvx, dev, 256)
+    ids = rng.choice(256, size=64, replace=False).tolist()
+    mgr.d2h(ids, list(range(64))).Await()
+    assert mgr.engine_stats()["staged_copies"] == 1
+    hids = (64 + rng.choice(192, size=64, replace=False)).tolist()  # clear of 0..63
+    mgr.d2h(ids, hids).Await()
+    assert mgr.engine_stats()["zero_copy_copies"] == 1
+    for l in range(2):
+        hv = mgr.host_view(l).reshape(256, 4096)
+        assert np.array_equal(hv[:64], host[l][0][ids])
+        assert np.array_equal(hv[hids], host[l][0][ids])
     mgr.close()

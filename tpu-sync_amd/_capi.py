@@ -20,6 +20,7 @@ STATUS_NAMES = {
 }
 
 HOST_MALLOC, HOST_PINNED, HOST_SHM = 0, 1, 2
+MODES = {"auto": 0, "staged": 1, "zero_copy": 2}
 LAYER_MAJOR, BLOCK_MAJOR = 0, 1
 
 
@@ -51,7 +52,8 @@ class ManagerConfig(ctypes.Structure):
         ("shm_server_name", ctypes.c_char_p),
         ("model_uid", ctypes.c_char_p),
         ("profile_kernels", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("transfer_mode", ctypes.c_int32),
+        ("zero_copy_workgroups", ctypes.c_int64),
     ]
 
 

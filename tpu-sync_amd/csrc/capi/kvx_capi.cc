@@ -121,6 +121,17 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   if (cfg->staging_chunks > 0) c.engine.staging_chunks = static_cast<int>(cfg->staging_chunks);
   if (cfg->direct_min_bytes > 0) c.engine.direct_min_bytes = cfg->direct_min_bytes;
   c.engine.profile_kernels = cfg->profile_kernels != 0;
+  if (cfg->transfer_mode < KVX_MODE_AUTO || cfg->transfer_mode > KVX_MODE_ZERO_COPY) {
+    return Fail(KVX_INVALID_ARGUMENT, "unknown transfer_mode");
+  }
+  if (cfg->transfer_mode == KVX_MODE_ZERO_COPY && cfg->host_alloc != KVX_HOST_PINNED) {
+    return Fail(KVX_INVALID_ARGUMENT, "zero-copy transfers need KVX_HOST_PINNED host memory");
+  }
+  c.engine.mode = static_cast<kvx::TransferMode>(cfg->transfer_mode);
+  if (cfg->zero_copy_workgroups > 0) {
+    c.engine.zero_copy_d2h_workgroups = cfg->zero_copy_workgroups;
+    c.engine.zero_copy_h2d_workgroups = cfg->zero_copy_workgroups;
+  }
   auto r = kvx::KVCacheManager::Create(std::move(c));
   if (!r.ok()) return Fail(r.status());
   auto* m = new kvx_manager;
@@ -342,17 +353,18 @@ int kvx_manager_wait_for_pending_work(kvx_manager* m) {
   if (m == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager");
   return Done(m->impl->WaitForPendingWork());
 }
-int kvx_manager_engine_stats(kvx_manager* m, int64_t* out5) {
-  if (m == nullptr || out5 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out6) {
+  if (m == nullptr || out6 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
   if (m->impl->engine() == nullptr) {
     return Fail(KVX_FAILED_PRECONDITION, "CPU-only manager has no transfer engine");
   }
   kvx::EngineStats s = m->impl->engine()->stats();
-  out5[0] = s.direct_copies;
-  out5[1] = s.staged_copies;
-  out5[2] = s.memcpy_calls;
-  out5[3] = s.kernel_launches;
-  out5[4] = s.chunks;
+  out6[0] = s.direct_copies;
+  out6[1] = s.staged_copies;
+  out6[2] = s.memcpy_calls;
+  out6[3] = s.kernel_launches;
+  out6[4] = s.chunks;
+  out6[5] = s.zero_copy_copies;
   return KVX_OK;
 }
 

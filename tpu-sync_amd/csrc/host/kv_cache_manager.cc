@@ -126,13 +126,16 @@ Status KVCacheManager::Init() {
 
   lbm_ = std::make_unique<LogicalBlockManager>(static_cast<int>(host_blocks_));
 
-  int64_t alloc_size = 0;
-  if (!RangeFits(host_blocks_, slice_byte_size_, 0,
-                 std::numeric_limits<int64_t>::max())) {
-    return InvalidArgumentError("host mirror size overflows");
-  }
-  alloc_size = host_blocks_ * slice_byte_size_;
   for (size_t k = 0; k < nstor; ++k) {
+    // Each (layer, shard) mirror holds host_blocks blocks of that layer's own
+    // block size. The reference sizes every mirror by the first layer's
+    // block; per-layer sizing is the same for uniform models and lets side
+    // tables with small blocks (fp8 scales) keep small mirrors.
+    const int64_t layer_bb = layer_block_bytes_[k / num_shards_];
+    if (!RangeFits(host_blocks_, layer_bb, 0, std::numeric_limits<int64_t>::max())) {
+      return InvalidArgumentError("host mirror size overflows");
+    }
+    const int64_t alloc_size = host_blocks_ * layer_bb;
     StatusOr<HostBufferAllocation> a = Status();
     switch (cfg_.host_alloc) {
       case HostAllocKind::kMalloc:
@@ -160,6 +163,9 @@ Status KVCacheManager::Init() {
     EngineOptions eo = cfg_.engine;
     eo.device = cfg_.device;
     KVX_ASSIGN_OR_RETURN(engine_, TransferEngine::Create(eo));
+    // hipHostMalloc memory is mapped into the GPU's address space, so the
+    // copy kernels may read and write the mirror directly.
+    host_kernel_access_ = cfg_.host_alloc == HostAllocKind::kPinned;
   }
   return OkStatus();
 }
@@ -265,7 +271,8 @@ StatusOr<CopyFuture> KVCacheManager::Transfer(
         }
       }
     }
-    views.push_back(StorageView{si.dev, si.dev_bytes, host, host_size, B});
+    views.push_back(StorageView{si.dev, si.dev_bytes, host, host_size, B,
+                                host_kernel_access_});
   }
   if (!is_partial) return engine_->CopyFull(dir, views, full_bytes, dep);
   return engine_->Copy(dir, views, src_c, dst_c, sizes_c, dep);

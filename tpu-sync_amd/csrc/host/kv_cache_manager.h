@@ -186,6 +186,7 @@ class KVCacheManager {
   std::vector<int64_t> layer_physical_bytes_;
   std::vector<StorageInfo> storages_;
   size_t allocated_host_bytes_ = 0;
+  bool host_kernel_access_ = false;
   int64_t staging_num_slots_ = 0;
   int64_t staging_max_major_per_slot_ = 0;
   std::unique_ptr<LogicalBlockManager> lbm_;

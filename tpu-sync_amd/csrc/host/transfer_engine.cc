@@ -269,7 +269,30 @@ StatusOr<CopyFuture> TransferEngine::Copy(
   if (min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) {
     return CopyDirect(dir, storages, src, dst, sizes, dep);
   }
-  return CopyStaged(dir, storages, src, dst, sizes, dep);
+  bool host_ok = true;
+  for (const StorageView& s : storages) host_ok = host_ok && s.host_kernel_access;
+  std::vector<int64_t> cdev, chost;
+  KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
+  bool zero_copy = opts_.mode == TransferMode::kZeroCopy;
+  if (opts_.mode == TransferMode::kAuto && host_ok) {
+    // The staged path costs one hipMemcpyAsync per (storage, host run) and
+    // lets SDMA carry H2D next to a D2H in flight; the zero-copy kernel costs
+    // the same for any host layout. Fragmented host ids (short runs) go
+    // zero-copy.
+    int64_t runs = 0;
+    for (size_t i = 0; i < chost.size(); ++i) {
+      if (i == 0 || chost[i] != chost[i - 1] + 1) ++runs;
+    }
+    zero_copy = static_cast<int64_t>(chost.size()) < opts_.auto_staged_min_run * runs;
+  }
+  if (zero_copy) {
+    if (!host_ok) {
+      return FailedPreconditionError(
+          "zero-copy transfers need a pinned host mirror the GPU can access");
+    }
+    return CopyZeroCopy(dir, storages, cdev, chost, dep);
+  }
+  return CopyStaged(dir, storages, cdev, chost, dep);
 }
 
 StatusOr<CopyFuture> TransferEngine::CopyDirect(
@@ -330,12 +353,13 @@ StatusOr<CopyFuture> TransferEngine::CopyFull(
   return CopyFuture::FromEvents({done}, {});
 }
 
-StatusOr<CopyFuture> TransferEngine::CopyStaged(
-    Direction dir, const std::vector<StorageView>& storages,
-    const std::vector<int64_t>& src, const std::vector<int64_t>& dst,
-    const std::vector<int64_t>& sizes, hipStream_t dep) {
+Status TransferEngine::PlanPairs(Direction dir, const std::vector<int64_t>& src,
+                                 const std::vector<int64_t>& dst,
+                                 const std::vector<int64_t>& sizes,
+                                 std::vector<int64_t>* dev_ids,
+                                 std::vector<int64_t>* host_ids) {
   const bool d2h = dir == Direction::kD2H;
-  // 1. Expand runs into (device id, host id) pairs.
+  // Expand runs into (device id, host id) pairs.
   int64_t N = 0;
   for (int64_t s : sizes) N += s;
   std::vector<int64_t> dev_id(N), host_id(N);
@@ -348,8 +372,8 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
       }
     }
   }
-  // 2. One writer per destination block: the last pair naming it wins, as
-  // when the copies are issued in order.
+  // One writer per destination block: the last pair naming it wins, as when
+  // the copies are issued in order.
   const std::vector<int64_t>& dest = d2h ? host_id : dev_id;
   std::vector<int64_t> order(N);
   std::iota(order.begin(), order.end(), 0);
@@ -361,18 +385,103 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
     if (k + 1 < N && dest[order[k + 1]] == dest[order[k]]) continue;
     kept.push_back(order[k]);
   }
-  // 3. Compact order: by host id, so every host run is contiguous in staging.
+  // Compact order: by host id, so every host run is contiguous in staging.
   if (!d2h) {
     std::stable_sort(kept.begin(), kept.end(), [&](int64_t a, int64_t b) {
       return host_id[a] < host_id[b];
     });
   }
   const int64_t n = static_cast<int64_t>(kept.size());
-  std::vector<int64_t> cdev(n), chost(n);
+  if (n > INT32_MAX) return InvalidArgumentError("too many blocks in one copy");
+  dev_ids->resize(n);
+  host_ids->resize(n);
   for (int64_t i = 0; i < n; ++i) {
-    cdev[i] = dev_id[kept[i]];
-    chost[i] = host_id[kept[i]];
+    (*dev_ids)[i] = dev_id[kept[i]];
+    (*host_ids)[i] = host_id[kept[i]];
   }
+  return OkStatus();
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyZeroCopy(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& cdev, const std::vector<int64_t>& chost,
+    hipStream_t dep) {
+  const bool d2h = dir == Direction::kD2H;
+  const int64_t n = static_cast<int64_t>(cdev.size());
+  std::vector<Group> groups = MakeGroups(storages);
+  for (const Group& gr : groups) {
+    if (static_cast<int64_t>(gr.members.size()) * n > UINT32_MAX) {
+      return InvalidArgumentError("copy too large for one launch");
+    }
+  }
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard dg(opts_.device);
+  hipStream_t ks = d2h ? gather_stream_ : scatter_stream_;
+  // Arguments: device ids, host ids, then a device and a host base-address
+  // table per group.
+  int64_t arg_bytes = 2 * AlignUp(n * 8, kArgAlign);
+  std::vector<int64_t> dev_tab(groups.size()), host_tab(groups.size());
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const int64_t tb = AlignUp(static_cast<int64_t>(groups[gi].members.size()) * 8, kArgAlign);
+    dev_tab[gi] = arg_bytes;
+    host_tab[gi] = arg_bytes + tb;
+    arg_bytes += 2 * tb;
+  }
+  KVX_ASSIGN_OR_RETURN(int64_t aoff, ArgAlloc(arg_bytes));
+  const int64_t ids2_off = AlignUp(n * 8, kArgAlign);
+  std::memcpy(arg_host_ + aoff, cdev.data(), n * 8);
+  std::memcpy(arg_host_ + aoff + ids2_off, chost.data(), n * 8);
+  uint64_t acc = 0;
+  std::vector<int64_t> other_blocks(groups.size(), INT64_MAX);
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    uint64_t* dt = reinterpret_cast<uint64_t*>(arg_host_ + aoff + dev_tab[gi]);
+    uint64_t* ht = reinterpret_cast<uint64_t*>(arg_host_ + aoff + host_tab[gi]);
+    for (size_t m = 0; m < groups[gi].members.size(); ++m) {
+      const StorageView& sv = storages[groups[gi].members[m]];
+      dt[m] = sv.dev;
+      ht[m] = reinterpret_cast<uint64_t>(sv.host);
+      acc |= dt[m] | ht[m];
+      other_blocks[gi] = std::min(other_blocks[gi], sv.host_bytes / sv.block_bytes);
+    }
+  }
+  KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(arg_dev_ + aoff),
+                                         arg_host_ + aoff, arg_bytes,
+                                         hipMemcpyHostToDevice, ks));
+  KVX_RETURN_IF_ERROR(WaitDep(dep, ks));
+  for (size_t g0 = 0; g0 < groups.size(); g0 += kMaxPieces) {
+    CopyLaunch cl;
+    cl.ids = reinterpret_cast<const int64_t*>(arg_dev_ + aoff);
+    cl.ids2 = reinterpret_cast<const int64_t*>(arg_dev_ + aoff + ids2_off);
+    cl.n = n;
+    cl.max_workgroups = d2h ? opts_.zero_copy_d2h_workgroups
+                            : opts_.zero_copy_h2d_workgroups;
+    for (size_t gi = g0; gi < groups.size() && gi < g0 + kMaxPieces; ++gi) {
+      const Group& gr = groups[gi];
+      CopyPiece& c = cl.pieces[cl.npieces++];
+      c.storages = arg_dev_ + aoff + dev_tab[gi];
+      c.others = arg_dev_ + aoff + host_tab[gi];
+      c.other_blocks = other_blocks[gi];
+      c.f0 = 0;
+      c.nblocks = static_cast<int64_t>(gr.members.size()) * n;
+      c.block_bytes = gr.block_bytes;
+      c.pool_blocks = gr.pool_blocks;
+    }
+    const int vec = LaunchVectorBytes(cl, acc);
+    KVX_RETURN_IF_ERROR(LaunchCopy(cl, d2h, vec, ks));
+  }
+  KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, ks));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, ks));
+  ++stats_.zero_copy_copies;
+  return CopyFuture::FromEvents({done}, {});
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyStaged(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& cdev, const std::vector<int64_t>& chost,
+    hipStream_t dep) {
+  const bool d2h = dir == Direction::kD2H;
+  const int64_t n = static_cast<int64_t>(cdev.size());
   std::vector<HostRun> runs;
   for (int64_t i = 0; i < n;) {
     int64_t e = i + 1;

@@ -41,9 +41,24 @@ struct StorageView {
   uint8_t* host = nullptr;
   int64_t host_bytes = 0;
   int64_t block_bytes = 0;
+  // The host region is page-locked and mapped into the GPU's address space
+  // (hipHostMalloc), so kernels may read and write it directly.
+  bool host_kernel_access = false;
 };
 
 enum class Direction : int { kD2H = 0, kH2D = 1 };
+
+// How a block copy with short runs crosses PCIe.
+//   kStaged: gather kernel -> device staging ring -> hipMemcpyAsync (and the
+//            mirror image for reload), pipelined chunk by chunk;
+//   kZeroCopy: one kernel moves every block between the pool and the pinned
+//            host mirror directly (GPU loads/stores over PCIe), no staging;
+//   kAuto: staged when the host ids form long runs (average at least
+//          auto_staged_min_run blocks) or the host memory is not mapped for
+//          the GPU; zero-copy for fragmented host ids.
+// Copies whose runs are all at least direct_min_bytes use one
+// hipMemcpyAsync per (storage, run) in every mode.
+enum class TransferMode : int { kAuto = 0, kStaged = 1, kZeroCopy = 2 };
 
 struct EngineOptions {
   int device = 0;
@@ -55,6 +70,15 @@ struct EngineOptions {
   int64_t direct_min_bytes = 4ll << 20;
   // Bracket every kernel launch with timing events on its stream.
   bool profile_kernels = false;
+  TransferMode mode = TransferMode::kAuto;
+  // Workgroup caps of a zero-copy launch. A few dozen workgroups keep enough
+  // 16-byte accesses in flight to fill the PCIe link in either direction;
+  // more D2H writers crowd out the reads of a reload running at the same
+  // time (measured on MI355X: 16 writers / 64 readers).
+  int64_t zero_copy_d2h_workgroups = 16;
+  int64_t zero_copy_h2d_workgroups = 64;
+  // kAuto stages a copy whose host runs average at least this many blocks.
+  int64_t auto_staged_min_run = 32;
 };
 
 // Accumulated duration of the profiled launches of one kernel direction.
@@ -71,6 +95,7 @@ struct EngineStats {
   int64_t memcpy_calls = 0;
   int64_t kernel_launches = 0;
   int64_t chunks = 0;
+  int64_t zero_copy_copies = 0;
 };
 
 class TransferEngine {
@@ -153,12 +178,24 @@ class TransferEngine {
                                   const std::vector<int64_t>& dst,
                                   const std::vector<int64_t>& sizes,
                                   hipStream_t dep);
+  // cdev / chost: compact (device id, host id) pairs from PlanPairs.
   StatusOr<CopyFuture> CopyStaged(Direction dir,
                                   const std::vector<StorageView>& storages,
-                                  const std::vector<int64_t>& src,
-                                  const std::vector<int64_t>& dst,
-                                  const std::vector<int64_t>& sizes,
+                                  const std::vector<int64_t>& cdev,
+                                  const std::vector<int64_t>& chost,
                                   hipStream_t dep);
+  StatusOr<CopyFuture> CopyZeroCopy(Direction dir,
+                                    const std::vector<StorageView>& storages,
+                                    const std::vector<int64_t>& cdev,
+                                    const std::vector<int64_t>& chost,
+                                    hipStream_t dep);
+  // Expands runs to (device id, host id) pairs, keeps the last pair naming
+  // each destination block and orders them by host id.
+  static Status PlanPairs(Direction dir, const std::vector<int64_t>& src,
+                          const std::vector<int64_t>& dst,
+                          const std::vector<int64_t>& sizes,
+                          std::vector<int64_t>* dev_ids,
+                          std::vector<int64_t>* host_ids);
   StatusOr<hipEvent_t> NewEvent();
   // Launches one block-copy kernel, bracketed by timing events when
   // profiling is on.

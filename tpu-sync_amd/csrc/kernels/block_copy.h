@@ -26,26 +26,39 @@ constexpr int kMaxPieces = 4;
 struct CopyPiece {
   // Device address of a table of uint64 storage base addresses, indexed by w.
   uint64_t storages = 0;
-  // Address of block (w, i) in staging: staging + w * stride_w + i * stride_i.
-  // Computed in wrapping uint64 arithmetic, so a piece that starts at f0 > 0
-  // may pass a base that lies before its buffer.
+  // Address of block (w, i) on the other side of the copy. When `others` is
+  // 0 it is staging + w * stride_w + i * stride_i (a contiguous staging
+  // buffer), computed in wrapping uint64 arithmetic, so a piece that starts
+  // at f0 > 0 may pass a base that lies before its buffer. Otherwise it is
+  // others[w] + ids2[i] * block_bytes: a second paged buffer (for example the
+  // pinned host mirror, read and written by the kernel over PCIe).
   uint64_t staging = 0;
+  uint64_t others = 0;
   int64_t stride_w = 0;
   int64_t stride_i = 0;
   int64_t f0 = 0;          // first flat block of the piece
   int64_t nblocks = 0;     // flat blocks in the piece
   int64_t block_bytes = 0; // bytes per block of every storage in the piece
   int64_t pool_blocks = 0; // valid block ids are [0, pool_blocks)
+  int64_t other_blocks = 0; // valid ids2 are [0, other_blocks) when others != 0
 };
 
 struct CopyLaunch {
   CopyPiece pieces[kMaxPieces];
   int npieces = 0;
-  const int64_t* ids = nullptr;  // device array of n block ids
+  const int64_t* ids = nullptr;   // device array of n block ids
+  const int64_t* ids2 = nullptr;  // block ids on the `others` side (if used)
   int64_t n = 0;
   int32_t* error = nullptr;      // optional device word; set to 1 on a bad id
+  // 0: one workgroup per large block (best for HBM-bound copies). Otherwise
+  // at most about this many workgroups: each then moves a run of
+  // consecutive blocks, which leaves CUs free for other work (a PCIe-bound
+  // zero-copy kernel needs only a few hundred workgroups in flight).
+  int64_t max_workgroups = 0;
 };
 
+// kGather reads the `storages` side and writes the other side; kScatter the
+// reverse.
 enum class CopyDir : int { kGather = 0, kScatter = 1 };
 
 // Largest vector width (16, 4 or 1 bytes) that every address of the launch

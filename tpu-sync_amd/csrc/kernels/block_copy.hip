@@ -48,20 +48,23 @@ __device__ __forceinline__ T uniform_load(uint64_t table, uint32_t idx) {
 struct KPiece {
   uint64_t storages;
   uint64_t staging;
+  uint64_t others;
   int64_t stride_w;
   int64_t stride_i;
   int64_t pool_blocks;
+  int64_t other_blocks;
   uint32_t f0;
   uint32_t nblocks;
   uint32_t elems;     // vectors per block
   uint32_t bpw;       // blocks per workgroup
   uint32_t wg_begin;  // first workgroup of the piece
-  uint32_t pad;
+  uint32_t whole;     // 1: every lane works on one block at a time
 };
 
 struct KParams {
   KPiece p[kMaxPieces];
   const int64_t* ids;
+  const int64_t* ids2;
   int32_t* error;
   uint32_t n;
   int32_t npieces;
@@ -104,6 +107,10 @@ __device__ __forceinline__ KPiece select_piece(const KParams& P, uint32_t wg) {
   return p;
 }
 
+__device__ __forceinline__ bool bad_id(int64_t id, int64_t limit) {
+  return static_cast<uint64_t>(id) >= static_cast<uint64_t>(limit);
+}
+
 template <typename V, bool kGather, int kUnroll>
 __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
   const uint32_t wg = blockIdx.x;
@@ -111,23 +118,39 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
   const uint32_t b0 = (wg - p.wg_begin) * p.bpw;
   const uint32_t n = P.n;
 
-  if (p.bpw == 1) {
-    const uint32_t f = p.f0 + b0;
-    const uint32_t w = f / n;
-    const uint32_t i = f - w * n;
-    const int64_t id = uniform_load<int64_t>(reinterpret_cast<uint64_t>(P.ids), i);
-    if (static_cast<uint64_t>(id) >= static_cast<uint64_t>(p.pool_blocks)) {
-      if (threadIdx.x == 0 && P.error != nullptr) atomicOr(P.error, 1);
-      return;
-    }
-    const uint64_t base = uniform_load<uint64_t>(p.storages, w);
-    KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(id) * p.elems;
-    KVX_GLOBAL V* stg = gptr<V>(p.staging + w * static_cast<uint64_t>(p.stride_w) +
-                                i * static_cast<uint64_t>(p.stride_i));
-    if (kGather) {
-      copy_whole_block<V, kUnroll>(pool, stg, p.elems);
-    } else {
-      copy_whole_block<V, kUnroll>(stg, pool, p.elems);
+  if (p.whole) {
+    // All lanes move one block at a time; the workgroup walks a run of
+    // consecutive flat blocks (one block unless the grid is capped).
+    const uint32_t left = p.nblocks - b0;
+    const uint32_t nb = left < p.bpw ? left : p.bpw;
+    for (uint32_t b = 0; b < nb; ++b) {
+      const uint32_t f = p.f0 + b0 + b;
+      const uint32_t w = f / n;
+      const uint32_t i = f - w * n;
+      const int64_t id = uniform_load<int64_t>(reinterpret_cast<uint64_t>(P.ids), i);
+      uint64_t other;
+      bool bad = bad_id(id, p.pool_blocks);
+      if (p.others != 0) {
+        const int64_t id2 = uniform_load<int64_t>(reinterpret_cast<uint64_t>(P.ids2), i);
+        bad = bad || bad_id(id2, p.other_blocks);
+        other = uniform_load<uint64_t>(p.others, w) +
+                static_cast<uint64_t>(id2) * p.elems * sizeof(V);
+      } else {
+        other = p.staging + w * static_cast<uint64_t>(p.stride_w) +
+                i * static_cast<uint64_t>(p.stride_i);
+      }
+      if (bad) {
+        if (threadIdx.x == 0 && P.error != nullptr) atomicOr(P.error, 1);
+        continue;
+      }
+      const uint64_t base = uniform_load<uint64_t>(p.storages, w);
+      KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(id) * p.elems;
+      KVX_GLOBAL V* stg = gptr<V>(other);
+      if (kGather) {
+        copy_whole_block<V, kUnroll>(pool, stg, p.elems);
+      } else {
+        copy_whole_block<V, kUnroll>(stg, pool, p.elems);
+      }
     }
     return;
   }
@@ -144,15 +167,24 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
     const uint32_t w = f / n;
     const uint32_t i = f - w * n;
     const int64_t id = gptr<const int64_t>(reinterpret_cast<uint64_t>(P.ids))[i];
-    if (static_cast<uint64_t>(id) >= static_cast<uint64_t>(p.pool_blocks)) {
+    bool bad = bad_id(id, p.pool_blocks);
+    uint64_t other;
+    if (p.others != 0) {
+      const int64_t id2 = gptr<const int64_t>(reinterpret_cast<uint64_t>(P.ids2))[i];
+      bad = bad || bad_id(id2, p.other_blocks);
+      other = gptr<const uint64_t>(p.others)[w] +
+              static_cast<uint64_t>(id2) * p.elems * sizeof(V);
+    } else {
+      other = p.staging + w * static_cast<uint64_t>(p.stride_w) +
+              i * static_cast<uint64_t>(p.stride_i);
+    }
+    if (bad) {
       if (P.error != nullptr) atomicOr(P.error, 1);
       continue;
     }
     const uint64_t base = gptr<const uint64_t>(p.storages)[w];
     KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(id) * p.elems + sub;
-    KVX_GLOBAL V* stg = gptr<V>(p.staging + w * static_cast<uint64_t>(p.stride_w) +
-                                i * static_cast<uint64_t>(p.stride_i)) +
-                        sub;
+    KVX_GLOBAL V* stg = gptr<V>(other) + sub;
     if (kGather) {
       st_nt(ld_nt(pool), stg);
     } else {
@@ -177,9 +209,14 @@ bool BuildParams(const CopyLaunch& l, int vec_bytes, KParams* P,
   }
   *P = KParams{};
   P->ids = l.ids;
+  P->ids2 = l.ids2;
   P->error = l.error;
   P->n = static_cast<uint32_t>(l.n);
   P->npieces = l.npieces;
+  uint64_t total_blocks = 0;
+  for (int k = 0; k < l.npieces; ++k) {
+    total_blocks += static_cast<uint64_t>(l.pieces[k].nblocks > 0 ? l.pieces[k].nblocks : 0);
+  }
   uint64_t wg = 0;
   for (int k = 0; k < l.npieces; ++k) {
     const CopyPiece& c = l.pieces[k];
@@ -187,24 +224,37 @@ bool BuildParams(const CopyLaunch& l, int vec_bytes, KParams* P,
         c.block_bytes % vec_bytes != 0 || c.pool_blocks <= 0) {
       return false;
     }
+    if (c.others != 0 && (l.ids2 == nullptr || c.other_blocks <= 0)) return false;
     if (static_cast<uint64_t>(c.f0) + static_cast<uint64_t>(c.nblocks) >
         UINT32_MAX) {
       return false;
     }
     const uint64_t elems = static_cast<uint64_t>(c.block_bytes) / vec_bytes;
     if (elems > UINT32_MAX) return false;
-    const uint32_t bpw = BlocksPerWorkgroup(elems);
-    if (static_cast<uint64_t>(bpw) * elems > UINT32_MAX) return false;
+    const bool whole = elems >= 2 * kThreads;
+    uint64_t bpw = BlocksPerWorkgroup(elems);
+    if (whole && l.max_workgroups > 0) {
+      // This piece's share of the workgroup cap, at least one.
+      uint64_t share = static_cast<uint64_t>(l.max_workgroups) *
+                       static_cast<uint64_t>(c.nblocks) / total_blocks;
+      if (share < 1) share = 1;
+      const uint64_t need = (static_cast<uint64_t>(c.nblocks) + share - 1) / share;
+      if (need > bpw) bpw = need;
+    }
+    if (bpw > UINT32_MAX || (!whole && bpw * elems > UINT32_MAX)) return false;
     KPiece& kp = P->p[k];
     kp.storages = c.storages;
     kp.staging = c.staging;
+    kp.others = c.others;
+    kp.other_blocks = c.other_blocks;
     kp.stride_w = c.stride_w;
     kp.stride_i = c.stride_i;
     kp.pool_blocks = c.pool_blocks;
     kp.f0 = static_cast<uint32_t>(c.f0);
     kp.nblocks = static_cast<uint32_t>(c.nblocks);
     kp.elems = static_cast<uint32_t>(elems);
-    kp.bpw = bpw;
+    kp.bpw = static_cast<uint32_t>(bpw);
+    kp.whole = whole ? 1u : 0u;
     kp.wg_begin = static_cast<uint32_t>(wg);
     wg += (static_cast<uint64_t>(c.nblocks) + bpw - 1) / bpw;
     if (wg > INT32_MAX) return false;

@@ -167,7 +167,8 @@ class KVCacheManager:
                  staging_chunk_bytes: int = 0, staging_chunks: int = 0,
                  direct_min_bytes: int = 0, shm_key: Optional[str] = None,
                  shm_server_name: Optional[str] = None,
-                 model_uid: Optional[str] = None, profile_kernels: bool = False):
+                 model_uid: Optional[str] = None, profile_kernels: bool = False,
+                 transfer_mode: str = "auto", zero_copy_workgroups: int = 0):
         if host_blocks_to_allocate is None:
             if max_blocks is None or num_slots is None:
                 raise ValueError("Must specify either (max_blocks, num_slots) or"
@@ -190,7 +191,7 @@ class KVCacheManager:
         self._init(device, len(layers), num_shards, ptrs, sizes, major_dim, 0,
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
-                   model_uid, profile_kernels)
+                   model_uid, profile_kernels, transfer_mode, zero_copy_workgroups)
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
             self.configure_host_staging_slots(num_slots, max_blocks)
@@ -198,7 +199,7 @@ class KVCacheManager:
     def _init(self, device, num_layers, num_shards, ptrs, sizes, major_dim,
               slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
               direct_min_bytes, shm_key, shm_server_name, model_uid,
-              profile_kernels=False):
+              profile_kernels=False, transfer_mode="auto", zero_copy_workgroups=0):
         lib = _capi.load()
         kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
                  "shm": _capi.HOST_SHM}
@@ -222,6 +223,8 @@ class KVCacheManager:
         cfg.shm_server_name = shm_server_name.encode() if shm_server_name else None
         cfg.model_uid = model_uid.encode() if model_uid else None
         cfg.profile_kernels = int(bool(profile_kernels))
+        cfg.transfer_mode = _capi.MODES[transfer_mode]
+        cfg.zero_copy_workgroups = zero_copy_workgroups
         h = ctypes.c_void_p()
         _capi.check(lib.kvx_manager_create(ctypes.byref(cfg), ctypes.byref(h)),
                     "KVCacheManager create")
@@ -411,10 +414,10 @@ class KVCacheManager:
         _capi.check(_capi.load().kvx_manager_wait_for_pending_work(self._h))
 
     def engine_stats(self) -> dict:
-        out = (ctypes.c_int64 * 5)()
+        out = (ctypes.c_int64 * 6)()
         _capi.check(_capi.load().kvx_manager_engine_stats(self._h, out))
         keys = ("direct_copies", "staged_copies", "memcpy_calls", "kernel_launches",
-                "chunks")
+                "chunks", "zero_copy_copies")
         return dict(zip(keys, list(out)))
 
     def kernel_times(self, gather: bool = True, reset: bool = False) -> dict:
