@@ -7,9 +7,12 @@ this package is a thin ctypes layer that only passes pointers.
 from . import _capi
 from ._capi import KvxError
 from .kv_cache_manager import KVCacheManager, LogicalBlockManager, RaidenFuture
+from .kv_cache_store import (BlockStatus, KVCacheMetadata, KVCacheMetadataShmRegion,
+                             KVCacheStore, LRUCache, RaidenBlockId, RaidenId)
 
 __all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError",
-           "library_path"]
+           "KVCacheStore", "RaidenId", "RaidenBlockId", "BlockStatus", "LRUCache",
+           "KVCacheMetadata", "KVCacheMetadataShmRegion", "library_path"]
 
 
 def library_path() -> str:

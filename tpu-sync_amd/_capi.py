@@ -57,6 +57,43 @@ class ManagerConfig(ctypes.Structure):
     ]
 
 
+class BlockSlice(ctypes.Structure):
+    """kvx_block_slice: RaidenBlockId across the C-ABI."""
+    _fields_ = [
+        ("host_block_id", ctypes.c_int32),
+        ("device_block_id", ctypes.c_int32),
+        ("status", ctypes.c_int32),
+        ("data_replica_idx", ctypes.c_int32),
+        ("job_name", ctypes.c_char_p),
+        ("job_replica_id", ctypes.c_char_p),
+        ("data_name", ctypes.c_char_p),
+    ]
+
+
+class StoreConfig(ctypes.Structure):
+    _fields_ = [
+        ("capacity", ctypes.c_int64),
+        ("job_name", ctypes.c_char_p),
+        ("job_replica_id", ctypes.c_char_p),
+        ("data_name", ctypes.c_char_p),
+        ("data_replica_idx", ctypes.c_int32),
+        ("num_shards", ctypes.c_int32),
+        ("shard_size_bytes", ctypes.c_int64),
+        ("store_server_ip", ctypes.c_char_p),
+        ("raiden_controller_port", ctypes.c_int32),
+        ("metadata_shm_key", ctypes.c_char_p),
+        ("model_uid", ctypes.c_char_p),
+        ("no_auto_recover", ctypes.c_int32),
+        ("host_blocks", ctypes.c_int64),
+    ]
+
+
+# kvx_transfer_fn(user, d2h, src, dst, n) -> status
+TRANSFER_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                               ctypes.POINTER(ctypes.c_int64),
+                               ctypes.POINTER(ctypes.c_int64), ctypes.c_int64)
+
+
 _i32, _i64, _u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
 _vp, _i64p, _i32p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32)
 _u64p = ctypes.POINTER(ctypes.c_uint64)
@@ -119,6 +156,67 @@ PROTOTYPES = {
     "kvx_block_manager_num_locked": (_i32, [_vp]),
     "kvx_gather_blocks": (_int, [_u64, _i64, _i64, _i64, _u64, _i64, _u64, _i32, _u64, _vp]),
     "kvx_scatter_blocks": (_int, [_u64, _i64, _i64, _i64, _u64, _i64, _u64, _i32, _u64, _vp]),
+    "kvx_manager_register_with_controller": (_int, [_vp, ctypes.c_char_p]),
+    "kvx_manager_shm_warm": (_i32, [_vp]),
+    # host tier
+    "kvx_strings_count": (_i64, [_vp]),
+    "kvx_strings_get": (_int, [_vp, _i64, ctypes.POINTER(_vp), _i64p]),
+    "kvx_strings_release": (None, [_vp]),
+    "kvx_slices_count": (_i64, [_vp]),
+    "kvx_slices_get": (_int, [_vp, _i64, ctypes.POINTER(_vp), _i64p,
+                              ctypes.POINTER(BlockSlice)]),
+    "kvx_slices_release": (None, [_vp]),
+    "kvx_store_create": (_int, [ctypes.POINTER(StoreConfig), ctypes.POINTER(_vp)]),
+    "kvx_store_destroy": (None, [_vp]),
+    "kvx_store_controller_address": (ctypes.c_char_p, [_vp]),
+    "kvx_store_capacity": (_i64, [_vp]),
+    "kvx_store_size": (_i64, [_vp]),
+    "kvx_store_recovered_blocks": (_i64, [_vp]),
+    "kvx_store_metadata_warm": (_i32, [_vp]),
+    "kvx_store_host_block_manager": (_vp, [_vp]),
+    "kvx_store_lookup": (_int, [_vp, _vp, _i64p, _i64, _i32, ctypes.POINTER(_vp)]),
+    "kvx_store_insert": (_int, [_vp, _vp, _i64p, _i64, ctypes.POINTER(BlockSlice), _i64,
+                                _i32]),
+    "kvx_store_release": (_int, [_vp, _vp, _i64p, _i64]),
+    "kvx_store_save": (_int, [_vp, _vp, _i64p, _i64]),
+    "kvx_store_load": (_int, [_vp, _vp, _i64p, _i64, _i32p, _i64]),
+    "kvx_store_load_slices": (_int, [_vp, _vp, _i64p, _i64, ctypes.POINTER(BlockSlice), _i64,
+                                     _i32p, _i64]),
+    "kvx_store_poll_save_status": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "kvx_store_poll_load_status": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "kvx_store_pin_count": (_i32, [_vp, _vp, _i64]),
+    "kvx_store_recover_from_local_manifest": (_int, [_vp, _i64p]),
+    "kvx_store_evictable_keys": (_int, [_vp, _i64, ctypes.POINTER(_vp)]),
+    "kvx_store_evict": (_int, [_vp, _vp, _i64p, _i64, _i64p]),
+    "kvx_store_candidate_keys": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "kvx_store_set_transfer_fn": (_int, [_vp, TRANSFER_FN, _vp]),
+    "kvx_lru_create": (_int, [_i64, ctypes.POINTER(_vp)]),
+    "kvx_lru_destroy": (None, [_vp]),
+    "kvx_lru_put": (_int, [_vp, _vp, _i64, _i64, _i32p, ctypes.POINTER(_vp), _i64p]),
+    "kvx_lru_put_back": (_int, [_vp, _vp, _i64, _i64]),
+    "kvx_lru_find": (_i32, [_vp, _i32, _vp, _i64, _i64p]),
+    "kvx_lru_contains": (_i32, [_vp, _vp, _i64]),
+    "kvx_lru_pin": (_i32, [_vp, _vp, _i64]),
+    "kvx_lru_unpin": (_i32, [_vp, _vp, _i64]),
+    "kvx_lru_erase": (_i32, [_vp, _vp, _i64]),
+    "kvx_lru_pin_count": (_i32, [_vp, _vp, _i64]),
+    "kvx_lru_evict": (_i32, [_vp, ctypes.POINTER(_vp), _i64p]),
+    "kvx_lru_evictable_keys": (_int, [_vp, _i64, ctypes.POINTER(_vp)]),
+    "kvx_lru_candidate_keys": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "kvx_lru_clear": (None, [_vp]),
+    "kvx_lru_sizes": (_int, [_vp, _i64p]),
+    "kvx_metadata_required_size": (_i64, [_i32]),
+    "kvx_metadata_format": (_int, [_vp, _i64, _i32, ctypes.c_char_p]),
+    "kvx_metadata_attach": (_int, [_vp, _i64, _i32, ctypes.c_char_p]),
+    "kvx_metadata_set": (_int, [_vp, _i64, _i32, ctypes.c_char_p, _i32, _vp, _i64, _u64]),
+    "kvx_metadata_clear": (_int, [_vp, _i64, _i32, ctypes.c_char_p, _i32]),
+    "kvx_metadata_valid_entries": (_int, [_vp, _i64, _i32, ctypes.c_char_p, _i32p, _u64p,
+                                          _i64p, ctypes.POINTER(_vp)]),
+    "kvx_metadata_shm_attach_or_format": (_int, [ctypes.c_char_p, _i32, ctypes.c_char_p,
+                                                 ctypes.POINTER(_vp), _i32p]),
+    "kvx_metadata_shm_region": (_int, [_vp, _u64p, _i64p]),
+    "kvx_metadata_shm_reformat": (_int, [_vp]),
+    "kvx_metadata_shm_release": (None, [_vp]),
 }
 
 _lib = None
@@ -161,3 +259,31 @@ def i32_array(values):
     vals = [int(v) for v in values]
     arr = (ctypes.c_int32 * max(len(vals), 1))(*vals)
     return arr, len(vals)
+
+
+def pack_bytes(items):
+    """Packs byte strings back to back: (buffer, offsets[n + 1], n)."""
+    items = [bytes(b) for b in items]
+    offs = [0]
+    for b in items:
+        offs.append(offs[-1] + len(b))
+    blob = b"".join(items)
+    buf = ctypes.create_string_buffer(blob, max(len(blob), 1))
+    arr = (ctypes.c_int64 * len(offs))(*offs)
+    return buf, arr, len(items)
+
+
+def take_strings(handle):
+    """Copies a kvx_strings list into Python bytes and releases it."""
+    lib = load()
+    if not handle:
+        return []
+    try:
+        out = []
+        data, ln = ctypes.c_void_p(), ctypes.c_int64()
+        for i in range(lib.kvx_strings_count(handle)):
+            check(lib.kvx_strings_get(handle, i, ctypes.byref(data), ctypes.byref(ln)))
+            out.append(ctypes.string_at(data, ln.value) if ln.value else b"")
+        return out
+    finally:
+        lib.kvx_strings_release(handle)

@@ -1,37 +1,21 @@
 // extern "C" layer over the C++ manager, futures and block allocator.
 // Each entry point validates its arguments, calls the C++ object and turns
 // a Status into its code plus a thread-local message.
-#include "../../../include/kvx.h"
-
 #include <cstring>
 #include <memory>
 #include <optional>
 #include <string>
 #include <vector>
 
-#include "../host/copy_future.h"
-#include "../host/kv_cache_manager.h"
-#include "../host/logical_block_manager.h"
+#include "../host/kv_cache_store.h"
 #include "../kernels/block_copy.h"
-
-struct kvx_block_manager {
-  kvx::LogicalBlockManager* lbm = nullptr;
-  std::unique_ptr<kvx::LogicalBlockManager> owned;
-  std::mutex* mu = nullptr;  // the owning manager's lock, if any
-};
-
-struct kvx_manager {
-  std::unique_ptr<kvx::KVCacheManager> impl;
-  kvx_block_manager lbm_view;  // borrowed view of the manager's allocator
-};
-
-struct kvx_future {
-  kvx::CopyFuture f;
-};
+#include "capi_internal.h"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+namespace kvx_capi {
 
 int Fail(const kvx::Status& s) {
   g_last_error = s.message();
@@ -48,6 +32,14 @@ int Done(const kvx::Status& s) {
   return KVX_OK;
 }
 
+}  // namespace kvx_capi
+
+namespace {
+
+using kvx_capi::BadArray;
+using kvx_capi::Done;
+using kvx_capi::Fail;
+
 std::vector<int64_t> Vec(const int64_t* p, int64_t n) {
   if (p == nullptr || n <= 0) return {};
   return std::vector<int64_t>(p, p + n);
@@ -61,7 +53,6 @@ std::optional<size_t> OptIdx(int64_t v) {
   return v < 0 ? std::nullopt : std::optional<size_t>(static_cast<size_t>(v));
 }
 
-bool BadArray(const void* p, int64_t n) { return n < 0 || (n > 0 && p == nullptr); }
 
 int EmitFuture(kvx::StatusOr<kvx::CopyFuture> r, kvx_future** out) {
   if (!r.ok()) return Fail(r.status());
@@ -142,7 +133,22 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   return KVX_OK;
 }
 
-void kvx_manager_destroy(kvx_manager* m) { delete m; }
+void kvx_manager_destroy(kvx_manager* m) {
+  if (m == nullptr) return;
+  kvx::UnregisterWorker(m->impl.get());
+  delete m;
+}
+
+int kvx_manager_register_with_controller(kvx_manager* m, const char* address) {
+  if (m == nullptr || address == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null manager or address");
+  }
+  return Done(kvx::RegisterWorkerAtController(address, m->impl.get()));
+}
+
+int32_t kvx_manager_shm_warm(const kvx_manager* m) {
+  return m != nullptr && m->impl->shm_warm() ? 1 : 0;
+}
 
 static int Transfer(bool d2h, kvx_manager* m, const int64_t* src, int64_t n_src,
                     const int64_t* dst, int64_t n_dst, const int64_t* sizes,

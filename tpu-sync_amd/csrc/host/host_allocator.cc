@@ -1,7 +1,12 @@
 #include "host_allocator.h"
 
+#include <fcntl.h>
 #include <hip/hip_runtime_api.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
+#include <cerrno>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -39,6 +44,117 @@ StatusOr<HostBufferAllocation> AllocatePinnedHost(size_t bytes, int device) {
   a.ptr = static_cast<uint8_t*>(p);
   a.size = bytes;
   a.owner = std::shared_ptr<void>(p, [](void* q) { (void)hipHostFree(q); });
+  return a;
+}
+
+std::string ShmSegmentName(const std::string& key, const std::string& server_name,
+                           int device) {
+  std::string name = key;
+  if (!server_name.empty()) name += "_" + server_name;
+  if (device >= 0) name += "_dev_" + std::to_string(device);
+  if (name.empty() || name[0] != '/') name.insert(0, "/");
+  return name;
+}
+
+namespace {
+
+bool SchemaMatches(const SharedMemoryHeader& h, const SharedMemoryHeader& want,
+                   size_t bytes) {
+  return h.magic == want.magic && h.version == want.version &&
+         strncmp(h.model_uid, want.model_uid, sizeof(h.model_uid)) == 0 &&
+         h.num_blocks == want.num_blocks && h.block_size == want.block_size &&
+         h.num_heads == want.num_heads && h.head_dim == want.head_dim &&
+         h.itemsize == want.itemsize && h.total_payload_bytes == bytes;
+}
+
+struct ShmMapping {
+  int fd = -1;
+  void* map = nullptr;
+  size_t size = 0;
+  ~ShmMapping() {
+    if (map != nullptr) {
+      auto* h = static_cast<SharedMemoryHeader*>(map);
+      if (h->reference_count > 0) --h->reference_count;
+      munmap(map, size);
+    }
+    if (fd >= 0) close(fd);
+  }
+};
+
+}  // namespace
+
+StatusOr<HostBufferAllocation> AllocateShmHost(const std::string& name,
+                                               const SharedMemoryHeader& expected,
+                                               size_t bytes, bool* warm) {
+  const size_t total =
+      (sizeof(SharedMemoryHeader) + ((bytes + 4095) & ~size_t{4095}) + 4095) &
+      ~size_t{4095};
+  *warm = false;
+  int fd = shm_open(name.c_str(), O_RDWR, 0666);
+  if (fd >= 0) {
+    struct stat st;
+    bool ok = fstat(fd, &st) == 0 && static_cast<size_t>(st.st_size) >= total;
+    if (ok) {
+      void* hp = mmap(nullptr, sizeof(SharedMemoryHeader), PROT_READ, MAP_SHARED, fd, 0);
+      ok = hp != MAP_FAILED &&
+           SchemaMatches(*static_cast<SharedMemoryHeader*>(hp), expected, bytes);
+      if (hp != MAP_FAILED) munmap(hp, sizeof(SharedMemoryHeader));
+    }
+    if (ok) {
+      *warm = true;
+    } else {
+      close(fd);
+      fd = -1;
+      shm_unlink(name.c_str());
+    }
+  }
+  if (fd < 0) {
+    fd = shm_open(name.c_str(), O_CREAT | O_RDWR, 0666);
+    if (fd < 0) {
+      return InternalError("shm_open failed to create segment " + name + ": " +
+                           std::strerror(errno));
+    }
+    if (ftruncate(fd, static_cast<off_t>(total)) != 0) {
+      Status st = InternalError("ftruncate failed on shm segment " + name + ": " +
+                                std::strerror(errno));
+      close(fd);
+      shm_unlink(name.c_str());
+      return st;
+    }
+  }
+  auto m = std::make_shared<ShmMapping>();
+  m->fd = fd;
+  void* map = mmap(nullptr, total, PROT_READ | PROT_WRITE, MAP_SHARED, fd, 0);
+  if (map == MAP_FAILED) {
+    return ResourceExhaustedError("mmap failed on shm segment " + name + ": " +
+                                  std::strerror(errno));
+  }
+  m->map = map;
+  m->size = total;
+  auto* h = static_cast<SharedMemoryHeader*>(map);
+  if (*warm) {
+    ++h->reference_count;
+  } else {
+    // A fresh segment reads as zeros; write the schema field by field (the
+    // padding stays zero) and take the first reference.
+    h->magic = expected.magic;
+    h->version = expected.version;
+    std::memcpy(h->model_uid, expected.model_uid, sizeof(h->model_uid));
+    std::memcpy(h->global_mesh_shape, expected.global_mesh_shape,
+                sizeof(h->global_mesh_shape));
+    std::memcpy(h->shard_layout, expected.shard_layout, sizeof(h->shard_layout));
+    h->num_blocks = expected.num_blocks;
+    h->block_size = expected.block_size;
+    h->num_heads = expected.num_heads;
+    h->head_dim = expected.head_dim;
+    h->itemsize = expected.itemsize;
+    h->total_payload_bytes = bytes;
+    h->reference_count = 1;
+  }
+  HostBufferAllocation a;
+  a.ptr = static_cast<uint8_t*>(map) + sizeof(SharedMemoryHeader);
+  a.size = bytes;
+  a.owner = m;
   return a;
 }
 

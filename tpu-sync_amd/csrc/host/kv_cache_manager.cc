@@ -126,6 +126,38 @@ Status KVCacheManager::Init() {
 
   lbm_ = std::make_unique<LogicalBlockManager>(static_cast<int>(host_blocks_));
 
+  // Shared-memory host tier: one segment holds every (layer, shard) mirror
+  // back to back, [storage][host_blocks][layer block bytes]. (The
+  // reference's shm allocator hands the same mapping to every mirror, which
+  // aliases the layers of a multi-layer pool.)
+  HostBufferAllocation shm;
+  int64_t shm_off = 0;
+  if (cfg_.host_alloc == HostAllocKind::kShm) {
+    if (cfg_.shm_key.empty()) {
+      return InvalidArgumentError("shared-memory host tier needs a shm_key");
+    }
+    int64_t total = 0;
+    for (size_t k = 0; k < nstor; ++k) {
+      const int64_t layer_bb = layer_block_bytes_[k / num_shards_];
+      if (!RangeFits(host_blocks_, layer_bb, total, std::numeric_limits<int64_t>::max())) {
+        return InvalidArgumentError("host mirror size overflows");
+      }
+      total += host_blocks_ * layer_bb;
+    }
+    SharedMemoryHeader want;
+    const std::string uid = cfg_.model_uid.empty() ? "default_model" : cfg_.model_uid;
+    if (uid.size() >= sizeof(want.model_uid)) {
+      return InvalidArgumentError("model_uid too long");
+    }
+    std::memcpy(want.model_uid, uid.data(), uid.size());
+    want.num_blocks = static_cast<uint32_t>(host_blocks_);
+    want.block_size = static_cast<uint32_t>(slice_byte_size_);
+    const std::string name = ShmSegmentName(cfg_.shm_key, cfg_.shm_server_name,
+                                            device_backed ? cfg_.device : -1);
+    KVX_ASSIGN_OR_RETURN(shm, AllocateShmHost(name, want, static_cast<size_t>(total),
+                                              &shm_warm_));
+  }
+
   for (size_t k = 0; k < nstor; ++k) {
     // Each (layer, shard) mirror holds host_blocks blocks of that layer's own
     // block size. The reference sizes every mirror by the first layer's
@@ -145,6 +177,15 @@ Status KVCacheManager::Init() {
         a = device_backed ? AllocatePinnedHost(static_cast<size_t>(alloc_size), cfg_.device)
                           : AllocateMallocHost(static_cast<size_t>(alloc_size));
         break;
+      case HostAllocKind::kShm: {
+        HostBufferAllocation part;
+        part.ptr = shm.ptr + shm_off;
+        part.size = static_cast<size_t>(alloc_size);
+        part.owner = shm.owner;
+        shm_off += alloc_size;
+        a = part;
+        break;
+      }
       default:
         return UnimplementedError("host allocator kind not supported");
     }

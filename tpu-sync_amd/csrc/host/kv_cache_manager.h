@@ -137,6 +137,8 @@ class KVCacheManager {
   int64_t major_dim() const { return major_dim_; }
   int64_t host_blocks() const { return host_blocks_; }
   bool device_backed() const { return engine_ != nullptr; }
+  // True when the shared-memory host tier attached to a surviving segment.
+  bool shm_warm() const { return shm_warm_; }
   int device() const { return cfg_.device; }
   TransferEngine* engine() { return engine_.get(); }
   Status WaitForPendingWork();
@@ -187,6 +189,7 @@ class KVCacheManager {
   std::vector<StorageInfo> storages_;
   size_t allocated_host_bytes_ = 0;
   bool host_kernel_access_ = false;
+  bool shm_warm_ = false;
   int64_t staging_num_slots_ = 0;
   int64_t staging_max_major_per_slot_ = 0;
   std::unique_ptr<LogicalBlockManager> lbm_;

@@ -64,6 +64,20 @@ def _stream_ptr(stream) -> int:
     return int(getattr(stream, "cuda_stream", stream))
 
 
+def _host_tier_from_env(host_alloc, shm_key, shm_server_name, model_uid):
+    """Host memory kind and shm naming, defaulting from RAIDEN_SHM_* like the
+    reference (tpu_sync/core/utils.h:48-91)."""
+    import os
+    env_key = os.environ.get("RAIDEN_SHM_KEY", "")
+    if host_alloc is None:
+        host_alloc = "shm" if (shm_key or env_key) else "pinned"
+    if host_alloc == "shm":
+        shm_key = shm_key or env_key
+        model_uid = model_uid or os.environ.get("RAIDEN_SHM_MODEL_UID") or "default_model"
+        shm_server_name = shm_server_name or os.environ.get("RAIDEN_SHM_SERVER_NAME") or None
+    return host_alloc, shm_key, shm_server_name, model_uid
+
+
 def _flatten_caches(kv_caches) -> Tuple[List[List[Any]], int]:
     layers = []
     for entry in kv_caches:
@@ -148,12 +162,17 @@ class KVCacheManager:
       host_blocks_to_allocate: host mirror blocks per (layer, shard).
       max_blocks / num_slots: alternatively, a staging-slot layout; the host
         mirror then holds max_blocks * num_slots blocks.
-      host_alloc: "pinned" (hipHostMalloc, default), "malloc" or "shm".
+      host_alloc: "pinned" (hipHostMalloc), "malloc" or "shm". Default:
+        "shm" when RAIDEN_SHM_KEY is set (segment key; model uid from
+        RAIDEN_SHM_MODEL_UID, server name from RAIDEN_SHM_SERVER_NAME, as the
+        reference's CreateHostMemoryAllocator reads them,
+        tpu_sync/core/utils.h:48-91), else "pinned".
+      raiden_controller_address: joins the KVCacheStore whose controller
+        has this address (in this process) as its transfer worker.
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
-      The remaining reference arguments (ports, controller address, worker
-      id, timeout, parallelism, unsafe_skip_buffer_lock) configure its
-      networking and control plane, which this single-GPU build does not
-      have; they are accepted and ignored.
+      The remaining reference arguments (ports, worker id, timeout,
+      parallelism, unsafe_skip_buffer_lock) configure its networking, which
+      this single-GPU build does not have; they are accepted and ignored.
     """
 
     def __init__(self, kv_caches: List[Any], local_control_port: int = 0,
@@ -163,7 +182,7 @@ class KVCacheManager:
                  node_id: int = 0, listener_port: Optional[int] = None,
                  raiden_worker_port: int = 0,
                  raiden_controller_address: Optional[str] = None,
-                 worker_id: Optional[str] = None, *, host_alloc: str = "pinned",
+                 worker_id: Optional[str] = None, *, host_alloc: Optional[str] = None,
                  staging_chunk_bytes: int = 0, staging_chunks: int = 0,
                  direct_min_bytes: int = 0, shm_key: Optional[str] = None,
                  shm_server_name: Optional[str] = None,
@@ -188,6 +207,8 @@ class KVCacheManager:
         if layers:
             major_dim = int(layers[0][0].shape[0])
         self._tensors = layers  # borrowed device buffers stay alive
+        host_alloc, shm_key, shm_server_name, model_uid = _host_tier_from_env(
+            host_alloc, shm_key, shm_server_name, model_uid)
         self._init(device, len(layers), num_shards, ptrs, sizes, major_dim, 0,
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
@@ -195,6 +216,14 @@ class KVCacheManager:
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
             self.configure_host_staging_slots(num_slots, max_blocks)
+        if raiden_controller_address:
+            _capi.check(_capi.load().kvx_manager_register_with_controller(
+                self._h, raiden_controller_address.encode()), "RegisterWorker")
+
+    @property
+    def shm_warm(self) -> bool:
+        """True when the shared-memory host tier attached to a surviving segment."""
+        return bool(_capi.load().kvx_manager_shm_warm(self._h))
 
     def _init(self, device, num_layers, num_shards, ptrs, sizes, major_dim,
               slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
@@ -235,12 +264,18 @@ class KVCacheManager:
                                      slice_byte_size: int, node_id: int = 0,
                                      local_port: Optional[int] = None,
                                      host_blocks: int, parallelism: int = 4,
-                                     host_alloc: str = "malloc") -> "KVCacheManager":
-        """CPU-only manager backed by library-owned host memory."""
+                                     host_alloc: str = "malloc",
+                                     shm_key: Optional[str] = None,
+                                     shm_server_name: Optional[str] = None,
+                                     model_uid: Optional[str] = None) -> "KVCacheManager":
+        """CPU-only manager backed by library-owned host memory ("shm": a
+        shared-memory segment named by shm_key or RAIDEN_SHM_KEY)."""
         obj = cls.__new__(cls)
         obj._tensors = []
+        host_alloc, shm_key, shm_server_name, model_uid = _host_tier_from_env(
+            host_alloc, shm_key, shm_server_name, model_uid)
         obj._init(0, num_layers, num_shards, [], [], 0, slice_byte_size, host_blocks,
-                  host_alloc, 0, 0, 0, None, None, None)
+                  host_alloc, 0, 0, 0, shm_key, shm_server_name, model_uid)
         obj.node_id = node_id
         return obj
 
