@@ -439,6 +439,77 @@ int kvx_metadata_shm_region(kvx_metadata_region* m, uint64_t* out_ptr,
 int kvx_metadata_shm_reformat(kvx_metadata_region* m);
 void kvx_metadata_shm_release(kvx_metadata_region* m);
 
+/* ---------------------------------------------------------------------------
+ * Weight sync: WeightSynchronizerBase::D2h / D2hLayer / H2d / H2dLayer
+ * (tpu_sync/weight_sync/weight_synchronizer_base.h:78-240,
+ * weight_synchronizer_base.cc:307-539) and the strided push-entry
+ * expansion of PushWeightsResharded (weight_synchronizer_base.cc:626-666).
+ * Each (layer, shard) is one device tensor; the host copies share one
+ * buffer at a per-tensor offset table (ascending, 256-byte aligned; bytes
+ * between tensors unspecified).
+ * ------------------------------------------------------------------------- */
+typedef struct kvx_weight_sync kvx_weight_sync;
+
+typedef struct kvx_weight_sync_config {
+  int32_t device;
+  int32_t host_alloc;          /* KVX_HOST_PINNED or KVX_HOST_MALLOC */
+  int64_t num_layers;          /* tensors */
+  int64_t num_shards;          /* >= 1 */
+  const uint64_t* device_ptrs; /* [num_layers * num_shards] */
+  const int64_t* device_bytes;
+  int64_t chunk_bytes;         /* device staging chunk, 0 = 256 MiB */
+  int64_t staging_chunks;      /* ring depth, 0 = 2 */
+  int32_t profile_kernels;
+} kvx_weight_sync_config;
+
+int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** out);
+void kvx_weight_sync_destroy(kvx_weight_sync* w);
+/* Whole parameter set: pack kernel -> staging ring -> one DMA per chunk
+ * (d2h), or one DMA per chunk -> unpack kernel (h2d). */
+int kvx_weight_sync_d2h(kvx_weight_sync* w, void* stream, kvx_future** out);
+int kvx_weight_sync_h2d(kvx_weight_sync* w, void* stream, kvx_future** out);
+/* One weight, one direct copy per shard. */
+int kvx_weight_sync_d2h_layer(kvx_weight_sync* w, int64_t layer, void* stream,
+                              kvx_future** out);
+int kvx_weight_sync_h2d_layer(kvx_weight_sync* w, int64_t layer, void* stream,
+                              kvx_future** out);
+/* Device-side pack of every tensor into a caller device buffer laid out by
+ * the offset table (and the reverse), one launch, on `stream`. */
+int kvx_weight_sync_pack(kvx_weight_sync* w, uint64_t staging, int64_t staging_bytes,
+                         void* stream, kvx_future** out);
+int kvx_weight_sync_unpack(kvx_weight_sync* w, uint64_t staging, int64_t staging_bytes,
+                           void* stream, kvx_future** out);
+int64_t kvx_weight_sync_total_bytes(const kvx_weight_sync* w);
+uint64_t kvx_weight_sync_host_base(const kvx_weight_sync* w);
+/* GetHostBufferPtr (weight_synchronizer_base.h:117-122): address, size and
+ * offset of one tensor's host copy. */
+int kvx_weight_sync_host_buffer(kvx_weight_sync* w, int64_t layer, int64_t shard,
+                                uint64_t* out_ptr, int64_t* out_bytes, int64_t* out_offset);
+int kvx_weight_sync_wait(kvx_weight_sync* w);
+/* Profiled pack (pack = 1) or unpack launches: count, ms, bytes moved. */
+int kvx_weight_sync_kernel_times(kvx_weight_sync* w, int32_t pack, int32_t reset,
+                                 int64_t* out_launches, double* out_ms, int64_t* out_bytes);
+
+/* Strided push entry with device addresses (ShardPushEntryProto,
+ * tpu_sync/rpc/raiden_service.proto:104-131): for c in [0, max(count, 1)):
+ * copy size_bytes from src + src_offset + c * src_stride to
+ * dst + dst_offset + c * dst_stride. */
+typedef struct kvx_strided_entry {
+  uint64_t src;
+  uint64_t dst;
+  int64_t src_offset_bytes;
+  int64_t dst_offset_bytes;
+  int64_t size_bytes;
+  int64_t count;
+  int64_t src_stride_bytes;
+  int64_t dst_stride_bytes;
+} kvx_strided_entry;
+
+/* Executes every entry in one kernel launch on `stream` (device addresses;
+ * destination rows must not overlap). */
+int kvx_copy_strided(int32_t device, const kvx_strided_entry* entries, int64_t n,
+                     void* stream, kvx_future** out);
+
 /*
  * Raw device kernels (no manager): gather / scatter block ids of W storages.
  * storage_table: device array of W uint64 base addresses; ids: device array

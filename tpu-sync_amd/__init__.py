@@ -10,9 +10,14 @@ from .kv_cache_manager import KVCacheManager, LogicalBlockManager, RaidenFuture
 from .kv_cache_store import (BlockStatus, KVCacheMetadata, KVCacheMetadataShmRegion,
                              KVCacheStore, LRUCache, RaidenBlockId, RaidenId)
 
+from .weight_synchronizer import (StridedEntry, WeightSynchronizer, column_split_entries,
+                                  compute_nd_shard_slices, copy_strided)
+
 __all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError",
            "KVCacheStore", "RaidenId", "RaidenBlockId", "BlockStatus", "LRUCache",
-           "KVCacheMetadata", "KVCacheMetadataShmRegion", "library_path"]
+           "KVCacheMetadata", "KVCacheMetadataShmRegion", "WeightSynchronizer",
+           "StridedEntry", "copy_strided", "column_split_entries",
+           "compute_nd_shard_slices", "library_path"]
 
 
 def library_path() -> str:

@@ -88,6 +88,33 @@ class StoreConfig(ctypes.Structure):
     ]
 
 
+class WeightSyncConfig(ctypes.Structure):
+    _fields_ = [
+        ("device", ctypes.c_int32),
+        ("host_alloc", ctypes.c_int32),
+        ("num_layers", ctypes.c_int64),
+        ("num_shards", ctypes.c_int64),
+        ("device_ptrs", ctypes.POINTER(ctypes.c_uint64)),
+        ("device_bytes", ctypes.POINTER(ctypes.c_int64)),
+        ("chunk_bytes", ctypes.c_int64),
+        ("staging_chunks", ctypes.c_int64),
+        ("profile_kernels", ctypes.c_int32),
+    ]
+
+
+class StridedEntryC(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_uint64),
+        ("dst", ctypes.c_uint64),
+        ("src_offset_bytes", ctypes.c_int64),
+        ("dst_offset_bytes", ctypes.c_int64),
+        ("size_bytes", ctypes.c_int64),
+        ("count", ctypes.c_int64),
+        ("src_stride_bytes", ctypes.c_int64),
+        ("dst_stride_bytes", ctypes.c_int64),
+    ]
+
+
 # kvx_transfer_fn(user, d2h, src, dst, n) -> status
 TRANSFER_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                ctypes.POINTER(ctypes.c_int64),
@@ -217,6 +244,23 @@ PROTOTYPES = {
     "kvx_metadata_shm_region": (_int, [_vp, _u64p, _i64p]),
     "kvx_metadata_shm_reformat": (_int, [_vp]),
     "kvx_metadata_shm_release": (None, [_vp]),
+    # weight sync
+    "kvx_weight_sync_create": (_int, [ctypes.POINTER(WeightSyncConfig), ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_destroy": (None, [_vp]),
+    "kvx_weight_sync_d2h": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_h2d": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_d2h_layer": (_int, [_vp, _i64, _vp, ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_h2d_layer": (_int, [_vp, _i64, _vp, ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_pack": (_int, [_vp, _u64, _i64, _vp, ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_unpack": (_int, [_vp, _u64, _i64, _vp, ctypes.POINTER(_vp)]),
+    "kvx_weight_sync_total_bytes": (_i64, [_vp]),
+    "kvx_weight_sync_host_base": (_u64, [_vp]),
+    "kvx_weight_sync_host_buffer": (_int, [_vp, _i64, _i64, _u64p, _i64p, _i64p]),
+    "kvx_weight_sync_wait": (_int, [_vp]),
+    "kvx_weight_sync_kernel_times": (_int, [_vp, _i32, _i32, _i64p,
+                                            ctypes.POINTER(ctypes.c_double), _i64p]),
+    "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
+                                ctypes.POINTER(_vp)]),
 }
 
 _lib = None

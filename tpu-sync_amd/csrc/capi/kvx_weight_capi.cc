@@ -1,0 +1,153 @@
+// extern "C" layer over the weight synchronizer and the strided-entry copy.
+#include <memory>
+#include <vector>
+
+#include "../host/weight_synchronizer.h"
+#include "capi_internal.h"
+
+struct kvx_weight_sync {
+  std::unique_ptr<kvx::WeightSynchronizer> impl;
+};
+
+namespace {
+
+using kvx_capi::BadArray;
+using kvx_capi::Done;
+using kvx_capi::Fail;
+
+int Emit(kvx::StatusOr<kvx::CopyFuture> r, kvx_future** out) {
+  if (!r.ok()) return Fail(r.status());
+  *out = new kvx_future{std::move(r).value()};
+  return KVX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** out) {
+  if (cfg == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null config or output");
+  *out = nullptr;
+  if (cfg->num_layers < 0 || cfg->num_shards <= 0) {
+    return Fail(KVX_INVALID_ARGUMENT, "num_layers must be >= 0 and num_shards >= 1");
+  }
+  const int64_t n = cfg->num_layers * cfg->num_shards;
+  if (BadArray(cfg->device_ptrs, n) || BadArray(cfg->device_bytes, n)) {
+    return Fail(KVX_INVALID_ARGUMENT, "null device_ptrs or device_bytes");
+  }
+  kvx::WeightSyncConfig c;
+  c.device = cfg->device;
+  c.num_layers = cfg->num_layers;
+  c.num_shards = cfg->num_shards;
+  c.device_ptrs.assign(cfg->device_ptrs, cfg->device_ptrs + n);
+  c.device_bytes.assign(cfg->device_bytes, cfg->device_bytes + n);
+  if (cfg->host_alloc != KVX_HOST_PINNED && cfg->host_alloc != KVX_HOST_MALLOC) {
+    return Fail(KVX_INVALID_ARGUMENT, "weight sync host memory must be pinned or malloc");
+  }
+  c.host_alloc = static_cast<kvx::HostAllocKind>(cfg->host_alloc);
+  if (cfg->chunk_bytes > 0) c.chunk_bytes = cfg->chunk_bytes;
+  if (cfg->staging_chunks > 0) c.staging_chunks = static_cast<int>(cfg->staging_chunks);
+  c.profile_kernels = cfg->profile_kernels != 0;
+  auto r = kvx::WeightSynchronizer::Create(std::move(c));
+  if (!r.ok()) return Fail(r.status());
+  *out = new kvx_weight_sync{std::move(r).value()};
+  return KVX_OK;
+}
+
+void kvx_weight_sync_destroy(kvx_weight_sync* w) { delete w; }
+
+int kvx_weight_sync_d2h(kvx_weight_sync* w, void* stream, kvx_future** out) {
+  if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(w->impl->D2h(static_cast<hipStream_t>(stream)), out);
+}
+
+int kvx_weight_sync_h2d(kvx_weight_sync* w, void* stream, kvx_future** out) {
+  if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(w->impl->H2d(static_cast<hipStream_t>(stream)), out);
+}
+
+int kvx_weight_sync_d2h_layer(kvx_weight_sync* w, int64_t layer, void* stream,
+                              kvx_future** out) {
+  if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(w->impl->D2hLayer(layer, static_cast<hipStream_t>(stream)), out);
+}
+
+int kvx_weight_sync_h2d_layer(kvx_weight_sync* w, int64_t layer, void* stream,
+                              kvx_future** out) {
+  if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(w->impl->H2dLayer(layer, static_cast<hipStream_t>(stream)), out);
+}
+
+int kvx_weight_sync_pack(kvx_weight_sync* w, uint64_t staging, int64_t staging_bytes,
+                         void* stream, kvx_future** out) {
+  if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(w->impl->Pack(staging, staging_bytes, static_cast<hipStream_t>(stream)), out);
+}
+
+int kvx_weight_sync_unpack(kvx_weight_sync* w, uint64_t staging, int64_t staging_bytes,
+                           void* stream, kvx_future** out) {
+  if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(w->impl->Unpack(staging, staging_bytes, static_cast<hipStream_t>(stream)), out);
+}
+
+int64_t kvx_weight_sync_total_bytes(const kvx_weight_sync* w) {
+  return w == nullptr ? 0 : w->impl->total_bytes();
+}
+
+int kvx_weight_sync_host_buffer(kvx_weight_sync* w, int64_t layer, int64_t shard,
+                                uint64_t* out_ptr, int64_t* out_bytes, int64_t* out_offset) {
+  if (w == nullptr || out_ptr == nullptr || out_bytes == nullptr || out_offset == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  }
+  if (layer < 0 || layer >= w->impl->num_layers() || shard < 0 ||
+      shard >= w->impl->num_shards()) {
+    return Fail(KVX_OUT_OF_RANGE, "layer or shard index out of range");
+  }
+  *out_offset = w->impl->offset(layer, shard);
+  *out_ptr = reinterpret_cast<uint64_t>(w->impl->host_base() + *out_offset);
+  *out_bytes = w->impl->size(layer, shard);
+  return KVX_OK;
+}
+
+uint64_t kvx_weight_sync_host_base(const kvx_weight_sync* w) {
+  return w == nullptr ? 0 : reinterpret_cast<uint64_t>(w->impl->host_base());
+}
+
+int kvx_weight_sync_wait(kvx_weight_sync* w) {
+  if (w == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle");
+  return Done(w->impl->Synchronize());
+}
+
+int kvx_weight_sync_kernel_times(kvx_weight_sync* w, int32_t pack, int32_t reset,
+                                 int64_t* out_launches, double* out_ms, int64_t* out_bytes) {
+  if (w == nullptr || out_launches == nullptr || out_ms == nullptr || out_bytes == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  }
+  return Done(w->impl->KernelTimes(pack != 0, reset != 0, out_launches, out_ms, out_bytes));
+}
+
+int kvx_copy_strided(int32_t device, const kvx_strided_entry* entries, int64_t n,
+                     void* stream, kvx_future** out) {
+  if (out == nullptr || BadArray(entries, n)) return Fail(KVX_INVALID_ARGUMENT, "bad arguments");
+  std::vector<kvx::StridedCopy> copies(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) {
+    const kvx_strided_entry& e = entries[i];
+    if (e.size_bytes <= 0 || e.src_stride_bytes < 0 || e.dst_stride_bytes < 0) {
+      return Fail(KVX_INVALID_ARGUMENT, "entry sizes and strides must be non-negative, size > 0");
+    }
+    const int64_t count = e.count > 0 ? e.count : 1;
+    // Rows of one entry must not overlap in the destination.
+    if (count > 1 && e.dst_stride_bytes < e.size_bytes) {
+      return Fail(KVX_INVALID_ARGUMENT, "destination rows overlap (dst_stride < size)");
+    }
+    copies[i].src = e.src + static_cast<uint64_t>(e.src_offset_bytes);
+    copies[i].dst = e.dst + static_cast<uint64_t>(e.dst_offset_bytes);
+    copies[i].size = e.size_bytes;
+    copies[i].count = count;
+    copies[i].src_stride = e.src_stride_bytes;
+    copies[i].dst_stride = e.dst_stride_bytes;
+  }
+  return Emit(kvx::CopyStridedOnDevice(device, copies, static_cast<hipStream_t>(stream)), out);
+}
+
+}  // extern "C"

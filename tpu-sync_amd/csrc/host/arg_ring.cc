@@ -1,0 +1,88 @@
+#include "arg_ring.h"
+
+#include <algorithm>
+
+#include "hip_util.h"
+
+namespace kvx {
+namespace {
+constexpr int64_t kAlign = 256;
+int64_t AlignUp(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+}  // namespace
+
+ArgRing::~ArgRing() {
+  for (Slice& s : inflight_) {
+    (void)hipEventSynchronize(s.done);
+    (void)hipEventDestroy(s.done);
+  }
+  if (host_ != nullptr) (void)hipHostFree(host_);
+  if (dev_ != 0) (void)hipFree(reinterpret_cast<void*>(dev_));
+}
+
+Status ArgRing::Init(int64_t bytes) { return Grow(bytes); }
+
+Status ArgRing::Grow(int64_t bytes) {
+  for (Slice& s : inflight_) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(s.done));
+    (void)hipEventDestroy(s.done);
+  }
+  inflight_.clear();
+  if (host_ != nullptr) (void)hipHostFree(host_);
+  if (dev_ != 0) (void)hipFree(reinterpret_cast<void*>(dev_));
+  host_ = nullptr;
+  dev_ = 0;
+  const int64_t size = AlignUp(std::max(bytes, size_ * 2));
+  void* h = nullptr;
+  void* d = nullptr;
+  KVX_HIP_RETURN_IF_ERROR(hipHostMalloc(&h, size, hipHostMallocDefault));
+  KVX_HIP_RETURN_IF_ERROR(hipMalloc(&d, size));
+  host_ = static_cast<uint8_t*>(h);
+  dev_ = reinterpret_cast<uint64_t>(d);
+  size_ = size;
+  head_ = 0;
+  return OkStatus();
+}
+
+StatusOr<int64_t> ArgRing::Alloc(int64_t bytes) {
+  bytes = AlignUp(std::max<int64_t>(bytes, 1));
+  if (bytes > size_) KVX_RETURN_IF_ERROR(Grow(bytes));
+  int64_t start = head_;
+  if (start + bytes > size_) start = 0;
+  const int64_t end = start + bytes;
+  for (auto it = inflight_.begin(); it != inflight_.end();) {
+    const bool overlap = it->begin < end && start < it->end;
+    hipError_t q = hipEventQuery(it->done);
+    if (q == hipErrorNotReady && overlap) {
+      KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(it->done));
+      q = hipSuccess;
+    }
+    if (q == hipErrorNotReady) {
+      ++it;
+      continue;
+    }
+    (void)hipEventDestroy(it->done);
+    it = inflight_.erase(it);
+  }
+  head_ = end;
+  return start;
+}
+
+Status ArgRing::Upload(int64_t off, int64_t bytes, hipStream_t stream) {
+  KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(dev_ + off), host_ + off,
+                                         bytes, hipMemcpyHostToDevice, stream));
+  return OkStatus();
+}
+
+Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {
+  hipEvent_t e = nullptr;
+  KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  Status st = HipStatus(hipEventRecord(e, stream), "hipEventRecord(arg ring)");
+  if (!st.ok()) {
+    (void)hipEventDestroy(e);
+    return st;
+  }
+  inflight_.push_back(Slice{off, off + AlignUp(bytes), e});
+  return OkStatus();
+}
+
+}  // namespace kvx

@@ -1,0 +1,55 @@
+// Pinned-host + device ring for kernel argument tables.
+//
+// A launch writes its table into the pinned half, uploads it with one
+// hipMemcpyAsync on the launching stream and records an event after the
+// launch; a region is handed out again only once the event that last read it
+// has completed (the host waits only when the ring wraps onto unfinished
+// work). Not thread-safe: the owner serialises calls.
+#ifndef KVX_HOST_ARG_RING_H_
+#define KVX_HOST_ARG_RING_H_
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <deque>
+
+#include "status.h"
+
+namespace kvx {
+
+class ArgRing {
+ public:
+  ArgRing() = default;
+  ~ArgRing();
+  ArgRing(const ArgRing&) = delete;
+  ArgRing& operator=(const ArgRing&) = delete;
+
+  Status Init(int64_t bytes);
+  // Reserves `bytes` (256-aligned); returns the offset. Grows the ring
+  // (after draining it) when a request is larger than the ring.
+  StatusOr<int64_t> Alloc(int64_t bytes);
+  uint8_t* host(int64_t off) const { return host_ + off; }
+  uint64_t dev(int64_t off) const { return dev_ + static_cast<uint64_t>(off); }
+  // Uploads [off, off + bytes) on `stream`.
+  Status Upload(int64_t off, int64_t bytes, hipStream_t stream);
+  // Marks [off, off + bytes) in use until the work now enqueued on `stream`
+  // finishes.
+  Status Commit(int64_t off, int64_t bytes, hipStream_t stream);
+
+ private:
+  struct Slice {
+    int64_t begin;
+    int64_t end;
+    hipEvent_t done;
+  };
+  Status Grow(int64_t bytes);
+  uint8_t* host_ = nullptr;
+  uint64_t dev_ = 0;
+  int64_t size_ = 0;
+  int64_t head_ = 0;
+  std::deque<Slice> inflight_;
+};
+
+}  // namespace kvx
+
+#endif  // KVX_HOST_ARG_RING_H_

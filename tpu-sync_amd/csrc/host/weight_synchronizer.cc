@@ -1,0 +1,344 @@
+#include "weight_synchronizer.h"
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+
+#include "hip_util.h"
+
+namespace kvx {
+namespace {
+
+constexpr int64_t kTensorAlign = 256;
+
+int64_t AlignUp(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Uploads the table and tile map of `copies` through `ring` and launches the
+// kernel on `stream`; the ring region stays reserved until the launch ends.
+Status LaunchThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
+                         hipStream_t stream) {
+  if (copies.empty()) return OkStatus();
+  const int vec = StridedVectorBytes(copies);
+  std::vector<StridedEntryDev> table;
+  uint32_t grid = 0;
+  if (!BuildStridedTable(copies, vec, &table, &grid)) {
+    return InvalidArgumentError("strided copy entry out of the kernel's limits");
+  }
+  const int64_t tbytes = static_cast<int64_t>(table.size() * sizeof(StridedEntryDev));
+  const int64_t bytes = tbytes + static_cast<int64_t>(grid) * 4;
+  KVX_ASSIGN_OR_RETURN(int64_t off, ring.Alloc(bytes));
+  std::memcpy(ring.host(off), table.data(), static_cast<size_t>(tbytes));
+  uint32_t* map = reinterpret_cast<uint32_t*>(ring.host(off) + tbytes);
+  for (size_t e = 0; e < table.size(); ++e) {
+    const uint32_t end = e + 1 < table.size() ? table[e + 1].tile_begin : grid;
+    for (uint32_t t = table[e].tile_begin; t < end; ++t) map[t] = static_cast<uint32_t>(e);
+  }
+  KVX_RETURN_IF_ERROR(ring.Upload(off, bytes, stream));
+  KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
+      reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
+      static_cast<uint32_t>(table.size()), grid, vec, stream));
+  return ring.Commit(off, bytes, stream);
+}
+
+StatusOr<hipEvent_t> NewEvent() {
+  hipEvent_t e = nullptr;
+  KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  return e;
+}
+
+}  // namespace
+
+StatusOr<std::unique_ptr<WeightSynchronizer>> WeightSynchronizer::Create(
+    WeightSyncConfig cfg) {
+  std::unique_ptr<WeightSynchronizer> w(new WeightSynchronizer(std::move(cfg)));
+  KVX_RETURN_IF_ERROR(w->Init());
+  return w;
+}
+
+Status WeightSynchronizer::Init() {
+  const int64_t n = cfg_.num_layers * cfg_.num_shards;
+  if (cfg_.num_layers < 0 || cfg_.num_shards <= 0) {
+    return InvalidArgumentError("num_layers must be >= 0 and num_shards >= 1");
+  }
+  if (static_cast<int64_t>(cfg_.device_ptrs.size()) != n ||
+      static_cast<int64_t>(cfg_.device_bytes.size()) != n) {
+    return InvalidArgumentError("device_ptrs and device_bytes need num_layers * num_shards entries");
+  }
+  if (cfg_.chunk_bytes <= 0 || cfg_.staging_chunks <= 0) {
+    return InvalidArgumentError("staging chunk size and count must be positive");
+  }
+  off_.resize(n);
+  int64_t pos = 0;
+  for (int64_t k = 0; k < n; ++k) {
+    if (cfg_.device_bytes[k] < 0 || (cfg_.device_bytes[k] > 0 && cfg_.device_ptrs[k] == 0)) {
+      return InvalidArgumentError("null device pointer or negative size");
+    }
+    off_[k] = pos;
+    pos = AlignUp(pos + cfg_.device_bytes[k], kTensorAlign);
+  }
+  total_ = pos;
+  DeviceGuard g(cfg_.device);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  switch (cfg_.host_alloc) {
+    case HostAllocKind::kPinned: {
+      KVX_ASSIGN_OR_RETURN(host_, AllocatePinnedHost(static_cast<size_t>(total_), cfg_.device));
+      break;
+    }
+    case HostAllocKind::kMalloc: {
+      KVX_ASSIGN_OR_RETURN(host_, AllocateMallocHost(static_cast<size_t>(total_)));
+      break;
+    }
+    default:
+      return UnimplementedError("weight sync host memory must be pinned or malloc");
+  }
+  for (hipStream_t* s : {&ks_, &d2h_, &h2d_}) {
+    KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(s, hipStreamNonBlocking));
+  }
+  const int64_t chunk = std::min<int64_t>(cfg_.chunk_bytes, std::max<int64_t>(total_, 1));
+  cfg_.chunk_bytes = chunk;
+  for (int k = 0; k < cfg_.staging_chunks; ++k) {
+    void* p = nullptr;
+    KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, chunk));
+    ring_.push_back(reinterpret_cast<uint64_t>(p));
+    KVX_ASSIGN_OR_RETURN(hipEvent_t r, NewEvent());
+    KVX_ASSIGN_OR_RETURN(hipEvent_t f, NewEvent());
+    ready_.push_back(r);
+    free_.push_back(f);
+    used_.push_back(false);
+  }
+  return args_.Init(1 << 20);
+}
+
+WeightSynchronizer::~WeightSynchronizer() {
+  DeviceGuard g(cfg_.device);
+  (void)Synchronize();
+  for (Sample& s : samples_) {
+    (void)hipEventDestroy(s.start);
+    (void)hipEventDestroy(s.stop);
+  }
+  for (uint64_t b : ring_) (void)hipFree(reinterpret_cast<void*>(b));
+  for (hipEvent_t e : ready_) (void)hipEventDestroy(e);
+  for (hipEvent_t e : free_) (void)hipEventDestroy(e);
+  for (hipStream_t s : {ks_, d2h_, h2d_}) {
+    if (s != nullptr) (void)hipStreamDestroy(s);
+  }
+}
+
+Status WeightSynchronizer::Synchronize() {
+  for (hipStream_t s : {ks_, d2h_, h2d_}) {
+    if (s != nullptr) KVX_HIP_RETURN_IF_ERROR(hipStreamSynchronize(s));
+  }
+  return OkStatus();
+}
+
+Status WeightSynchronizer::WaitDep(hipStream_t dep, hipStream_t on) {
+  if (dep == nullptr) return OkStatus();
+  KVX_ASSIGN_OR_RETURN(hipEvent_t e, NewEvent());
+  Status st = HipStatus(hipEventRecord(e, dep), "hipEventRecord(dep)");
+  if (st.ok()) st = HipStatus(hipStreamWaitEvent(on, e, 0), "hipStreamWaitEvent");
+  (void)hipEventDestroy(e);
+  return st;
+}
+
+void WeightSynchronizer::RangeEntries(int64_t lo, int64_t hi, uint64_t image, bool pack,
+                                      std::vector<StridedCopy>* out) const {
+  out->clear();
+  // Tensors are laid out in ascending offset order: find the first one that
+  // ends after lo.
+  const int64_t n = static_cast<int64_t>(off_.size());
+  int64_t k = std::upper_bound(off_.begin(), off_.end(), lo) - off_.begin() - 1;
+  if (k < 0) k = 0;
+  for (; k < n && off_[k] < hi; ++k) {
+    const int64_t a = std::max(lo, off_[k]);
+    const int64_t b = std::min(hi, off_[k] + cfg_.device_bytes[k]);
+    if (a >= b) continue;
+    StridedCopy c;
+    const uint64_t dev = cfg_.device_ptrs[k] + static_cast<uint64_t>(a - off_[k]);
+    const uint64_t img = image + static_cast<uint64_t>(a - lo);
+    c.src = pack ? dev : img;
+    c.dst = pack ? img : dev;
+    c.size = b - a;
+    c.count = 1;
+    out->push_back(c);
+  }
+}
+
+Status WeightSynchronizer::Launch(const std::vector<StridedCopy>& copies, bool pack,
+                                  hipStream_t stream) {
+  Sample s;
+  if (cfg_.profile_kernels) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.start));
+    KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.stop));
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.start, stream));
+  }
+  KVX_RETURN_IF_ERROR(LaunchThroughRing(args_, copies, stream));
+  if (cfg_.profile_kernels) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.stop, stream));
+    for (const StridedCopy& c : copies) s.bytes += c.size * (c.count > 0 ? c.count : 1);
+    s.pack = pack;
+    samples_.push_back(s);
+  }
+  return OkStatus();
+}
+
+Status WeightSynchronizer::KernelTimes(bool pack, bool reset, int64_t* launches, double* ms,
+                                       int64_t* bytes) {
+  std::lock_guard<std::mutex> l(mu_);
+  *launches = 0;
+  *ms = 0;
+  *bytes = 0;
+  std::vector<Sample> keep;
+  for (Sample& s : samples_) {
+    if (s.pack != pack) {
+      keep.push_back(s);
+      continue;
+    }
+    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(s.stop));
+    float t = 0;
+    KVX_HIP_RETURN_IF_ERROR(hipEventElapsedTime(&t, s.start, s.stop));
+    ++*launches;
+    *ms += t;
+    *bytes += s.bytes;
+    if (reset) {
+      (void)hipEventDestroy(s.start);
+      (void)hipEventDestroy(s.stop);
+    } else {
+      keep.push_back(s);
+    }
+  }
+  samples_.swap(keep);
+  return OkStatus();
+}
+
+StatusOr<CopyFuture> WeightSynchronizer::Chunked(bool d2h, hipStream_t dep) {
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(cfg_.device);
+  if (total_ == 0) return CopyFuture();
+  hipStream_t cs = d2h ? d2h_ : h2d_;
+  // The kernel stream reads (pack) or writes (unpack) the tensors, so it is
+  // ordered after the caller's work; so is the copy stream.
+  KVX_RETURN_IF_ERROR(WaitDep(dep, ks_));
+  KVX_RETURN_IF_ERROR(WaitDep(dep, cs));
+  const int64_t C = cfg_.chunk_bytes;
+  std::vector<StridedCopy> entries;
+  for (int64_t lo = 0; lo < total_; lo += C) {
+    const int64_t hi = std::min(total_, lo + C);
+    const size_t k = next_;
+    next_ = (next_ + 1) % ring_.size();
+    const uint64_t buf = ring_[k];
+    RangeEntries(lo, hi, buf, /*pack=*/d2h, &entries);
+    if (d2h) {
+      if (used_[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks_, free_[k], 0));
+      KVX_RETURN_IF_ERROR(Launch(entries, true, ks_));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ready_[k], ks_));
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ready_[k], 0));
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host_.ptr + lo, reinterpret_cast<void*>(buf),
+                                             static_cast<size_t>(hi - lo),
+                                             hipMemcpyDeviceToHost, cs));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(free_[k], cs));
+    } else {
+      if (used_[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, free_[k], 0));
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(buf), host_.ptr + lo,
+                                             static_cast<size_t>(hi - lo),
+                                             hipMemcpyHostToDevice, cs));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ready_[k], cs));
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks_, ready_[k], 0));
+      KVX_RETURN_IF_ERROR(Launch(entries, false, ks_));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(free_[k], ks_));
+    }
+    used_[k] = true;
+  }
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, d2h ? cs : ks_));
+  return CopyFuture::FromEvents({done}, {host_.owner});
+}
+
+StatusOr<CopyFuture> WeightSynchronizer::D2h(hipStream_t dep) { return Chunked(true, dep); }
+StatusOr<CopyFuture> WeightSynchronizer::H2d(hipStream_t dep) { return Chunked(false, dep); }
+
+StatusOr<CopyFuture> WeightSynchronizer::D2hLayer(int64_t layer, hipStream_t dep) {
+  if (layer < 0 || layer >= cfg_.num_layers) return CopyFuture();
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(cfg_.device);
+  KVX_RETURN_IF_ERROR(WaitDep(dep, d2h_));
+  for (int64_t s = 0; s < cfg_.num_shards; ++s) {
+    const int64_t k = layer * cfg_.num_shards + s;
+    if (cfg_.device_bytes[k] == 0) continue;
+    KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host_.ptr + off_[k],
+                                           reinterpret_cast<void*>(cfg_.device_ptrs[k]),
+                                           static_cast<size_t>(cfg_.device_bytes[k]),
+                                           hipMemcpyDeviceToHost, d2h_));
+  }
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, d2h_));
+  return CopyFuture::FromEvents({done}, {host_.owner});
+}
+
+StatusOr<CopyFuture> WeightSynchronizer::H2dLayer(int64_t layer, hipStream_t dep) {
+  if (layer < 0 || layer >= cfg_.num_layers) return CopyFuture();
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(cfg_.device);
+  KVX_RETURN_IF_ERROR(WaitDep(dep, h2d_));
+  for (int64_t s = 0; s < cfg_.num_shards; ++s) {
+    const int64_t k = layer * cfg_.num_shards + s;
+    if (cfg_.device_bytes[k] == 0) continue;
+    KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(cfg_.device_ptrs[k]),
+                                           host_.ptr + off_[k],
+                                           static_cast<size_t>(cfg_.device_bytes[k]),
+                                           hipMemcpyHostToDevice, h2d_));
+  }
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, h2d_));
+  return CopyFuture::FromEvents({done}, {host_.owner});
+}
+
+StatusOr<CopyFuture> WeightSynchronizer::WholeCopy(bool pack, uint64_t staging, int64_t bytes,
+                                                   hipStream_t stream) {
+  if (staging == 0 || bytes < total_) {
+    return InvalidArgumentError("staging buffer smaller than the packed parameter set (" +
+                                std::to_string(total_) + " bytes)");
+  }
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(cfg_.device);
+  std::vector<StridedCopy> entries;
+  RangeEntries(0, total_, staging, pack, &entries);
+  KVX_RETURN_IF_ERROR(Launch(entries, pack, stream));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
+  return CopyFuture::FromEvents({done}, {});
+}
+
+StatusOr<CopyFuture> WeightSynchronizer::Pack(uint64_t staging, int64_t bytes,
+                                              hipStream_t stream) {
+  return WholeCopy(true, staging, bytes, stream);
+}
+
+StatusOr<CopyFuture> WeightSynchronizer::Unpack(uint64_t staging, int64_t bytes,
+                                                hipStream_t stream) {
+  return WholeCopy(false, staging, bytes, stream);
+}
+
+StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCopy>& copies,
+                                         hipStream_t stream) {
+  static std::mutex mu;
+  static std::map<int, ArgRing*>* rings = new std::map<int, ArgRing*>();
+  std::lock_guard<std::mutex> l(mu);
+  DeviceGuard g(device);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  ArgRing*& ring = (*rings)[device];
+  if (ring == nullptr) {
+    auto* r = new ArgRing();
+    Status st = r->Init(1 << 20);
+    if (!st.ok()) {
+      delete r;
+      return st;
+    }
+    ring = r;
+  }
+  KVX_RETURN_IF_ERROR(LaunchThroughRing(*ring, copies, stream));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
+  return CopyFuture::FromEvents({done}, {});
+}
+
+}  // namespace kvx

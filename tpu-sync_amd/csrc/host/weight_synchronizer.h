@@ -1,0 +1,118 @@
+// Weight sync on one GPU: the host-staging half of the reference's
+// WeightSynchronizerBase (tpu_sync/weight_sync/weight_synchronizer_base.h:
+// 78-240; D2h / D2hLayer / H2d / H2dLayer at
+// weight_synchronizer_base.cc:307-539) for row-major GPU tensors.
+//
+// Each (layer, shard) is one device tensor ("layer" = one weight). Their host
+// copies live in ONE pinned buffer at a per-tensor offset table (ascending,
+// 256-byte aligned; bytes between tensors are unspecified), so the whole
+// parameter set moves as a few large DMAs:
+//   * D2h: the offset-table pack kernel gathers the scattered tensors chunk by
+//     chunk into a device staging ring; each chunk crosses PCIe as one
+//     hipMemcpyAsync while the next chunk is packed;
+//   * H2d: the mirror image (one H2D per chunk, then the unpack kernel);
+//   * D2hLayer / H2dLayer: one direct copy per shard of that weight, as the
+//     reference issues.
+// Pack / Unpack run the same kernel against a caller device buffer laid out
+// by the offset table (device-side contiguous staging), and CopyStrided runs
+// arbitrary strided push entries (column-split resharding) on the device.
+// TPU tiled layouts do not exist here, so there is no tile/detile step.
+#ifndef KVX_HOST_WEIGHT_SYNCHRONIZER_H_
+#define KVX_HOST_WEIGHT_SYNCHRONIZER_H_
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+#include "../kernels/strided_copy.h"
+#include "arg_ring.h"
+#include "copy_future.h"
+#include "host_allocator.h"
+#include "status.h"
+
+namespace kvx {
+
+struct WeightSyncConfig {
+  int device = 0;
+  int64_t num_layers = 0;
+  int64_t num_shards = 1;
+  std::vector<uint64_t> device_ptrs;  // [layer * num_shards + shard]
+  std::vector<int64_t> device_bytes;
+  HostAllocKind host_alloc = HostAllocKind::kPinned;
+  int64_t chunk_bytes = 256ll << 20;  // device staging chunk
+  int staging_chunks = 2;
+  bool profile_kernels = false;
+};
+
+class WeightSynchronizer {
+ public:
+  static StatusOr<std::unique_ptr<WeightSynchronizer>> Create(WeightSyncConfig cfg);
+  ~WeightSynchronizer();
+
+  StatusOr<CopyFuture> D2h(hipStream_t dep = nullptr);
+  StatusOr<CopyFuture> H2d(hipStream_t dep = nullptr);
+  StatusOr<CopyFuture> D2hLayer(int64_t layer, hipStream_t dep = nullptr);
+  StatusOr<CopyFuture> H2dLayer(int64_t layer, hipStream_t dep = nullptr);
+  // Device-side pack of every tensor into `staging` at its offset (and the
+  // reverse); staging must hold total_bytes().
+  StatusOr<CopyFuture> Pack(uint64_t staging, int64_t staging_bytes, hipStream_t stream);
+  StatusOr<CopyFuture> Unpack(uint64_t staging, int64_t staging_bytes, hipStream_t stream);
+
+  int64_t num_layers() const { return cfg_.num_layers; }
+  int64_t num_shards() const { return cfg_.num_shards; }
+  int64_t total_bytes() const { return total_; }
+  int64_t offset(int64_t layer, int64_t shard) const { return off_[layer * cfg_.num_shards + shard]; }
+  int64_t size(int64_t layer, int64_t shard) const { return cfg_.device_bytes[layer * cfg_.num_shards + shard]; }
+  uint8_t* host_base() const { return host_.ptr; }
+  Status Synchronize();
+  // Profiled pack (pack = true) or unpack kernel launches: count, summed
+  // milliseconds (HIP events on the kernel stream), bytes moved.
+  Status KernelTimes(bool pack, bool reset, int64_t* launches, double* ms, int64_t* bytes);
+
+ private:
+  explicit WeightSynchronizer(WeightSyncConfig cfg) : cfg_(std::move(cfg)) {}
+  Status Init();
+  StatusOr<CopyFuture> Chunked(bool d2h, hipStream_t dep);
+  StatusOr<CopyFuture> WholeCopy(bool pack, uint64_t staging, int64_t bytes,
+                                 hipStream_t stream);
+  // Entries for packed range [lo, hi) with the image placed at `image`
+  // (pack: tensors -> image; unpack: image -> tensors).
+  void RangeEntries(int64_t lo, int64_t hi, uint64_t image, bool pack,
+                    std::vector<StridedCopy>* out) const;
+  Status Launch(const std::vector<StridedCopy>& copies, bool pack, hipStream_t stream);
+  Status WaitDep(hipStream_t dep, hipStream_t on);
+
+  struct Sample {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+    int64_t bytes = 0;
+    bool pack = true;
+  };
+
+  WeightSyncConfig cfg_;
+  std::vector<int64_t> off_;
+  int64_t total_ = 0;
+  HostBufferAllocation host_;
+  std::mutex mu_;
+  hipStream_t ks_ = nullptr;
+  hipStream_t d2h_ = nullptr;
+  hipStream_t h2d_ = nullptr;
+  std::vector<uint64_t> ring_;
+  std::vector<hipEvent_t> ready_, free_;
+  std::vector<bool> used_;
+  size_t next_ = 0;
+  ArgRing args_;
+  std::vector<Sample> samples_;
+};
+
+// Runs arbitrary strided entries with device addresses in one launch on
+// `stream` (no synchronizer needed); returns a future for the launch.
+StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCopy>& copies,
+                                         hipStream_t stream);
+
+}  // namespace kvx
+
+#endif  // KVX_HOST_WEIGHT_SYNCHRONIZER_H_

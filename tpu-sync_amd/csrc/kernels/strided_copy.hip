@@ -1,0 +1,177 @@
+// Strided-entry copy for gfx950 (MI355X): per-tensor offset-table pack /
+// unpack and column splits of row-major weights, any number of entries per
+// launch.
+//
+// Pure data movement, bound by HBM bandwidth. Work is cut into tiles of
+// kTileVecs vectors (32 KiB at 16-byte vectors); a workgroup of 256 lanes
+// moves one tile with kUnroll independent loads in flight per lane before
+// its stores, the pattern that keeps HBM busy. A tile is either a run of
+// whole rows of one entry (short rows, e.g. the 1-3.5 KiB row chunks of a
+// column split) or a slice of one long row (a whole tensor is one row).
+// The tile -> entry map and the entry table are read with workgroup-uniform
+// scalar loads; lanes find their row with a multiply-shift instead of a
+// division. Loads and stores are non-temporal (every byte is touched once).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "strided_copy.h"
+
+namespace kvx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+constexpr uint32_t kTileVecs = kThreads * kUnroll;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define KVX_GLOBAL __attribute__((address_space(1)))
+#define KVX_CONST __attribute__((address_space(4)))
+
+struct KArgs {
+  const StridedEntryDev* table;
+  const uint32_t* tile_entry;  // workgroup -> entry index
+};
+
+template <typename V>
+__global__ __launch_bounds__(kThreads) void strided_copy_kernel(KArgs a) {
+  const uint32_t wg = blockIdx.x;
+  const uint32_t e = ((const KVX_CONST uint32_t*)a.tile_entry)[wg];
+  const KVX_CONST StridedEntryDev* ent = (const KVX_CONST StridedEntryDev*)a.table + e;
+  const uint64_t src = ent->src;
+  const uint64_t dst = ent->dst;
+  const uint64_t sstride = ent->src_stride;
+  const uint64_t dstride = ent->dst_stride;
+  const uint32_t vecs = ent->vecs;
+  const uint32_t t = wg - ent->tile_begin;
+  uint32_t row0, nrows, v0, nv;
+  if (ent->rows_per_tile > 0) {
+    const uint32_t rpt = ent->rows_per_tile;
+    row0 = t * rpt;
+    const uint32_t left = ent->count - row0;
+    nrows = left < rpt ? left : rpt;
+    v0 = 0;
+    nv = vecs;
+  } else {
+    const uint32_t tpr = ent->tiles_per_row;
+    row0 = t / tpr;
+    v0 = (t - row0 * tpr) * kTileVecs;
+    const uint32_t left = vecs - v0;
+    nv = left < kTileVecs ? left : kTileVecs;
+    nrows = 1;
+  }
+  const uint32_t total = nrows * nv;
+  const uint32_t last = total - 1;
+  const uint64_t magic = ent->div_magic;
+  V r[kUnroll];
+  uint64_t doff[kUnroll];
+  // Every lane issues all kUnroll loads unconditionally (lanes past the end
+  // of the tile re-read its last vector), so the loads go out back to back;
+  // only the stores are predicated.
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    uint32_t k = threadIdx.x + u * kThreads;
+    k = k < total ? k : last;
+    // nrows == 1 whenever nv != vecs, so the row is 0 there.
+    const uint32_t row = nrows == 1 ? 0u : static_cast<uint32_t>((k * magic) >> 32);
+    const uint32_t v = k - row * nv;
+    const uint64_t r_abs = row0 + row;
+    const uint64_t col = static_cast<uint64_t>(v0 + v) * sizeof(V);
+    r[u] = __builtin_nontemporal_load((const KVX_GLOBAL V*)(src + r_abs * sstride + col));
+    doff[u] = r_abs * dstride + col;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    if (threadIdx.x + u * kThreads < total) {
+      __builtin_nontemporal_store(r[u], (KVX_GLOBAL V*)(dst + doff[u]));
+    }
+  }
+}
+
+}  // namespace
+
+int StridedVectorBytes(const std::vector<StridedCopy>& copies) {
+  uint64_t acc = 0;
+  for (const StridedCopy& c : copies) {
+    acc |= c.src | c.dst | static_cast<uint64_t>(c.size);
+    if (c.count > 1) {
+      acc |= static_cast<uint64_t>(c.src_stride) | static_cast<uint64_t>(c.dst_stride);
+    }
+  }
+  for (int v : {16, 8, 4, 2}) {
+    if ((acc & static_cast<uint64_t>(v - 1)) == 0) return v;
+  }
+  return 1;
+}
+
+bool BuildStridedTable(const std::vector<StridedCopy>& copies, int vec_bytes,
+                       std::vector<StridedEntryDev>* table, uint32_t* grid) {
+  table->clear();
+  uint64_t tiles = 0;
+  for (const StridedCopy& c : copies) {
+    const int64_t count = c.count > 0 ? c.count : 1;
+    if (c.size <= 0 || c.size % vec_bytes != 0 || c.src == 0 || c.dst == 0 ||
+        c.src_stride < 0 || c.dst_stride < 0 || count > UINT32_MAX) {
+      return false;
+    }
+    const uint64_t vecs = static_cast<uint64_t>(c.size) / vec_bytes;
+    if (vecs > UINT32_MAX) return false;
+    StridedEntryDev d{};
+    d.src = c.src;
+    d.dst = c.dst;
+    d.src_stride = static_cast<uint64_t>(c.src_stride);
+    d.dst_stride = static_cast<uint64_t>(c.dst_stride);
+    d.count = static_cast<uint32_t>(count);
+    d.vecs = static_cast<uint32_t>(vecs);
+    d.div_magic = (uint64_t{1} << 32) / vecs + 1;
+    d.tile_begin = static_cast<uint32_t>(tiles);
+    uint64_t t;
+    if (vecs <= kTileVecs) {
+      d.rows_per_tile = static_cast<uint32_t>(kTileVecs / vecs);
+      t = (static_cast<uint64_t>(count) + d.rows_per_tile - 1) / d.rows_per_tile;
+    } else {
+      d.tiles_per_row = static_cast<uint32_t>((vecs + kTileVecs - 1) / kTileVecs);
+      t = static_cast<uint64_t>(count) * d.tiles_per_row;
+    }
+    tiles += t;
+    if (tiles > INT32_MAX) return false;
+    table->push_back(d);
+  }
+  *grid = static_cast<uint32_t>(tiles);
+  return true;
+}
+
+hipError_t LaunchStridedCopy(const StridedEntryDev* table_dev, uint32_t n,
+                             uint32_t grid, int vec_bytes, hipStream_t stream) {
+  (void)n;
+  if (grid == 0) return hipSuccess;
+  KArgs a;
+  a.table = table_dev;
+  // The tile -> entry map follows the table in the same device allocation.
+  a.tile_entry = reinterpret_cast<const uint32_t*>(table_dev + n);
+  switch (vec_bytes) {
+    case 16:
+      hipLaunchKernelGGL(strided_copy_kernel<u32x4>, dim3(grid), dim3(kThreads), 0, stream, a);
+      break;
+    case 8:
+      hipLaunchKernelGGL(strided_copy_kernel<u32x2>, dim3(grid), dim3(kThreads), 0, stream, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL(strided_copy_kernel<uint32_t>, dim3(grid), dim3(kThreads), 0, stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL(strided_copy_kernel<uint16_t>, dim3(grid), dim3(kThreads), 0, stream, a);
+      break;
+    case 1:
+      hipLaunchKernelGGL(strided_copy_kernel<uint8_t>, dim3(grid), dim3(kThreads), 0, stream, a);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace kvx

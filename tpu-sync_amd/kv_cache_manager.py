@@ -169,6 +169,9 @@ class KVCacheManager:
         tpu_sync/core/utils.h:48-91), else "pinned".
       raiden_controller_address: joins the KVCacheStore whose controller
         has this address (in this process) as its transfer worker.
+      scale_tables: per-layer side tables with the same major dimension (for
+        an fp8 cache, [num_blocks, kv_heads] float32 scales); they are block
+        arrays num_kv_layers.. and move with every copy of the same block ids.
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
       The remaining reference arguments (ports, worker id, timeout,
       parallelism, unsafe_skip_buffer_lock) configure its networking, which
@@ -187,12 +190,19 @@ class KVCacheManager:
                  direct_min_bytes: int = 0, shm_key: Optional[str] = None,
                  shm_server_name: Optional[str] = None,
                  model_uid: Optional[str] = None, profile_kernels: bool = False,
-                 transfer_mode: str = "auto", zero_copy_workgroups: int = 0):
+                 transfer_mode: str = "auto", zero_copy_workgroups: int = 0,
+                 scale_tables: Optional[List[Any]] = None):
         if host_blocks_to_allocate is None:
             if max_blocks is None or num_slots is None:
                 raise ValueError("Must specify either (max_blocks, num_slots) or"
                                  " host_blocks_to_allocate.")
             host_blocks_to_allocate = max_blocks * num_slots
+        # Side tables (e.g. per-(block, head) fp8 scales, [major_dim, ...])
+        # travel with the KV payload: they become block arrays after the KV
+        # layers, so every copy and gather moves payload and scales of the
+        # same block ids together, in the same kernel launch.
+        self.num_kv_layers = len(kv_caches)
+        kv_caches = list(kv_caches) + list(scale_tables or [])
         layers, num_shards = _flatten_caches(kv_caches)
         ptrs, sizes = [], []
         major_dim = 0

@@ -1,0 +1,247 @@
+"""Weight synchronizer over libkvx (one MI355X).
+
+Mirrors the reference's Python surface (tpu_sync/api/torch/
+weight_synchronizer.py:19-140): ``WeightSynchronizer(device_tensors)`` over
+``[layers][shards]`` contiguous device tensors, ``d2h()`` / ``h2d()`` of the
+whole parameter set, ``get_host_buffer(layer, shard)`` as a zero-copy CPU
+tensor view, ``num_layers`` / ``num_shards`` / ``slice_byte_size``. The host
+copies share one pinned buffer laid out by a per-tensor offset table, and
+``d2h`` / ``h2d`` run the offset-table pack / unpack kernel through a device
+staging ring so the parameters cross PCIe as a few large DMAs.
+
+Resharding is the reference's strided push-entry expansion
+(tpu_sync/weight_sync/weight_synchronizer_base.cc:626-666) executed on the
+device: ``copy_strided(entries)`` runs any list of
+``(src, dst, size, count, src_stride, dst_stride)`` entries in one launch,
+and ``column_split_entries`` builds the entries of a column split whose
+bounds follow ``compute_nd_shard_slices`` (tpu_sync/kv_cache/
+nd_slice_math.py:23-70: equal tiles, remainder to the last shard).
+Networked pushes (push_weights, listeners) are out of scope.
+"""
+import ctypes
+import itertools
+from typing import Any, List, Optional, Sequence, Tuple
+
+from . import _capi
+from .kv_cache_manager import RaidenFuture, _stream_ptr
+
+
+def compute_nd_shard_slices(global_shape: Sequence[int], mesh_shape: Sequence[int]
+                            ) -> List[List[Tuple[int, int]]]:
+    """Per-shard [start, end) bounds of every dimension, shards in row-major
+    order; the last shard of a dimension takes the remainder."""
+    if len(global_shape) != len(mesh_shape):
+        raise ValueError(f"Tensor rank ({len(global_shape)}) and sharding mesh rank"
+                         f" ({len(mesh_shape)}) must match exactly.")
+    for d, m in enumerate(mesh_shape):
+        if m <= 0:
+            raise ValueError(f"Mesh shape at dimension {d} must be positive.")
+    tiles = [g // m for g, m in zip(global_shape, mesh_shape)]
+    out = []
+    for coord in itertools.product(*[range(m) for m in mesh_shape]):
+        box = []
+        for d, c in enumerate(coord):
+            start = c * tiles[d]
+            end = (c + 1) * tiles[d] if c < mesh_shape[d] - 1 else global_shape[d]
+            box.append((start, end))
+        out.append(box)
+    return out
+
+
+class StridedEntry:
+    """One strided push entry with device addresses."""
+
+    __slots__ = ("src", "dst", "size", "count", "src_stride", "dst_stride")
+
+    def __init__(self, src: int, dst: int, size: int, count: int = 1,
+                 src_stride: int = 0, dst_stride: int = 0):
+        self.src, self.dst, self.size = int(src), int(dst), int(size)
+        self.count, self.src_stride, self.dst_stride = int(count), int(src_stride), int(dst_stride)
+
+    def as_tuple(self):
+        return (self.src, self.dst, self.size, self.count, self.src_stride, self.dst_stride)
+
+
+def column_split_entries(weight, outputs: Sequence[Any]) -> List[StridedEntry]:
+    """Entries copying column chunk j of a row-major 2-D ``weight`` [R, C]
+    into contiguous ``outputs[j]`` ([R, C_j]); chunk bounds from
+    compute_nd_shard_slices((R, C), (1, k))."""
+    rows, cols = int(weight.shape[0]), int(weight.shape[1])
+    item = weight.element_size()
+    k = len(outputs)
+    bounds = compute_nd_shard_slices((rows, cols), (1, k))
+    entries = []
+    for j, box in enumerate(bounds):
+        c0, c1 = box[1]
+        out = outputs[j]
+        if tuple(out.shape) != (rows, c1 - c0) or not out.is_contiguous():
+            raise ValueError(f"output {j} must be a contiguous [{rows}, {c1 - c0}] tensor")
+        if c1 == c0 or rows == 0:
+            continue  # an empty chunk moves nothing
+        entries.append(StridedEntry(weight.data_ptr() + c0 * item, out.data_ptr(),
+                                    (c1 - c0) * item, rows, cols * item, (c1 - c0) * item))
+    return entries
+
+
+def copy_strided(entries: Sequence[StridedEntry], stream=None, device: int = 0,
+                 keep_alive=None) -> RaidenFuture:
+    """Runs every entry in one kernel launch on `stream` (default: torch's
+    current stream)."""
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream(device)
+    arr = (_capi.StridedEntryC * max(len(entries), 1))()
+    for i, e in enumerate(entries):
+        arr[i].src, arr[i].dst = e.src, e.dst
+        arr[i].src_offset_bytes = arr[i].dst_offset_bytes = 0
+        arr[i].size_bytes, arr[i].count = e.size, e.count
+        arr[i].src_stride_bytes, arr[i].dst_stride_bytes = e.src_stride, e.dst_stride
+    out = ctypes.c_void_p()
+    _capi.check(_capi.load().kvx_copy_strided(device, arr, len(entries),
+                                              ctypes.c_void_p(_stream_ptr(stream)),
+                                              ctypes.byref(out)), "copy_strided")
+    return RaidenFuture(out, keep_alive, "copy_strided")
+
+
+class WeightSynchronizer:
+    """Host staging of a model's weights (one device tensor per layer/shard)."""
+
+    def __init__(self, device_tensors: List[List[Any]], local_port: Optional[int] = None,
+                 parallelism: int = 1, listener_port: Optional[int] = None,
+                 bind_ip: Optional[str] = None, unsafe_skip_buffer_lock: bool = True,
+                 auto_h2d: bool = False, *, host_alloc: str = "pinned",
+                 chunk_bytes: int = 0, staging_chunks: int = 0,
+                 profile_kernels: bool = False):
+        del local_port, parallelism, listener_port, bind_ip, unsafe_skip_buffer_lock, auto_h2d
+        layers = [list(x) if isinstance(x, (list, tuple)) else [x] for x in device_tensors]
+        num_shards = len(layers[0]) if layers else 1
+        if any(len(s) != num_shards for s in layers):
+            raise RuntimeError("Number of shards mismatch across layers")
+        ptrs, sizes, device = [], [], 0
+        for shards in layers:
+            for t in shards:
+                if not t.is_contiguous():
+                    raise RuntimeError("weight tensors must be contiguous")
+                ptrs.append(t.data_ptr())
+                sizes.append(t.numel() * t.element_size())
+                device = t.device.index or 0
+        self._tensors = layers
+        self._device = device
+        cfg = _capi.WeightSyncConfig()
+        cfg.device = device
+        cfg.host_alloc = {"pinned": _capi.HOST_PINNED, "malloc": _capi.HOST_MALLOC}[host_alloc]
+        cfg.num_layers = len(layers)
+        cfg.num_shards = num_shards
+        self._ptr_arr = (ctypes.c_uint64 * max(len(ptrs), 1))(*ptrs)
+        self._size_arr = (ctypes.c_int64 * max(len(sizes), 1))(*sizes)
+        cfg.device_ptrs = self._ptr_arr
+        cfg.device_bytes = self._size_arr
+        cfg.chunk_bytes = chunk_bytes
+        cfg.staging_chunks = staging_chunks
+        cfg.profile_kernels = int(bool(profile_kernels))
+        h = ctypes.c_void_p()
+        _capi.check(_capi.load().kvx_weight_sync_create(ctypes.byref(cfg), ctypes.byref(h)),
+                    "WeightSynchronizer create")
+        self._h = h
+
+    def _fut(self, fn, where, *args, stream=None, keep=None):
+        out = ctypes.c_void_p()
+        _capi.check(fn(self._h, *args, ctypes.c_void_p(_stream_ptr(stream)),
+                       ctypes.byref(out)), where)
+        return RaidenFuture(out, keep if keep is not None else self, where)
+
+    def d2h(self, stream=None) -> RaidenFuture:
+        """Asynchronous copy of every weight to the host buffer."""
+        return self._fut(_capi.load().kvx_weight_sync_d2h, "WeightSynchronizer D2h",
+                         stream=stream)
+
+    def h2d(self, stream=None) -> RaidenFuture:
+        """Asynchronous copy of the host buffer back into every weight."""
+        return self._fut(_capi.load().kvx_weight_sync_h2d, "WeightSynchronizer H2d",
+                         stream=stream)
+
+    def d2h_layer(self, layer_idx: int, stream=None) -> RaidenFuture:
+        return self._fut(_capi.load().kvx_weight_sync_d2h_layer, "WeightSynchronizer D2hLayer",
+                         layer_idx, stream=stream)
+
+    def h2d_layer(self, layer_idx: int, stream=None) -> RaidenFuture:
+        return self._fut(_capi.load().kvx_weight_sync_h2d_layer, "WeightSynchronizer H2dLayer",
+                         layer_idx, stream=stream)
+
+    def pack(self, staging, stream=None) -> RaidenFuture:
+        """Packs every weight into a device tensor of total_bytes bytes laid
+        out by the offset table (one kernel launch)."""
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream(staging.device)
+        return self._fut(_capi.load().kvx_weight_sync_pack, "WeightSynchronizer pack",
+                         staging.data_ptr(), staging.numel() * staging.element_size(),
+                         stream=stream, keep=(self, staging))
+
+    def unpack(self, staging, stream=None) -> RaidenFuture:
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream(staging.device)
+        return self._fut(_capi.load().kvx_weight_sync_unpack, "WeightSynchronizer unpack",
+                         staging.data_ptr(), staging.numel() * staging.element_size(),
+                         stream=stream, keep=(self, staging))
+
+    def host_buffer_info(self, layer_idx: int = 0, shard_idx: int = 0) -> Tuple[int, int, int]:
+        """(host address, bytes, offset in the packed image) of one weight."""
+        p, n, o = ctypes.c_uint64(), ctypes.c_int64(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_weight_sync_host_buffer(
+            self._h, layer_idx, shard_idx, ctypes.byref(p), ctypes.byref(n), ctypes.byref(o)))
+        return p.value, n.value, o.value
+
+    def get_host_buffer(self, layer_idx: int = 0, shard_idx: int = 0):
+        """Zero-copy CPU tensor view of one weight's host copy (its dtype and
+        shape)."""
+        import torch
+        ptr, nbytes, _ = self.host_buffer_info(layer_idx, shard_idx)
+        t = self._tensors[layer_idx][shard_idx]
+        buf = (ctypes.c_uint8 * nbytes).from_address(ptr)
+        return torch.frombuffer(buf, dtype=torch.uint8).view(t.dtype).view(t.shape)
+
+    def host_image(self):
+        """numpy uint8 view of the whole packed host buffer."""
+        import numpy as np
+        lib = _capi.load()
+        base, total = lib.kvx_weight_sync_host_base(self._h), self.total_bytes
+        return np.ctypeslib.as_array((ctypes.c_uint8 * total).from_address(base))
+
+    @property
+    def total_bytes(self) -> int:
+        return _capi.load().kvx_weight_sync_total_bytes(self._h)
+
+    @property
+    def num_layers(self) -> int:
+        return len(self._tensors)
+
+    @property
+    def num_shards(self) -> int:
+        return len(self._tensors[0]) if self._tensors else 0
+
+    @property
+    def slice_byte_size(self) -> int:
+        t = self._tensors[0][0]
+        return t.numel() * t.element_size() // max(int(t.shape[0]), 1) if t.dim() else 0
+
+    def wait(self) -> None:
+        _capi.check(_capi.load().kvx_weight_sync_wait(self._h))
+
+    def kernel_times(self, pack: bool = True, reset: bool = False) -> dict:
+        n, ms, b = ctypes.c_int64(), ctypes.c_double(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_weight_sync_kernel_times(
+            self._h, int(pack), int(reset), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(b)))
+        return {"launches": n.value, "total_ms": ms.value, "bytes": b.value}
+
+    def push_weights(self, peers: List[str]) -> None:
+        raise NotImplementedError("networked weight pushes are not part of this build")
+
+    def close(self) -> None:
+        h, self._h = getattr(self, "_h", None), None
+        if h and _capi._lib is not None:
+            _capi._lib.kvx_weight_sync_destroy(h)
+
+    def __del__(self):
+        self.close()
