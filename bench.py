@@ -62,6 +62,12 @@ def parse_args():
                    help="skip the per-mode, one-direction and PCIe-peak measurements")
     p.add_argument("--mode", default="auto", choices=["auto", "staged", "zero_copy"],
                    help="transfer mode of the headline offload/reload loop")
+    p.add_argument("--configs", default="fp8,weights,zipf",
+                   help="comma list of extra workloads to measure after the headline "
+                        "(fp8, weights, zipf; empty for none)")
+    p.add_argument("--zipf-host-blocks", type=int, default=2048,
+                   help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks")
+    p.add_argument("--zipf-batches", type=int, default=24)
     p.add_argument("--rocpd-summary", metavar="DB",
                    help="print per-kernel (name, grid) duration statistics of a "
                         "rocprofv3 results database and exit")
@@ -241,6 +247,218 @@ def one_direction(mgr, batch, slots, reps):
     return t_off, t_rel
 
 
+def kernel_gbps(kt):
+    """GB/s of profiled launches: algorithmic bytes / summed event time."""
+    if kt["launches"] == 0 or kt["total_ms"] <= 0:
+        return None
+    return kt["bytes"] / (kt["total_ms"] / 1e3) / 1e9
+
+
+def bench_fp8_scales(torch, pkg, dev, args, rng):
+    """fp8 KV (32 layers, 8 KV heads, head_dim 128, 16-token blocks, e4m3
+    bytes) plus one fp32 scale per (layer, block, head): 512-block offload +
+    reload at once, and the gather kernel moving payload and scales in one
+    launch."""
+    L, P, H, n = 32, 16384, 8, 512
+    bb = 16 * H * 128
+    log(f"fp8: allocating {2 * L} x {P} x {bb} B pool + {L} scale tables")
+    gen = torch.Generator(device=dev).manual_seed(1)
+    kv = [torch.randint(0, 256, (P, bb), dtype=torch.uint8, device=dev, generator=gen)
+          for _ in range(2 * L)]
+    sc = [torch.randn(P, H, device=dev, generator=gen) for _ in range(L)]
+    mgr = pkg.KVCacheManager(kv, host_blocks_to_allocate=2 * n, scale_tables=sc,
+                             staging_chunk_bytes=args.chunk_mib << 20,
+                             staging_chunks=args.chunks, profile_kernels=True)
+    slots = [list(range(0, n)), list(range(n, 2 * n))]
+
+    def batch():
+        perm = rng.permutation(P)
+        return perm[:n].tolist(), perm[n:2 * n].tolist()
+
+    step_bytes = 2 * n * (2 * L * bb + L * H * 4)
+    el = run_duplex(torch, mgr, batch, slots, args.steps, args.warmup)
+    staging = torch.empty(n * (2 * L * bb + L * H * 4), dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream(dev)
+    ids, _ = batch()
+    mgr.gather(ids, staging, stream=s).Await()
+    mgr.kernel_times(True, reset=True)
+    for f in [mgr.gather(ids, staging, stream=s) for _ in range(args.steps)]:
+        f.Await()
+    g = kernel_gbps(mgr.kernel_times(True, reset=True))
+    out = {"workload": "fp8 e4m3 KV + fp32 scale per (layer, block, head), Llama-3-8B shape",
+           "offload_reload_gbps": round(args.steps * step_bytes / el / 1e9, 2),
+           "blocks_per_s": round(args.steps * 2 * n / el, 1),
+           "gather_payload_and_scales_gbps": round(g, 1) if g else None,
+           "gather_frac_of_hbm_peak": round(g / HBM_PEAK_GBPS, 4) if g else None,
+           "bytes_per_block": 2 * L * bb + L * H * 4}
+    log(f"fp8: {out}")
+    mgr.close()
+    del kv, sc, staging
+    torch.cuda.empty_cache()
+    return out
+
+
+def llama3_8b_param_shapes():
+    h, kvh, ffn, vocab = 4096, 1024, 14336, 128256
+    shapes = [(vocab, h)]
+    for _ in range(32):
+        shapes += [(h,), (h, h), (kvh, h), (kvh, h), (h, h), (h,), (ffn, h), (ffn, h), (h, ffn)]
+    return shapes + [(h,), (vocab, h)]
+
+
+def bench_weight_sync(torch, pkg, dev, args):
+    """Llama-3-8B parameter set (291 bf16 tensors, 8.03e9 elements): device
+    pack into one contiguous staging buffer via the offset table, pipelined
+    pack + D2H to pinned host, H2D + unpack, and an 8-way column split of the
+    226 2-D weights."""
+    shapes = llama3_8b_param_shapes()
+    log("weights: allocating 291 bf16 tensors (16.06 GB)")
+    params = [torch.empty(s, dtype=torch.bfloat16, device=dev).normal_(0, 0.02)
+              for s in shapes]
+    total = sum(t.numel() * 2 for t in params)
+    t0 = time.perf_counter()
+    ws = pkg.WeightSynchronizer([[t] for t in params], profile_kernels=True)
+    setup_s = time.perf_counter() - t0
+    staging = torch.empty(ws.total_bytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream(dev)
+    reps = max(3, args.steps // 4)
+    ws.pack(staging, stream=s).Await()
+    ws.kernel_times(True, reset=True)
+    for f in [ws.pack(staging, stream=s) for _ in range(reps)]:
+        f.Await()
+    pack_gbps = kernel_gbps(ws.kernel_times(True, reset=True))  # read+write counted once
+    pack_gbps = pack_gbps * 2 if pack_gbps else None
+    ws.d2h().Await()
+    ws.kernel_times(True, reset=True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ws.d2h().Await()
+    d2h_gbps = reps * total / (time.perf_counter() - t0) / 1e9
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ws.h2d().Await()
+    h2d_gbps = reps * total / (time.perf_counter() - t0) / 1e9
+    ws.kernel_times(True, reset=True)
+    ws.kernel_times(False, reset=True)
+    del staging
+    # Column split: one launch over every 2-D weight.
+    mats = [t for t in params if t.dim() == 2]
+    entries, outs = [], []
+    for m in mats:
+        bounds = pkg.compute_nd_shard_slices(tuple(m.shape), (1, 8))
+        chunk = [torch.empty(m.shape[0], b[1][1] - b[1][0], dtype=m.dtype, device=dev)
+                 for b in bounds]
+        entries += pkg.column_split_entries(m, chunk)
+        outs.append(chunk)
+    split_bytes = sum(m.numel() * 2 for m in mats)
+    pkg.copy_strided(entries, stream=s).Await()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(s)
+    for _ in range(reps):
+        pkg.copy_strided(entries, stream=s)
+    ev1.record(s)
+    ev1.synchronize()
+    split_s = ev0.elapsed_time(ev1) / 1e3 / reps
+    out = {"workload": "Llama-3-8B parameter set, 291 bf16 tensors, 16.06 GB",
+           "bytes": total, "pinned_host_setup_s": round(setup_s, 2),
+           "pack_kernel_gbps": round(pack_gbps, 1) if pack_gbps else None,
+           "pack_frac_of_hbm_peak": round(pack_gbps / HBM_PEAK_GBPS, 4) if pack_gbps else None,
+           "d2h_gbps": round(d2h_gbps, 2), "h2d_gbps": round(h2d_gbps, 2),
+           "column_split_gbps": round(2 * split_bytes / split_s / 1e9, 1),
+           "column_split_frac_of_hbm_peak": round(2 * split_bytes / split_s / 1e9
+                                                  / HBM_PEAK_GBPS, 4),
+           "column_split_entries": len(entries)}
+    log(f"weights: {out}")
+    ws.close()
+    del params, outs, mats
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_zipf_store(torch, pkg, dev, args, rng):
+    """Llama-3-70B-shaped KV (80 layers, K and V: 160 storages of 12000 x 32
+    KiB blocks, 58.6 GiB) with a host tier of pinned blocks behind the
+    KVCacheStore; prefix-cache churn: batches of 64-2048 block hashes drawn
+    Zipf(1.1); hits are loaded into device blocks, misses inserted and saved
+    (evicting LRU entries once the host tier is full)."""
+    L, P, bb = 80, 12000, 32768
+    host_blocks = args.zipf_host_blocks
+    S = 2 * L
+    log(f"zipf: allocating {S} x {P} x {bb} B pool ({S * P * bb / 2**30:.1f} GiB), "
+        f"{host_blocks} host blocks ({host_blocks * S * bb / 2**30:.1f} GiB pinned)")
+    pools = [torch.empty(P, bb, dtype=torch.uint8, device=dev) for _ in range(S)]
+    for p in pools:
+        p.random_(0, 256)
+    store = pkg.KVCacheStore(capacity=host_blocks, num_shards=1, store_server_ip="127.0.0.1",
+                             metadata_shm_key="")
+    mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=host_blocks,
+                             staging_chunk_bytes=args.chunk_mib << 20,
+                             staging_chunks=args.chunks,
+                             raiden_controller_address=store.raiden_controller_address)
+    rid = store.raiden_id
+    universe = 8 * host_blocks
+    # Zipf(1.1) over the universe by inverse CDF.
+    w = 1.0 / np.arange(1, universe + 1) ** 1.1
+    cdf = np.cumsum(w) / w.sum()
+
+    def poll(fn, want):
+        while True:
+            done, failed = fn()[:2]
+            if failed:
+                raise RuntimeError(f"store transfer failed: {len(failed)} blocks")
+            if len(done) >= want:
+                return
+
+    moved = saved = loaded = hits = asked = 0
+    t_run = 0.0
+    for step in range(args.zipf_batches):
+        nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
+        keys = np.unique(np.searchsorted(cdf, rng.random(nb)))
+        hashes = [b"z%08d" % k for k in keys]
+        t0 = time.perf_counter()
+        found = store.lookup(hashes, pin_found=False)
+        hit_set = {h for h, _ in found}
+        # lookup() answers up to the first miss; pin and load every resident
+        # hash individually.
+        res = [h for h in hashes if h in hit_set or store.lookup([h], pin_found=False)]
+        res_set = set(res)
+        miss = [h for h in hashes if h not in res_set]
+        dev_ids = rng.permutation(P)[:len(hashes)].tolist()
+        if res:
+            got = [h for h in res if store.lookup([h])]
+            if got:
+                assert store.load(got, dev_ids[:len(got)])
+                poll(store.poll_load_status, len(got))
+                loaded += len(got)
+        if miss:
+            sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM)
+                  for d in dev_ids[len(res):len(res) + len(miss)]]
+            if store.insert(miss, sl, on_host=False):
+                if store.save(miss):
+                    poll(store.poll_save_status, len(miss))
+                    saved += len(miss)
+                else:
+                    store.release(miss)
+        t_run += time.perf_counter() - t0
+        hits += len(res)
+        asked += len(hashes)
+    moved = (saved + loaded) * S * bb
+    out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), Zipf(1.1) "
+                       "prefix-cache churn through the KV store",
+           "host_tier_blocks": host_blocks,
+           "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
+           "batches": args.zipf_batches, "blocks_saved": saved, "blocks_loaded": loaded,
+           "hit_rate": round(hits / max(asked, 1), 4),
+           "gbps": round(moved / t_run / 1e9, 2),
+           "blocks_per_s": round((saved + loaded) / t_run, 1)}
+    log(f"zipf: {out}")
+    mgr.close()
+    store.close()
+    del pools
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse_args()
     if args.rocpd_summary:
@@ -384,6 +602,16 @@ def main():
     del pools
     torch.cuda.empty_cache()
 
+    # The other workloads of the path, each measured on its own shape.
+    configs = {}
+    wanted = [c for c in args.configs.split(",") if c]
+    if "fp8" in wanted:
+        configs["fp8_kv_scales"] = bench_fp8_scales(torch, pkg, dev, args, rng)
+    if "weights" in wanted:
+        configs["weight_sync_pack"] = bench_weight_sync(torch, pkg, dev, args)
+    if "zipf" in wanted:
+        configs["llama3_70b_zipf_churn"] = bench_zipf_store(torch, pkg, dev, args, rng)
+
     cpu = None
     if args.cpu_seconds > 0:
         log("CPU baseline (oracle host pack/unpack)")
@@ -418,6 +646,7 @@ def main():
         "gather_frac_of_measured_copy": round(iso["gather"]["achieved"] / hbm_copy_gbps, 4),
         "cpu_baseline": cpu,
         **extras,
+        "configs": configs,
     }
     print(json.dumps(out), flush=True)
 
