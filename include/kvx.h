@@ -203,10 +203,10 @@ int64_t kvx_manager_block_array_host_size(kvx_manager* m, int64_t block_array_id
 int64_t kvx_manager_allocated_host_bytes(const kvx_manager* m);
 /* Blocks until every copy the manager issued has finished. */
 int kvx_manager_wait_for_pending_work(kvx_manager* m);
-/* Counters of what the transfer engine issued: out[0..5] = direct copies,
+/* Counters of what the transfer engine issued: out[0..6] = direct copies,
  * staged copies, hipMemcpyAsync calls, kernel launches, staging chunks,
- * zero-copy copies. */
-int kvx_manager_engine_stats(kvx_manager* m, int64_t* out6);
+ * zero-copy copies, pool-extent kernel copies. */
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out7);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the
  * gather (gather = 1) or scatter (gather = 0) kernels so far. Waits for the
@@ -438,6 +438,84 @@ int kvx_metadata_shm_region(kvx_metadata_region* m, uint64_t* out_ptr,
                             int64_t* out_size);
 int kvx_metadata_shm_reformat(kvx_metadata_region* m);
 void kvx_metadata_shm_release(kvx_metadata_region* m);
+
+/* ---------------------------------------------------------------------------
+ * Block pools: byte-level pool/region geometry over a manager's storages
+ * (tpu_sync/kv_cache/pool_layout.h:31-164, pool_layout.cc:91-605) and the
+ * manager's pool table and pool-block copies
+ * (kv_cache_manager_base.cc:1554-1872; Python surface
+ * tpu_sync/api/torch/kv_cache_manager.py:239-330, bound by
+ * tpu_sync/frameworks/torch/pool_layout_nanobind.h:131-228).
+ * ------------------------------------------------------------------------- */
+typedef struct kvx_region_spec {
+  const char* name; /* NUL-terminated; NULL in outputs */
+  int64_t offset_bytes;
+  int64_t stride_bytes;
+  int64_t unit_bytes;
+  int64_t num_units;
+  int64_t units_per_stride;
+} kvx_region_spec;
+
+typedef struct kvx_pool_spec {
+  const char* tag;
+  int64_t storage_index;
+  int64_t base_offset_bytes;
+  int64_t block_stride_bytes;
+  int64_t num_blocks;
+  const kvx_region_spec* regions;
+  int64_t num_regions;
+  const char* dtype_tag;
+} kvx_pool_spec;
+
+/* PoolSpec::Validate(storage_bytes); storage_bytes < 0 checks geometry only. */
+int kvx_pool_validate(const kvx_pool_spec* pool, int64_t storage_bytes);
+/* PoolSpec::storage_extent_end_bytes (INT64_MAX on overflow). */
+int64_t kvx_pool_storage_extent_end(const kvx_pool_spec* pool);
+/* ComputePoolBlockCopyExtents: sorted, coalesced (offset, size) pairs into
+ * out[2 * i]; *n_out receives the count, which may exceed `cap` (then call
+ * again with a larger buffer). KVX_OUT_OF_RANGE for a bad block id. */
+int kvx_pool_copy_extents(const kvx_pool_spec* pool, const int64_t* block_ids,
+                          int64_t n, int64_t* out, int64_t cap, int64_t* n_out);
+/* ExpandPoolLiveSegments: (logical, physical, size) triples into out[3 * i]. */
+int kvx_pool_live_segments(const kvx_pool_spec* pool, int64_t* out, int64_t cap,
+                           int64_t* n_out);
+/* PhysicalLiveRangeToLogical over the pool's live segments. */
+int kvx_pool_physical_to_logical(const kvx_pool_spec* pool, int64_t physical_offset,
+                                 int64_t size, int64_t* out_begin, int64_t* out_end);
+/* TranslateLiveCopy between two pools' compact-live byte spaces:
+ * (src_physical, dst_physical, size) triples into out[3 * i]. */
+int kvx_pool_translate_live_copy(const kvx_pool_spec* src, const kvx_pool_spec* dst,
+                                 int64_t src_offset, int64_t dst_offset, int64_t size,
+                                 int64_t* out, int64_t cap, int64_t* n_out);
+/* RegionsCoverRange: 1 if the regions' packed runs cover [start, end). */
+int32_t kvx_regions_cover_range(const kvx_region_spec* regions, int64_t n,
+                                int64_t start, int64_t end);
+
+/* KVCacheManagerBase::RegisterPools. */
+int kvx_manager_register_pools(kvx_manager* m, const kvx_pool_spec* pools, int64_t n);
+int64_t kvx_manager_num_pools(kvx_manager* m);
+int32_t kvx_manager_has_explicit_pools(kvx_manager* m);
+/* Pool indices with `tag` into out (count in *n_out, may exceed cap). */
+int kvx_manager_pool_indices_with_tag(kvx_manager* m, const char* tag, int64_t* out,
+                                      int64_t cap, int64_t* n_out);
+/* One pool's descriptor. `out->regions` and the strings are not set:
+ * *out_num_regions geometries go to regions[0..cap) (names NULL), and
+ * *out_names holds [tag, dtype_tag, region names...]. */
+int kvx_manager_pool_spec(kvx_manager* m, int64_t pool_idx, kvx_pool_spec* out,
+                          kvx_region_spec* regions, int64_t cap,
+                          int64_t* out_num_regions, kvx_strings** out_names);
+/* GetPoolBlockRef: host address of the block in one shard's mirror. */
+int kvx_manager_pool_block_ref(kvx_manager* m, int64_t pool_idx, int64_t shard_idx,
+                               int64_t block_id, uint64_t* out_ptr,
+                               int64_t* out_block_stride_bytes);
+/* D2hPoolBlocks / H2dPoolBlocks: live bytes of `block_ids`, all shards
+ * (shard_idx < 0) or one, ordered after work on `stream` (may be NULL). */
+int kvx_manager_d2h_pool_blocks(kvx_manager* m, int64_t pool_idx,
+                                const int64_t* block_ids, int64_t n, int64_t shard_idx,
+                                void* stream, kvx_future** out);
+int kvx_manager_h2d_pool_blocks(kvx_manager* m, int64_t pool_idx,
+                                const int64_t* block_ids, int64_t n, int64_t shard_idx,
+                                void* stream, kvx_future** out);
 
 /* ---------------------------------------------------------------------------
  * Weight sync: WeightSynchronizerBase::D2h / D2hLayer / H2d / H2dLayer

@@ -9,7 +9,8 @@ from ._capi import KvxError
 from .kv_cache_manager import KVCacheManager, LogicalBlockManager, RaidenFuture
 from .kv_cache_store import (BlockStatus, KVCacheMetadata, KVCacheMetadataShmRegion,
                              KVCacheStore, LRUCache, RaidenBlockId, RaidenId)
-
+from . import pool_layout
+from .pool_layout import PoolSpec, RegionSpec
 from .weight_synchronizer import (StridedEntry, WeightSynchronizer, column_split_entries,
                                   compute_nd_shard_slices, copy_strided)
 
@@ -17,7 +18,8 @@ __all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError",
            "KVCacheStore", "RaidenId", "RaidenBlockId", "BlockStatus", "LRUCache",
            "KVCacheMetadata", "KVCacheMetadataShmRegion", "WeightSynchronizer",
            "StridedEntry", "copy_strided", "column_split_entries",
-           "compute_nd_shard_slices", "library_path"]
+           "compute_nd_shard_slices", "pool_layout", "PoolSpec", "RegionSpec",
+           "library_path"]
 
 
 def library_path() -> str:

@@ -115,6 +115,30 @@ class StridedEntryC(ctypes.Structure):
     ]
 
 
+class RegionSpecC(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("offset_bytes", ctypes.c_int64),
+        ("stride_bytes", ctypes.c_int64),
+        ("unit_bytes", ctypes.c_int64),
+        ("num_units", ctypes.c_int64),
+        ("units_per_stride", ctypes.c_int64),
+    ]
+
+
+class PoolSpecC(ctypes.Structure):
+    _fields_ = [
+        ("tag", ctypes.c_char_p),
+        ("storage_index", ctypes.c_int64),
+        ("base_offset_bytes", ctypes.c_int64),
+        ("block_stride_bytes", ctypes.c_int64),
+        ("num_blocks", ctypes.c_int64),
+        ("regions", ctypes.POINTER(RegionSpecC)),
+        ("num_regions", ctypes.c_int64),
+        ("dtype_tag", ctypes.c_char_p),
+    ]
+
+
 # kvx_transfer_fn(user, d2h, src, dst, n) -> status
 TRANSFER_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                ctypes.POINTER(ctypes.c_int64),
@@ -261,6 +285,29 @@ PROTOTYPES = {
                                             ctypes.POINTER(ctypes.c_double), _i64p]),
     "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
                                 ctypes.POINTER(_vp)]),
+    "kvx_pool_validate": (_int, [ctypes.POINTER(PoolSpecC), _i64]),
+    "kvx_pool_storage_extent_end": (_i64, [ctypes.POINTER(PoolSpecC)]),
+    "kvx_pool_copy_extents": (_int, [ctypes.POINTER(PoolSpecC), _i64p, _i64, _i64p, _i64,
+                                     _i64p]),
+    "kvx_pool_live_segments": (_int, [ctypes.POINTER(PoolSpecC), _i64p, _i64, _i64p]),
+    "kvx_pool_physical_to_logical": (_int, [ctypes.POINTER(PoolSpecC), _i64, _i64, _i64p,
+                                            _i64p]),
+    "kvx_pool_translate_live_copy": (_int, [ctypes.POINTER(PoolSpecC),
+                                            ctypes.POINTER(PoolSpecC), _i64, _i64, _i64,
+                                            _i64p, _i64, _i64p]),
+    "kvx_regions_cover_range": (_i32, [ctypes.POINTER(RegionSpecC), _i64, _i64, _i64]),
+    "kvx_manager_register_pools": (_int, [_vp, ctypes.POINTER(PoolSpecC), _i64]),
+    "kvx_manager_num_pools": (_i64, [_vp]),
+    "kvx_manager_has_explicit_pools": (_i32, [_vp]),
+    "kvx_manager_pool_indices_with_tag": (_int, [_vp, ctypes.c_char_p, _i64p, _i64, _i64p]),
+    "kvx_manager_pool_spec": (_int, [_vp, _i64, ctypes.POINTER(PoolSpecC),
+                                     ctypes.POINTER(RegionSpecC), _i64, _i64p,
+                                     ctypes.POINTER(_vp)]),
+    "kvx_manager_pool_block_ref": (_int, [_vp, _i64, _i64, _i64, _u64p, _i64p]),
+    "kvx_manager_d2h_pool_blocks": (_int, [_vp, _i64, _i64p, _i64, _i64, _vp,
+                                           ctypes.POINTER(_vp)]),
+    "kvx_manager_h2d_pool_blocks": (_int, [_vp, _i64, _i64p, _i64, _i64, _vp,
+                                           ctypes.POINTER(_vp)]),
 }
 
 _lib = None

@@ -7,6 +7,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../../include/kvx.h"
 #include "../host/copy_future.h"
@@ -27,6 +28,10 @@ struct kvx_manager {
 
 struct kvx_future {
   kvx::CopyFuture f;
+};
+
+struct kvx_strings {
+  std::vector<std::string> items;
 };
 
 namespace kvx_capi {

@@ -359,18 +359,19 @@ int kvx_manager_wait_for_pending_work(kvx_manager* m) {
   if (m == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager");
   return Done(m->impl->WaitForPendingWork());
 }
-int kvx_manager_engine_stats(kvx_manager* m, int64_t* out6) {
-  if (m == nullptr || out6 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out7) {
+  if (m == nullptr || out7 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
   if (m->impl->engine() == nullptr) {
     return Fail(KVX_FAILED_PRECONDITION, "CPU-only manager has no transfer engine");
   }
   kvx::EngineStats s = m->impl->engine()->stats();
-  out6[0] = s.direct_copies;
-  out6[1] = s.staged_copies;
-  out6[2] = s.memcpy_calls;
-  out6[3] = s.kernel_launches;
-  out6[4] = s.chunks;
-  out6[5] = s.zero_copy_copies;
+  out7[0] = s.direct_copies;
+  out7[1] = s.staged_copies;
+  out7[2] = s.memcpy_calls;
+  out7[3] = s.kernel_launches;
+  out7[4] = s.chunks;
+  out7[5] = s.zero_copy_copies;
+  out7[6] = s.extent_kernel_copies;
   return KVX_OK;
 }
 

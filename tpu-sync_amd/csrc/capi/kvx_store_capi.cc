@@ -15,10 +15,6 @@ struct kvx_store {
   kvx_block_manager lbm_view;
 };
 
-struct kvx_strings {
-  std::vector<std::string> items;
-};
-
 struct kvx_slices {
   kvx::BlockSliceList items;
 };

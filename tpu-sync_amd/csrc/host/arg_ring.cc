@@ -1,6 +1,7 @@
 #include "arg_ring.h"
 
 #include <algorithm>
+#include <cstring>
 
 #include "hip_util.h"
 
@@ -83,6 +84,31 @@ Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {
   }
   inflight_.push_back(Slice{off, off + AlignUp(bytes), e});
   return OkStatus();
+}
+
+Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
+                                hipStream_t stream) {
+  if (copies.empty()) return OkStatus();
+  const int vec = StridedVectorBytes(copies);
+  std::vector<StridedEntryDev> table;
+  uint32_t grid = 0;
+  if (!BuildStridedTable(copies, vec, &table, &grid)) {
+    return InvalidArgumentError("strided copy entry out of the kernel's limits");
+  }
+  const int64_t tbytes = static_cast<int64_t>(table.size() * sizeof(StridedEntryDev));
+  const int64_t bytes = tbytes + static_cast<int64_t>(grid) * 4;
+  KVX_ASSIGN_OR_RETURN(int64_t off, ring.Alloc(bytes));
+  std::memcpy(ring.host(off), table.data(), static_cast<size_t>(tbytes));
+  uint32_t* map = reinterpret_cast<uint32_t*>(ring.host(off) + tbytes);
+  for (size_t e = 0; e < table.size(); ++e) {
+    const uint32_t end = e + 1 < table.size() ? table[e + 1].tile_begin : grid;
+    for (uint32_t t = table[e].tile_begin; t < end; ++t) map[t] = static_cast<uint32_t>(e);
+  }
+  KVX_RETURN_IF_ERROR(ring.Upload(off, bytes, stream));
+  KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
+      reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
+      static_cast<uint32_t>(table.size()), grid, vec, stream));
+  return ring.Commit(off, bytes, stream);
 }
 
 }  // namespace kvx

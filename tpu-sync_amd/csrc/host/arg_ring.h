@@ -12,7 +12,9 @@
 
 #include <cstdint>
 #include <deque>
+#include <vector>
 
+#include "../kernels/strided_copy.h"
 #include "status.h"
 
 namespace kvx {
@@ -49,6 +51,12 @@ class ArgRing {
   int64_t head_ = 0;
   std::deque<Slice> inflight_;
 };
+
+// Uploads the table and tile map of `copies` through `ring` and launches the
+// strided-copy kernel on `stream`; the ring region stays reserved until the
+// launch ends.
+Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
+                                hipStream_t stream);
 
 }  // namespace kvx
 

@@ -560,4 +560,218 @@ Status KVCacheManager::WriteBlockBytes(size_t layer_idx, int block_id,
   return OkStatus();
 }
 
+void KVCacheManager::EnsureImplicitPoolsLocked() {
+  if (explicit_pools_ || !pools_.empty()) return;
+  for (int64_t l = 0; l < num_layers_; ++l) {
+    const int64_t stride = LayerBlockByteSize(static_cast<size_t>(l));
+    if (stride <= 0) continue;
+    const int64_t nb = static_cast<int64_t>(GetHostSize(static_cast<size_t>(l), 0)) / stride;
+    if (nb <= 0) continue;
+    PoolSpec p;
+    p.tag = "opaque";
+    p.storage_index = static_cast<size_t>(l);
+    p.block_stride_bytes = stride;
+    p.num_blocks = nb;
+    RegionSpec r;
+    r.name = "block";
+    r.stride_bytes = stride;
+    r.unit_bytes = stride;
+    r.num_units = 1;
+    p.regions.push_back(std::move(r));
+    pools_.push_back(std::move(p));
+  }
+}
+
+Status KVCacheManager::EnsureHostMirrorCovers(size_t storage_idx, int64_t needed_bytes) {
+  if (storage_idx >= static_cast<size_t>(num_layers_) || needed_bytes <= 0) return OkStatus();
+  for (int64_t s = 0; s < num_shards_; ++s) {
+    StorageInfo& si = storage(storage_idx, static_cast<size_t>(s));
+    if (si.host_bytes >= needed_bytes) continue;
+    if (cfg_.host_alloc == HostAllocKind::kShm) {
+      // Mirrors are carved out of one fixed shared-memory segment.
+      return FailedPreconditionError(
+          "shared-memory host mirror cannot grow to cover pool: storage " +
+          std::to_string(storage_idx) + " needs " + std::to_string(needed_bytes) +
+          " bytes, has " + std::to_string(si.host_bytes));
+    }
+    const size_t want = static_cast<size_t>(needed_bytes);
+    StatusOr<HostBufferAllocation> a =
+        cfg_.host_alloc == HostAllocKind::kPinned ? AllocatePinnedHost(want, cfg_.device)
+                                                  : AllocateMallocHost(want);
+    if (!a.ok()) return a.status();
+    if (a->ptr == nullptr || a->size < want) {
+      return InternalError(
+          "host allocator returned undersized buffer for pool mirror: requested=" +
+          std::to_string(want));
+    }
+    // Copies in flight may still read or write the old mirror.
+    KVX_RETURN_IF_ERROR(WaitForPendingWork());
+    if (si.host != nullptr && si.host_bytes > 0) {
+      std::memcpy(a->ptr, si.host, static_cast<size_t>(si.host_bytes));
+    }
+    allocated_host_bytes_ = allocated_host_bytes_ - static_cast<size_t>(si.host_bytes) + a->size;
+    si.host = a->ptr;
+    si.host_bytes = static_cast<int64_t>(a->size);
+    si.host_owner = a->owner;
+  }
+  return OkStatus();
+}
+
+Status KVCacheManager::RegisterPools(std::vector<PoolSpec> pools) {
+  if (pools.empty()) return InvalidArgumentError("pool table must be non-empty");
+  const bool dev = engine_ != nullptr;
+  for (size_t i = 0; i < pools.size(); ++i) {
+    const PoolSpec& p = pools[i];
+    if (p.storage_index >= static_cast<size_t>(num_layers_)) {
+      return InvalidArgumentError("pool " + std::to_string(i) + " (" + p.tag +
+                                  ") storage_index " + std::to_string(p.storage_index) +
+                                  " out of range: manager wraps " +
+                                  std::to_string(num_layers_) + " storages");
+    }
+    // The device storage bounds a device-backed pool; the host mirror (the
+    // storage itself) bounds a host-only one; -1 checks geometry only.
+    int64_t storage_bytes = -1;
+    if (dev && layer_physical_bytes_[p.storage_index] > 0) {
+      storage_bytes = layer_physical_bytes_[p.storage_index];
+    } else if (GetHostSize(p.storage_index, 0) > 0) {
+      storage_bytes = static_cast<int64_t>(GetHostSize(p.storage_index, 0));
+    }
+    Status st = p.Validate(storage_bytes);
+    if (!st.ok()) {
+      return InvalidArgumentError("invalid pool " + std::to_string(i) + ": " + st.message());
+    }
+    if (dev) KVX_RETURN_IF_ERROR(EnsureHostMirrorCovers(p.storage_index,
+                                                        p.storage_extent_end_bytes()));
+  }
+  std::lock_guard<std::mutex> l(pools_mu_);
+  pools_ = std::move(pools);
+  explicit_pools_ = true;
+  return OkStatus();
+}
+
+StatusOr<PoolBlockRef> KVCacheManager::GetPoolBlockRef(size_t pool_idx, size_t shard_idx,
+                                                       int64_t block_id) {
+  std::lock_guard<std::mutex> l(pools_mu_);
+  EnsureImplicitPoolsLocked();
+  if (pool_idx >= pools_.size()) {
+    return OutOfRangeError("pool index " + std::to_string(pool_idx) +
+                           " out of range: " + std::to_string(pools_.size()) + " pools");
+  }
+  if (block_id < 0) return InvalidArgumentError("block_id must be non-negative");
+  const PoolSpec& p = pools_[pool_idx];
+  if (p.storage_index >= static_cast<size_t>(num_layers_) ||
+      shard_idx >= static_cast<size_t>(num_shards_)) {
+    return OutOfRangeError("storage or shard index out of range");
+  }
+  const StorageInfo& si = storage(p.storage_index, shard_idx);
+  if (si.host == nullptr) return FailedPreconditionError("host pointer is null");
+  if (block_id >= p.num_blocks) {
+    return OutOfRangeError("block_id " + std::to_string(block_id) + " out of range for pool " +
+                           std::to_string(pool_idx) + " (" + p.tag +
+                           "): num_blocks=" + std::to_string(p.num_blocks));
+  }
+  const int64_t off = p.base_offset_bytes + block_id * p.block_stride_bytes;
+  int64_t live_end = 0;
+  for (const RegionSpec& r : p.regions) live_end = std::max(live_end, r.extent_end_bytes());
+  if (off > si.host_bytes || live_end > si.host_bytes - off) {
+    return OutOfRangeError("block live regions exceed host buffer");
+  }
+  PoolBlockRef ref;
+  ref.ptr = si.host + off;
+  ref.block_stride_bytes = p.block_stride_bytes;
+  ref.pool_idx = pool_idx;
+  ref.shard_idx = shard_idx;
+  ref.block_id = block_id;
+  return ref;
+}
+
+StatusOr<PoolSpec> KVCacheManager::pool_spec(size_t pool_idx) {
+  std::lock_guard<std::mutex> l(pools_mu_);
+  EnsureImplicitPoolsLocked();
+  if (pool_idx >= pools_.size()) {
+    return OutOfRangeError("pool index out of range: " + std::to_string(pool_idx));
+  }
+  return pools_[pool_idx];
+}
+
+size_t KVCacheManager::num_pools() {
+  std::lock_guard<std::mutex> l(pools_mu_);
+  EnsureImplicitPoolsLocked();
+  return pools_.size();
+}
+
+bool KVCacheManager::has_explicit_pools() {
+  std::lock_guard<std::mutex> l(pools_mu_);
+  return explicit_pools_;
+}
+
+std::vector<size_t> KVCacheManager::PoolIndicesWithTag(const std::string& tag) {
+  std::lock_guard<std::mutex> l(pools_mu_);
+  EnsureImplicitPoolsLocked();
+  std::vector<size_t> out;
+  for (size_t i = 0; i < pools_.size(); ++i) {
+    if (pools_[i].tag == tag) out.push_back(i);
+  }
+  return out;
+}
+
+StatusOr<CopyFuture> KVCacheManager::CopyPoolBlocks(size_t pool_idx,
+                                                    const std::vector<int64_t>& block_ids,
+                                                    std::optional<size_t> shard_idx,
+                                                    bool d2h, hipStream_t dep) {
+  PoolSpec p;
+  {
+    std::lock_guard<std::mutex> l(pools_mu_);
+    EnsureImplicitPoolsLocked();
+    if (pool_idx >= pools_.size()) {
+      return OutOfRangeError("pool index " + std::to_string(pool_idx) +
+                             " out of range: " + std::to_string(pools_.size()) + " pools");
+    }
+    p = pools_[pool_idx];
+  }
+  if (!engine_ || p.storage_index >= static_cast<size_t>(num_layers_)) {
+    return FailedPreconditionError("pool storage has no device buffers (host-only manager)");
+  }
+  if (shard_idx.has_value() && *shard_idx >= static_cast<size_t>(num_shards_)) {
+    return OutOfRangeError("shard index out of range");
+  }
+  KVX_ASSIGN_OR_RETURN(std::vector<PoolBlockCopyExtent> extents,
+                       ComputePoolBlockCopyExtents(p, block_ids));
+  std::vector<StorageView> views;
+  for (int64_t s = 0; s < num_shards_; ++s) {
+    if (shard_idx.has_value() && static_cast<size_t>(s) != *shard_idx) continue;
+    const StorageInfo& si = storage(p.storage_index, static_cast<size_t>(s));
+    if (si.host == nullptr) return FailedPreconditionError("host pointer is null");
+    for (const PoolBlockCopyExtent& e : extents) {
+      const int64_t end = e.offset_bytes + e.size_bytes;
+      if (end > si.host_bytes) {
+        return OutOfRangeError("pool block copy exceeds host buffer size");
+      }
+      if (end > si.dev_bytes) {
+        return OutOfRangeError("pool block copy exceeds device buffer size");
+      }
+    }
+    views.push_back(StorageView{si.dev, si.dev_bytes, si.host, si.host_bytes,
+                                layer_block_bytes(p.storage_index), host_kernel_access_});
+  }
+  std::vector<ByteExtent> ext;
+  ext.reserve(extents.size());
+  for (const PoolBlockCopyExtent& e : extents) ext.push_back({e.offset_bytes, e.size_bytes});
+  return engine_->CopyExtents(d2h ? Direction::kD2H : Direction::kH2D, views, ext, dep);
+}
+
+StatusOr<CopyFuture> KVCacheManager::D2hPoolBlocks(size_t pool_idx,
+                                                   const std::vector<int64_t>& block_ids,
+                                                   std::optional<size_t> shard_idx,
+                                                   hipStream_t dep) {
+  return CopyPoolBlocks(pool_idx, block_ids, shard_idx, true, dep);
+}
+
+StatusOr<CopyFuture> KVCacheManager::H2dPoolBlocks(size_t pool_idx,
+                                                   const std::vector<int64_t>& block_ids,
+                                                   std::optional<size_t> shard_idx,
+                                                   hipStream_t dep) {
+  return CopyPoolBlocks(pool_idx, block_ids, shard_idx, false, dep);
+}
+
 }  // namespace kvx

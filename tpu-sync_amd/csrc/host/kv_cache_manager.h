@@ -26,6 +26,7 @@
 #include "copy_future.h"
 #include "host_allocator.h"
 #include "logical_block_manager.h"
+#include "pool_layout.h"
 #include "status.h"
 #include "transfer_engine.h"
 
@@ -63,6 +64,16 @@ struct KVCacheHostSpan {
   int64_t num_major = 0;
   size_t layer_idx = 0;
   size_t shard_idx = 0;
+};
+
+// A host-side pool block (kv_cache_manager_base.h PoolBlockRef): the block's
+// first byte in the host mirror of one shard.
+struct PoolBlockRef {
+  uint8_t* ptr = nullptr;
+  int64_t block_stride_bytes = 0;
+  size_t pool_idx = 0;
+  size_t shard_idx = 0;
+  int64_t block_id = 0;
 };
 
 class KVCacheManager {
@@ -122,6 +133,33 @@ class KVCacheManager {
   uint8_t* GetHostPointer(size_t layer_idx, size_t shard_idx);
   size_t GetHostSize(size_t layer_idx, size_t shard_idx);
 
+  // Pool table over the wrapped storages (storage index = layer)
+  // (kv_cache_manager_base.cc:1554-1872). Until RegisterPools succeeds each
+  // storage is one implicit pool tagged "opaque" whose single region
+  // "block" covers a whole block, with as many blocks as the host mirror
+  // holds. RegisterPools validates every pool against its device storage
+  // (or host mirror for a host-only manager) and grows a device-backed
+  // storage's host mirror to cover the pool's last live byte, since pool
+  // offsets address the device buffer and the mirror alike.
+  Status RegisterPools(std::vector<PoolSpec> pools);
+  StatusOr<PoolBlockRef> GetPoolBlockRef(size_t pool_idx, size_t shard_idx,
+                                         int64_t block_id);
+  StatusOr<PoolSpec> pool_spec(size_t pool_idx);
+  size_t num_pools();
+  bool has_explicit_pools();
+  std::vector<size_t> PoolIndicesWithTag(const std::string& tag);
+  // Copies the live bytes of pool blocks `block_ids` (padding skipped,
+  // extents coalesced) between the device storage and the host mirror, at
+  // the same byte offsets on both sides, for every shard or one.
+  StatusOr<CopyFuture> D2hPoolBlocks(size_t pool_idx,
+                                     const std::vector<int64_t>& block_ids,
+                                     std::optional<size_t> shard_idx,
+                                     hipStream_t dep = nullptr);
+  StatusOr<CopyFuture> H2dPoolBlocks(size_t pool_idx,
+                                     const std::vector<int64_t>& block_ids,
+                                     std::optional<size_t> shard_idx,
+                                     hipStream_t dep = nullptr);
+
   LogicalBlockManager* host_block_manager() const { return lbm_.get(); }
   std::mutex& host_block_mutex() { return lbm_mu_; }
   size_t bytes_per_block() const { return static_cast<size_t>(slice_byte_size_); }
@@ -171,6 +209,13 @@ class KVCacheManager {
                                 std::optional<size_t> layer_idx,
                                 std::optional<size_t> shard_idx,
                                 hipStream_t dep);
+  // Callers hold pools_mu_.
+  void EnsureImplicitPoolsLocked();
+  Status EnsureHostMirrorCovers(size_t storage_idx, int64_t needed_bytes);
+  StatusOr<CopyFuture> CopyPoolBlocks(size_t pool_idx,
+                                      const std::vector<int64_t>& block_ids,
+                                      std::optional<size_t> shard_idx, bool d2h,
+                                      hipStream_t dep);
   StatusOr<CopyFuture> DeviceCopy(bool gather, const std::vector<int64_t>& ids,
                                   uint64_t staging, int64_t staging_bytes,
                                   bool block_major,
@@ -195,6 +240,9 @@ class KVCacheManager {
   std::unique_ptr<LogicalBlockManager> lbm_;
   std::mutex lbm_mu_;
   std::unique_ptr<TransferEngine> engine_;
+  std::mutex pools_mu_;
+  std::vector<PoolSpec> pools_;
+  bool explicit_pools_ = false;
 };
 
 // The reference's offset validation (kv_cache_manager_base.cc:72-102) and

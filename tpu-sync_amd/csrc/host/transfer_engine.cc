@@ -5,6 +5,7 @@
 #include <numeric>
 
 #include "../kernels/block_copy.h"
+#include "../kernels/strided_copy.h"
 #include "hip_util.h"
 
 namespace kvx {
@@ -77,6 +78,7 @@ TransferEngine::~TransferEngine() {
   }
   for (ArgSlice& s : arg_inflight_) (void)hipEventDestroy(s.done);
   arg_inflight_.clear();
+  extent_args_.reset();
   for (KernelSample& s : samples_) {
     (void)hipEventDestroy(s.start);
     (void)hipEventDestroy(s.stop);
@@ -400,6 +402,69 @@ Status TransferEngine::PlanPairs(Direction dir, const std::vector<int64_t>& src,
     (*host_ids)[i] = host_id[kept[i]];
   }
   return OkStatus();
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyExtents(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<ByteExtent>& extents, hipStream_t dep) {
+  const bool d2h = dir == Direction::kD2H;
+  bool kernel = opts_.mode != TransferMode::kStaged;
+  bool any_short = false;
+  for (const ByteExtent& e : extents) any_short |= e.bytes < opts_.direct_min_bytes;
+  for (const StorageView& s : storages) kernel &= s.host_kernel_access;
+  kernel &= any_short;
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard g(opts_.device);
+  if (!kernel) {
+    hipStream_t cs = d2h ? d2h_stream_ : h2d_stream_;
+    KVX_RETURN_IF_ERROR(WaitDep(dep, cs));
+    for (const StorageView& s : storages) {
+      for (const ByteExtent& e : extents) {
+        if (e.bytes == 0) continue;
+        void* dev = reinterpret_cast<void*>(s.dev + static_cast<uint64_t>(e.offset));
+        if (d2h) {
+          KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(s.host + e.offset, dev, e.bytes,
+                                                 hipMemcpyDeviceToHost, cs));
+        } else {
+          KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(dev, s.host + e.offset, e.bytes,
+                                                 hipMemcpyHostToDevice, cs));
+        }
+        ++stats_.memcpy_calls;
+      }
+    }
+    KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, cs));
+    ++stats_.direct_copies;
+    return CopyFuture::FromEvents({done}, {});
+  }
+  // One launch for every (storage, extent): the kernel moves the live bytes
+  // between HBM and the mapped host region itself.
+  std::vector<StridedCopy> copies;
+  copies.reserve(storages.size() * extents.size());
+  for (const StorageView& s : storages) {
+    const uint64_t host = reinterpret_cast<uint64_t>(s.host);
+    for (const ByteExtent& e : extents) {
+      if (e.bytes == 0) continue;
+      StridedCopy c;
+      c.src = (d2h ? s.dev : host) + static_cast<uint64_t>(e.offset);
+      c.dst = (d2h ? host : s.dev) + static_cast<uint64_t>(e.offset);
+      c.size = e.bytes;
+      copies.push_back(c);
+    }
+  }
+  hipStream_t ks = d2h ? gather_stream_ : scatter_stream_;
+  if (!extent_args_) {
+    auto ring = std::make_unique<ArgRing>();
+    KVX_RETURN_IF_ERROR(ring->Init(1 << 20));
+    extent_args_ = std::move(ring);
+  }
+  KVX_RETURN_IF_ERROR(WaitDep(dep, ks));
+  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(*extent_args_, copies, ks));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, ks));
+  ++stats_.kernel_launches;
+  ++stats_.extent_kernel_copies;
+  return CopyFuture::FromEvents({done}, {});
 }
 
 StatusOr<CopyFuture> TransferEngine::CopyZeroCopy(

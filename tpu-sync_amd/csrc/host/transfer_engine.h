@@ -26,6 +26,7 @@
 #include <mutex>
 #include <vector>
 
+#include "arg_ring.h"
 #include "copy_future.h"
 #include "status.h"
 
@@ -47,6 +48,13 @@ struct StorageView {
 };
 
 enum class Direction : int { kD2H = 0, kH2D = 1 };
+
+// A byte range at the same offset in a storage's device buffer and in its
+// host region (pool-block copies address both sides alike).
+struct ByteExtent {
+  int64_t offset = 0;
+  int64_t bytes = 0;
+};
 
 // How a block copy with short runs crosses PCIe.
 //   kStaged: gather kernel -> device staging ring -> hipMemcpyAsync (and the
@@ -96,6 +104,7 @@ struct EngineStats {
   int64_t kernel_launches = 0;
   int64_t chunks = 0;
   int64_t zero_copy_copies = 0;
+  int64_t extent_kernel_copies = 0;
 };
 
 class TransferEngine {
@@ -123,6 +132,17 @@ class TransferEngine {
                                 const std::vector<StorageView>& storages,
                                 const std::vector<int64_t>& bytes,
                                 hipStream_t dep);
+
+  // Copies `extents` of every storage between its device buffer and its
+  // host region, the same offsets on both sides. Extents shorter than
+  // direct_min_bytes go through one strided-copy kernel that reads and
+  // writes the page-locked host region directly (no staging); otherwise, or
+  // when the host region is not mapped for the GPU, one hipMemcpyAsync per
+  // (storage, extent). The caller has validated every range.
+  StatusOr<CopyFuture> CopyExtents(Direction dir,
+                                   const std::vector<StorageView>& storages,
+                                   const std::vector<ByteExtent>& extents,
+                                   hipStream_t dep);
 
   // Device-only gather/scatter between the storages and a caller buffer
   // laid out layer-major [storage][n][block] (block_major=false) or
@@ -223,6 +243,7 @@ class TransferEngine {
   int64_t arg_bytes_ = 0;
   int64_t arg_head_ = 0;
   std::deque<ArgSlice> arg_inflight_;
+  std::unique_ptr<ArgRing> extent_args_;  // strided tables of CopyExtents
   EngineStats stats_;
 };
 

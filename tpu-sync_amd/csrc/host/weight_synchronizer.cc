@@ -13,33 +13,6 @@ constexpr int64_t kTensorAlign = 256;
 
 int64_t AlignUp(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
-// Uploads the table and tile map of `copies` through `ring` and launches the
-// kernel on `stream`; the ring region stays reserved until the launch ends.
-Status LaunchThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
-                         hipStream_t stream) {
-  if (copies.empty()) return OkStatus();
-  const int vec = StridedVectorBytes(copies);
-  std::vector<StridedEntryDev> table;
-  uint32_t grid = 0;
-  if (!BuildStridedTable(copies, vec, &table, &grid)) {
-    return InvalidArgumentError("strided copy entry out of the kernel's limits");
-  }
-  const int64_t tbytes = static_cast<int64_t>(table.size() * sizeof(StridedEntryDev));
-  const int64_t bytes = tbytes + static_cast<int64_t>(grid) * 4;
-  KVX_ASSIGN_OR_RETURN(int64_t off, ring.Alloc(bytes));
-  std::memcpy(ring.host(off), table.data(), static_cast<size_t>(tbytes));
-  uint32_t* map = reinterpret_cast<uint32_t*>(ring.host(off) + tbytes);
-  for (size_t e = 0; e < table.size(); ++e) {
-    const uint32_t end = e + 1 < table.size() ? table[e + 1].tile_begin : grid;
-    for (uint32_t t = table[e].tile_begin; t < end; ++t) map[t] = static_cast<uint32_t>(e);
-  }
-  KVX_RETURN_IF_ERROR(ring.Upload(off, bytes, stream));
-  KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
-      reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
-      static_cast<uint32_t>(table.size()), grid, vec, stream));
-  return ring.Commit(off, bytes, stream);
-}
-
 StatusOr<hipEvent_t> NewEvent() {
   hipEvent_t e = nullptr;
   KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -171,7 +144,7 @@ Status WeightSynchronizer::Launch(const std::vector<StridedCopy>& copies, bool p
     KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.stop));
     KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.start, stream));
   }
-  KVX_RETURN_IF_ERROR(LaunchThroughRing(args_, copies, stream));
+  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(args_, copies, stream));
   if (cfg_.profile_kernels) {
     KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.stop, stream));
     for (const StridedCopy& c : copies) s.bytes += c.size * (c.count > 0 ? c.count : 1);
@@ -335,7 +308,7 @@ StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCo
     }
     ring = r;
   }
-  KVX_RETURN_IF_ERROR(LaunchThroughRing(*ring, copies, stream));
+  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(*ring, copies, stream));
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
   return CopyFuture::FromEvents({done}, {});

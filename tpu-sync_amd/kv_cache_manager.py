@@ -423,6 +423,111 @@ class KVCacheManager:
             return np.zeros(0, np.uint8)
         return np.ctypeslib.as_array((ctypes.c_uint8 * size).from_address(ptr))
 
+    # -- block pools -------------------------------------------------------
+    def register_pools(self, pools: Sequence[Any]) -> dict:
+        """Registers explicit block pools over the wrapped storages
+        (tpu_sync/api/torch/kv_cache_manager.py:239-283): Python-side checks
+        first, then the library's, which also grows a storage's host mirror
+        to the pool's last live byte. Returns the admission summary."""
+        from . import pool_layout
+        coerced = tuple(pool_layout.coerce_pool_spec(p) for p in pools)
+        if not coerced:
+            raise ValueError("pool table must be non-empty")
+        num_storages = self.num_layers
+        for i, p in enumerate(coerced):
+            try:
+                p.validate()
+            except Exception as exc:
+                raise ValueError(f"invalid pool {i}: {exc}") from exc
+            if p.storage_index >= num_storages:
+                raise ValueError(f"pool {i} ({p.tag}) storage_index {p.storage_index} "
+                                 f"out of range: manager wraps {num_storages} storages")
+        arr, keep = pool_layout.native_pools(coerced)
+        _capi.check(_capi.load().kvx_manager_register_pools(self._h, arr, len(coerced)),
+                    "KVCacheManager register_pools")
+        del keep
+        tags = {}
+        for p in coerced:
+            tags[p.tag] = tags.get(p.tag, 0) + 1
+        summary = {"admitted": True, "pools": len(coerced),
+                   "storages": len({p.storage_index for p in coerced}), "tags": tags}
+        self._admission_summary = dict(summary)
+        return dict(summary)
+
+    def admission_summary(self) -> dict:
+        summary = getattr(self, "_admission_summary", None)
+        return {"admitted": False} if summary is None else dict(summary)
+
+    def num_pools(self) -> int:
+        return int(_capi.load().kvx_manager_num_pools(self._h))
+
+    def has_explicit_pools(self) -> bool:
+        return bool(_capi.load().kvx_manager_has_explicit_pools(self._h))
+
+    def pool_ids_with_tag(self, tag: str) -> List[int]:
+        fn = _capi.load().kvx_manager_pool_indices_with_tag
+        cap = max(self.num_pools(), 1)
+        out = (ctypes.c_int64 * cap)()
+        n = ctypes.c_int64()
+        _capi.check(fn(self._h, tag.encode(), out, cap, ctypes.byref(n)))
+        return [int(v) for v in out[:n.value]]
+
+    def pool_spec(self, pool_idx: int) -> dict:
+        """One pool's descriptor as a dict (pool_layout_nanobind.h:98-112)."""
+        lib = _capi.load()
+        spec = _capi.PoolSpecC()
+        nreg = ctypes.c_int64()
+        names = ctypes.c_void_p()
+        _capi.check(lib.kvx_manager_pool_spec(self._h, pool_idx, ctypes.byref(spec), None, 0,
+                                              ctypes.byref(nreg), ctypes.byref(names)))
+        _capi.take_strings(names)
+        regs = (_capi.RegionSpecC * max(nreg.value, 1))()
+        _capi.check(lib.kvx_manager_pool_spec(self._h, pool_idx, ctypes.byref(spec), regs,
+                                              nreg.value, ctypes.byref(nreg),
+                                              ctypes.byref(names)))
+        s = [b.decode() for b in _capi.take_strings(names)]
+        regions = [{"name": s[2 + i], "offset_bytes": regs[i].offset_bytes,
+                    "stride_bytes": regs[i].stride_bytes, "unit_bytes": regs[i].unit_bytes,
+                    "num_units": regs[i].num_units,
+                    "units_per_stride": regs[i].units_per_stride}
+                   for i in range(nreg.value)]
+        return {"tag": s[0], "storage_index": spec.storage_index,
+                "base_offset_bytes": spec.base_offset_bytes,
+                "block_stride_bytes": spec.block_stride_bytes,
+                "num_blocks": spec.num_blocks, "regions": regions, "dtype_tag": s[1]}
+
+    def get_block_ref(self, pool_idx: int, block_id: int, shard_idx: int = 0) -> dict:
+        """Host-side reference to one pool block (pool_layout_nanobind.h:114-129)."""
+        ptr, stride = ctypes.c_uint64(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_pool_block_ref(
+            self._h, pool_idx, shard_idx, block_id, ctypes.byref(ptr), ctypes.byref(stride)),
+            "KVCacheManager get_pool_block_ref")
+        spec = self.pool_spec(pool_idx)
+        return {"ptr": ptr.value, "block_stride_bytes": stride.value, "tag": spec["tag"],
+                "dtype_tag": spec["dtype_tag"], "pool_idx": pool_idx,
+                "shard_idx": shard_idx, "block_id": block_id, "regions": spec["regions"]}
+
+    def _pool_copy(self, fn, where, pool_idx, block_ids, shard_idx, stream):
+        ids, n = _capi.i64_array(block_ids)
+        out = ctypes.c_void_p()
+        _capi.check(fn(self._h, pool_idx, ids, n, -1 if shard_idx is None else shard_idx,
+                       ctypes.c_void_p(_stream_ptr(stream)), ctypes.byref(out)), where)
+        return RaidenFuture(out, self, where)
+
+    def d2h_pool_blocks(self, pool_idx: int, block_ids: Sequence[int],
+                        shard_idx: Optional[int] = None, *, stream=None) -> RaidenFuture:
+        """Partial D2H of whole pool blocks into the host mirror (live bytes)."""
+        return self._pool_copy(_capi.load().kvx_manager_d2h_pool_blocks,
+                               "KVCacheManager d2h_pool_blocks", pool_idx, block_ids,
+                               shard_idx, stream)
+
+    def h2d_pool_blocks(self, pool_idx: int, block_ids: Sequence[int],
+                        shard_idx: Optional[int] = None, *, stream=None) -> RaidenFuture:
+        """Partial H2D of whole pool blocks from the host mirror (live bytes)."""
+        return self._pool_copy(_capi.load().kvx_manager_h2d_pool_blocks,
+                               "KVCacheManager h2d_pool_blocks", pool_idx, block_ids,
+                               shard_idx, stream)
+
     # -- geometry ----------------------------------------------------------
     @property
     def num_layers(self) -> int:
@@ -459,10 +564,10 @@ class KVCacheManager:
         _capi.check(_capi.load().kvx_manager_wait_for_pending_work(self._h))
 
     def engine_stats(self) -> dict:
-        out = (ctypes.c_int64 * 6)()
+        out = (ctypes.c_int64 * 7)()
         _capi.check(_capi.load().kvx_manager_engine_stats(self._h, out))
         keys = ("direct_copies", "staged_copies", "memcpy_calls", "kernel_launches",
-                "chunks", "zero_copy_copies")
+                "chunks", "zero_copy_copies", "extent_kernel_copies")
         return dict(zip(keys, list(out)))
 
     def kernel_times(self, gather: bool = True, reset: bool = False) -> dict:
