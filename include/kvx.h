@@ -440,6 +440,79 @@ int kvx_metadata_shm_reformat(kvx_metadata_region* m);
 void kvx_metadata_shm_release(kvx_metadata_region* m);
 
 /* ---------------------------------------------------------------------------
+ * Copy specs and the staging-slot pool: OffsetsImpl, BuildCoalescedCopySpec,
+ * BuildLoadCopyPlan (tpu_sync/core/kv_cache_manager_with_transfer.cc:294-426),
+ * InitializeSlotPool / AcquireSlot / ReleaseSlot (:1859-1916), LayerSpans
+ * (:1807-1857), IssueH2D (:1751-1805), the D2H half of StartPushInternal
+ * (:2253-2335) and the host-id assignment of StartRead (:1520-1565).
+ * Spec outputs hold up to n runs for n input ids; *n_runs gets the count.
+ * ------------------------------------------------------------------------- */
+int kvx_offsets_impl(const int64_t* ids, int64_t n, int32_t source_is_compact,
+                     int64_t* out_src, int64_t* out_dst, int64_t* out_sizes,
+                     int64_t* n_runs);
+int kvx_build_coalesced_copy_spec(const int64_t* src_ids, const int64_t* dst_ids,
+                                  int64_t n, int64_t* out_src, int64_t* out_dst,
+                                  int64_t* out_sizes, int64_t* n_runs);
+
+/* CopyPlan outputs; every array has room for n entries. */
+typedef struct kvx_load_plan_out {
+  int64_t* producer_remote_block_ids;
+  int64_t* transport_host_block_ids;
+  int64_t* h2d_local_block_ids;
+  int64_t* h2d_host_block_ids;
+  int64_t num_h2d;
+  int64_t* h2d_src;
+  int64_t* h2d_dst;
+  int64_t* h2d_sizes;
+  int64_t num_runs;
+} kvx_load_plan_out;
+
+int kvx_build_load_copy_plan(const int64_t* remote_block_ids,
+                             const int64_t* local_block_ids,
+                             const int64_t* local_host_block_ids, int64_t n,
+                             kvx_load_plan_out* out);
+
+/* Slot pool (slot size = max_major_per_slot of
+ * kvx_manager_configure_host_staging_slots). */
+int kvx_manager_initialize_slot_pool(kvx_manager* m, int64_t num_slots);
+int kvx_manager_acquire_slot(kvx_manager* m, int64_t* out_slot_idx);
+void kvx_manager_release_slot(kvx_manager* m, int64_t slot_idx);
+int64_t kvx_manager_num_free_slots(kvx_manager* m);
+int kvx_manager_slot_block_ids(kvx_manager* m, int64_t slot_idx, int64_t* out,
+                               int64_t cap, int64_t* n_out);
+
+/* KVCacheHostSpan. */
+typedef struct kvx_host_span {
+  uint64_t ptr;
+  int64_t nbytes;
+  int64_t slot_idx;
+  int64_t base_major;
+  int64_t num_major;
+  int64_t layer_idx;
+  int64_t shard_idx;
+} kvx_host_span;
+
+int kvx_manager_layer_spans(kvx_manager* m, int64_t slot_idx, int64_t num_blocks,
+                            kvx_host_span* out, int64_t cap, int64_t* n_out);
+/* Host ids slot[0..num_blocks) -> device ids local_ids (all layers). */
+int kvx_manager_issue_h2d(kvx_manager* m, int64_t slot_idx, int64_t num_blocks,
+                          const int64_t* local_ids, int64_t n, void* stream,
+                          kvx_future** out, int64_t* out_total_bytes,
+                          int64_t* out_copy_segments);
+/* Acquires a slot and stages device ids src_ids into its first n host ids,
+ * one future per layer into out_layer_futures[num_layers]. */
+int kvx_manager_stage_for_push(kvx_manager* m, const int64_t* src_ids, int64_t n,
+                               void* stream, int64_t* out_slot_idx,
+                               int64_t* out_host_ids, kvx_future** out_layer_futures,
+                               int64_t* out_copy_segments);
+/* Host ids for local_ids (from `host_ids`, or a slot acquired here when it is
+ * NULL; *out_slot_idx = -1 then) and the load plan. */
+int kvx_manager_prepare_load(kvx_manager* m, const int64_t* remote_ids,
+                             const int64_t* local_ids, int64_t n,
+                             const int64_t* host_ids, int64_t* out_slot_idx,
+                             int64_t* out_host_ids, kvx_load_plan_out* out_plan);
+
+/* ---------------------------------------------------------------------------
  * Block pools: byte-level pool/region geometry over a manager's storages
  * (tpu_sync/kv_cache/pool_layout.h:31-164, pool_layout.cc:91-605) and the
  * manager's pool table and pool-block copies

@@ -10,6 +10,12 @@ Parity status of each function (what pins it):
   validate / coalesce / offsets_impl / build_coalesced_copy_spec:
       brute force (expanding runs reproduces the 1-block list) and the
       reference tests' known answers (tests/golden/reference_cases.json).
+  build_load_copy_plan (pure Python, below):
+      invariants fixed independently of the restated loop -- the
+      transport order is the stable sort by remote id of the (remote, host)
+      pairs, expanding the H2D runs gives exactly one (host -> local) copy
+      per distinct local id with that id's host id, and conflicting
+      duplicates are rejected (tests/test_copy_plan.py).
   transfer (D2h/H2d byte semantics), read_block / write_block,
   extract / insert:
       numpy fancy indexing (pool[:, ids]) as an independent library routine,
@@ -106,6 +112,31 @@ def build_coalesced_copy_spec(src_ids, dst_ids):
     if len(s) != len(d):
         raise ValueError("src and dst block lists must have same length")
     return _runs(lambda *p: lib().oracle_build_coalesced_copy_spec(sp, dp, len(s), *p), s)
+
+
+def build_load_copy_plan(remote, local, host):
+    """BuildLoadCopyPlan (tpu_sync/core/kv_cache_manager_with_transfer.cc:
+    357-426): transport order = stable sort by remote id; H2D order = stable
+    sort by local id, a repeated local id dropped (it must carry the same
+    host id); h2d_copy = BuildCoalescedCopySpec(h2d hosts, h2d locals)."""
+    if not len(remote) == len(local) == len(host):
+        raise ValueError("remote_block_ids, local_block_ids, and local_host_block_ids "
+                         "must have same length")
+    order_r = sorted(range(len(remote)), key=lambda i: remote[i])
+    order_l = sorted(range(len(local)), key=lambda i: local[i])
+    h2d_local, h2d_host = [], []
+    for i in order_l:
+        if h2d_local and h2d_local[-1] == local[i]:
+            if h2d_host[-1] != host[i]:
+                raise ValueError("Duplicate local block IDs must map to the same host block ID")
+            continue
+        h2d_local.append(local[i])
+        h2d_host.append(host[i])
+    s, d, z = build_coalesced_copy_spec(h2d_host, h2d_local) if h2d_local else ([], [], [])
+    return {"producer_remote_block_ids": [remote[i] for i in order_r],
+            "transport_host_block_ids": [host[i] for i in order_r],
+            "h2d_local_block_ids": h2d_local, "h2d_host_block_ids": h2d_host,
+            "h2d_copy": {"src_offsets": s, "dst_offsets": d, "sizes": z}}
 
 
 def _ptrs(bufs):

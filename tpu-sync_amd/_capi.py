@@ -139,6 +139,32 @@ class PoolSpecC(ctypes.Structure):
     ]
 
 
+class LoadPlanOut(ctypes.Structure):
+    _fields_ = [
+        ("producer_remote_block_ids", ctypes.POINTER(ctypes.c_int64)),
+        ("transport_host_block_ids", ctypes.POINTER(ctypes.c_int64)),
+        ("h2d_local_block_ids", ctypes.POINTER(ctypes.c_int64)),
+        ("h2d_host_block_ids", ctypes.POINTER(ctypes.c_int64)),
+        ("num_h2d", ctypes.c_int64),
+        ("h2d_src", ctypes.POINTER(ctypes.c_int64)),
+        ("h2d_dst", ctypes.POINTER(ctypes.c_int64)),
+        ("h2d_sizes", ctypes.POINTER(ctypes.c_int64)),
+        ("num_runs", ctypes.c_int64),
+    ]
+
+
+class HostSpanC(ctypes.Structure):
+    _fields_ = [
+        ("ptr", ctypes.c_uint64),
+        ("nbytes", ctypes.c_int64),
+        ("slot_idx", ctypes.c_int64),
+        ("base_major", ctypes.c_int64),
+        ("num_major", ctypes.c_int64),
+        ("layer_idx", ctypes.c_int64),
+        ("shard_idx", ctypes.c_int64),
+    ]
+
+
 # kvx_transfer_fn(user, d2h, src, dst, n) -> status
 TRANSFER_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                ctypes.POINTER(ctypes.c_int64),
@@ -285,6 +311,24 @@ PROTOTYPES = {
                                             ctypes.POINTER(ctypes.c_double), _i64p]),
     "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
                                 ctypes.POINTER(_vp)]),
+    "kvx_offsets_impl": (_int, [_i64p, _i64, _i32, _i64p, _i64p, _i64p, _i64p]),
+    "kvx_build_coalesced_copy_spec": (_int, [_i64p, _i64p, _i64, _i64p, _i64p, _i64p,
+                                             _i64p]),
+    "kvx_build_load_copy_plan": (_int, [_i64p, _i64p, _i64p, _i64,
+                                        ctypes.POINTER(LoadPlanOut)]),
+    "kvx_manager_initialize_slot_pool": (_int, [_vp, _i64]),
+    "kvx_manager_acquire_slot": (_int, [_vp, _i64p]),
+    "kvx_manager_release_slot": (None, [_vp, _i64]),
+    "kvx_manager_num_free_slots": (_i64, [_vp]),
+    "kvx_manager_slot_block_ids": (_int, [_vp, _i64, _i64p, _i64, _i64p]),
+    "kvx_manager_layer_spans": (_int, [_vp, _i64, _i64, ctypes.POINTER(HostSpanC), _i64,
+                                       _i64p]),
+    "kvx_manager_issue_h2d": (_int, [_vp, _i64, _i64, _i64p, _i64, _vp, ctypes.POINTER(_vp),
+                                     _i64p, _i64p]),
+    "kvx_manager_stage_for_push": (_int, [_vp, _i64p, _i64, _vp, _i64p, _i64p,
+                                          ctypes.POINTER(_vp), _i64p]),
+    "kvx_manager_prepare_load": (_int, [_vp, _i64p, _i64p, _i64, _i64p, _i64p, _i64p,
+                                        ctypes.POINTER(LoadPlanOut)]),
     "kvx_pool_validate": (_int, [ctypes.POINTER(PoolSpecC), _i64]),
     "kvx_pool_storage_extent_end": (_i64, [ctypes.POINTER(PoolSpecC)]),
     "kvx_pool_copy_extents": (_int, [ctypes.POINTER(PoolSpecC), _i64p, _i64, _i64p, _i64,

@@ -774,4 +774,202 @@ StatusOr<CopyFuture> KVCacheManager::H2dPoolBlocks(size_t pool_idx,
   return CopyPoolBlocks(pool_idx, block_ids, shard_idx, false, dep);
 }
 
+Status KVCacheManager::InitializeSlotPool(int64_t num_slots) {
+  if (num_slots <= 0) return InvalidArgumentError("num_slots must be positive");
+  if (staging_max_major_per_slot_ <= 0) {
+    return FailedPreconditionError("host staging slots are not configured");
+  }
+  const int64_t max_blocks = staging_max_major_per_slot_;
+  std::lock_guard<std::mutex> sl(slots_mu_);
+  std::lock_guard<std::mutex> bl(lbm_mu_);
+  if (lbm_->num_free_blocks() < num_slots * max_blocks) {
+    return FailedPreconditionError(
+        "Insufficient free host blocks to initialize slot pool. Required: " +
+        std::to_string(num_slots * max_blocks) +
+        ", Available: " + std::to_string(lbm_->num_free_blocks()));
+  }
+  // Slots of an earlier pool go back to the block manager.
+  for (const StagingSlot& s : all_slots_) {
+    std::vector<int> ids(s.block_ids.begin(), s.block_ids.end());
+    KVX_RETURN_IF_ERROR(lbm_->Unlock(ids));
+    KVX_RETURN_IF_ERROR(lbm_->Deallocate(ids));
+  }
+  all_slots_.clear();
+  free_slots_.clear();
+  for (int64_t i = 0; i < num_slots; ++i) {
+    KVX_ASSIGN_OR_RETURN(std::vector<int> ids,
+                         lbm_->Allocate(static_cast<int>(max_blocks), /*lock=*/true));
+    if (static_cast<int64_t>(ids.size()) != max_blocks) {
+      return InternalError("Slot pool allocation returned incorrect number of blocks: " +
+                           std::to_string(ids.size()) + ", expected: " +
+                           std::to_string(max_blocks));
+    }
+    all_slots_.push_back(StagingSlot{i, std::vector<int64_t>(ids.begin(), ids.end())});
+    free_slots_.push_back(i);
+  }
+  return OkStatus();
+}
+
+StatusOr<StagingSlot> KVCacheManager::AcquireSlot() {
+  std::lock_guard<std::mutex> l(slots_mu_);
+  if (free_slots_.empty()) return ResourceExhaustedError("Raiden host slot pool exhausted");
+  const int64_t i = free_slots_.front();
+  free_slots_.pop_front();
+  return all_slots_[static_cast<size_t>(i)];
+}
+
+void KVCacheManager::ReleaseSlot(int64_t slot_idx) {
+  std::lock_guard<std::mutex> l(slots_mu_);
+  if (slot_idx < 0 || slot_idx >= static_cast<int64_t>(all_slots_.size())) return;
+  free_slots_.push_back(slot_idx);
+}
+
+int64_t KVCacheManager::num_free_slots() {
+  std::lock_guard<std::mutex> l(slots_mu_);
+  return static_cast<int64_t>(free_slots_.size());
+}
+
+StatusOr<std::vector<int64_t>> KVCacheManager::SlotBlockIds(int64_t slot_idx) {
+  std::lock_guard<std::mutex> l(slots_mu_);
+  if (slot_idx < 0 || slot_idx >= static_cast<int64_t>(all_slots_.size())) {
+    return OutOfRangeError("slot_idx out of range");
+  }
+  return all_slots_[static_cast<size_t>(slot_idx)].block_ids;
+}
+
+StatusOr<std::vector<KVCacheHostSpan>> KVCacheManager::LayerSpans(int64_t slot_idx,
+                                                                  int64_t num_blocks) {
+  if (num_layers_ == 0) return FailedPreconditionError("KV cache manager is not registered");
+  KVX_ASSIGN_OR_RETURN(std::vector<int64_t> ids, SlotBlockIds(slot_idx));
+  if (num_blocks < 0 || num_blocks > static_cast<int64_t>(ids.size())) {
+    return OutOfRangeError("num_blocks out of range");
+  }
+  ids.resize(static_cast<size_t>(num_blocks));
+  const CopySpec runs = OffsetsImpl(ids, /*source_is_compact=*/false);
+  std::vector<KVCacheHostSpan> spans;
+  spans.reserve(static_cast<size_t>(num_layers_ * num_shards_) * runs.sizes.size());
+  for (int64_t l = 0; l < num_layers_; ++l) {
+    const int64_t per_layer = LayerBlockByteSize(static_cast<size_t>(l));
+    const int64_t bytes = per_layer > 0 ? per_layer : slice_byte_size_;
+    for (int64_t s = 0; s < num_shards_; ++s) {
+      const StorageInfo& si = storage(static_cast<size_t>(l), static_cast<size_t>(s));
+      for (size_t r = 0; r < runs.sizes.size(); ++r) {
+        KVCacheHostSpan span;
+        span.ptr = si.host + runs.src_offsets[r] * bytes;
+        span.nbytes = static_cast<size_t>(runs.sizes[r] * bytes);
+        span.slot_idx = slot_idx;
+        span.base_major = runs.src_offsets[r];
+        span.num_major = runs.sizes[r];
+        span.layer_idx = static_cast<size_t>(l);
+        span.shard_idx = static_cast<size_t>(s);
+        spans.push_back(span);
+      }
+    }
+  }
+  return spans;
+}
+
+StatusOr<StageResult> KVCacheManager::IssueH2D(int64_t slot_idx, int64_t num_blocks,
+                                               const std::vector<int64_t>& local_block_ids,
+                                               hipStream_t dep) {
+  if (num_layers_ == 0) return FailedPreconditionError("KV cache manager is not registered");
+  std::vector<int64_t> host_ids;
+  {
+    std::lock_guard<std::mutex> l(slots_mu_);
+    if (slot_idx < 0 || slot_idx >= static_cast<int64_t>(all_slots_.size())) {
+      return OutOfRangeError("slot_idx out of range");
+    }
+    host_ids = all_slots_[static_cast<size_t>(slot_idx)].block_ids;
+  }
+  if (num_blocks < 0 || num_blocks > static_cast<int64_t>(host_ids.size())) {
+    return OutOfRangeError("num_blocks out of range");
+  }
+  if (num_blocks != static_cast<int64_t>(local_block_ids.size())) {
+    return InvalidArgumentError("num_blocks must match len(local_block_ids)");
+  }
+  host_ids.resize(static_cast<size_t>(num_blocks));
+  KVX_ASSIGN_OR_RETURN(CopySpec spec, BuildCoalescedCopySpec(host_ids, local_block_ids));
+  StageResult r;
+  KVX_ASSIGN_OR_RETURN(r.host_spans, LayerSpans(slot_idx, num_blocks));
+  for (const KVCacheHostSpan& s : r.host_spans) r.total_bytes += static_cast<int64_t>(s.nbytes);
+  r.copy_segments = static_cast<int64_t>(spec.sizes.size());
+  if (spec.sizes.empty()) return r;
+  KVX_ASSIGN_OR_RETURN(r.future, H2d(spec.src_offsets, spec.dst_offsets, spec.sizes,
+                                     std::nullopt, std::nullopt, std::nullopt, dep));
+  return r;
+}
+
+StatusOr<PushStage> KVCacheManager::StageForPush(const std::vector<int64_t>& src_block_ids,
+                                                 hipStream_t dep) {
+  if (num_layers_ == 0) return FailedPreconditionError("KV cache manager is not registered");
+  if (static_cast<int64_t>(src_block_ids.size()) > staging_max_major_per_slot_) {
+    return InvalidArgumentError("push of " + std::to_string(src_block_ids.size()) +
+                                " blocks exceeds the slot size " +
+                                std::to_string(staging_max_major_per_slot_));
+  }
+  KVX_ASSIGN_OR_RETURN(StagingSlot slot, AcquireSlot());
+  PushStage st;
+  st.slot_idx = slot.slot_idx;
+  st.host_block_ids.assign(slot.block_ids.begin(),
+                           slot.block_ids.begin() + static_cast<int64_t>(src_block_ids.size()));
+  auto fail = [&](const Status& s) {
+    for (const CopyFuture& f : st.layer_futures) (void)f.Await();
+    ReleaseSlot(slot.slot_idx);
+    return s;
+  };
+  StatusOr<CopySpec> spec = BuildCoalescedCopySpec(src_block_ids, st.host_block_ids);
+  if (!spec.ok()) return fail(spec.status());
+  st.copy_segments = static_cast<int64_t>(spec->sizes.size());
+  if (spec->sizes.empty()) return st;
+  for (int64_t l = 0; l < num_layers_; ++l) {
+    StatusOr<CopyFuture> f = D2h(spec->src_offsets, spec->dst_offsets, spec->sizes,
+                                 std::nullopt, static_cast<size_t>(l), std::nullopt, dep);
+    if (!f.ok()) return fail(f.status());
+    st.layer_futures.push_back(*f);
+  }
+  return st;
+}
+
+StatusOr<LoadStage> KVCacheManager::PrepareLoad(
+    const std::vector<int64_t>& remote_block_ids, const std::vector<int64_t>& local_block_ids,
+    const std::vector<int64_t>* local_host_block_ids) {
+  LoadStage st;
+  if (local_host_block_ids != nullptr) {
+    st.host_block_ids = *local_host_block_ids;
+  } else if (!local_block_ids.empty()) {
+    std::vector<int64_t> distinct = local_block_ids;
+    std::sort(distinct.begin(), distinct.end());
+    distinct.erase(std::unique(distinct.begin(), distinct.end()), distinct.end());
+    if (static_cast<int64_t>(distinct.size()) > staging_max_major_per_slot_) {
+      return ResourceExhaustedError("load of " + std::to_string(distinct.size()) +
+                                    " distinct blocks exceeds the slot size " +
+                                    std::to_string(staging_max_major_per_slot_));
+    }
+    KVX_ASSIGN_OR_RETURN(StagingSlot slot, AcquireSlot());
+    st.slot_idx = slot.slot_idx;
+    // First occurrence of each local id takes the next host id of the slot.
+    std::vector<std::pair<int64_t, int64_t>> assigned;  // (local, host), by local
+    size_t next = 0;
+    for (int64_t local : local_block_ids) {
+      auto it = std::lower_bound(assigned.begin(), assigned.end(),
+                                 std::make_pair(local, INT64_MIN));
+      if (it != assigned.end() && it->first == local) {
+        st.host_block_ids.push_back(it->second);
+        continue;
+      }
+      const int64_t host = slot.block_ids[next++];
+      assigned.insert(it, {local, host});
+      st.host_block_ids.push_back(host);
+    }
+  }
+  StatusOr<CopyPlan> plan =
+      BuildLoadCopyPlan(remote_block_ids, local_block_ids, st.host_block_ids);
+  if (!plan.ok()) {
+    if (st.slot_idx >= 0) ReleaseSlot(st.slot_idx);
+    return plan.status();
+  }
+  st.plan = std::move(*plan);
+  return st;
+}
+
 }  // namespace kvx

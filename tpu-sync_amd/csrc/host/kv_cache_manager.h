@@ -16,6 +16,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <deque>
 #include <memory>
 #include <mutex>
 #include <optional>
@@ -24,6 +25,7 @@
 #include <vector>
 
 #include "copy_future.h"
+#include "copy_plan.h"
 #include "host_allocator.h"
 #include "logical_block_manager.h"
 #include "pool_layout.h"
@@ -64,6 +66,37 @@ struct KVCacheHostSpan {
   int64_t num_major = 0;
   size_t layer_idx = 0;
   size_t shard_idx = 0;
+};
+
+// One staging slot: max_blocks host block ids reserved (locked) in the host
+// block manager (kv_cache_manager_with_transfer.h Slot).
+struct StagingSlot {
+  int64_t slot_idx = -1;
+  std::vector<int64_t> block_ids;
+};
+
+// kv_cache_manager_with_transfer.h:120-128 StageResult.
+struct StageResult {
+  CopyFuture future;
+  std::vector<KVCacheHostSpan> host_spans;
+  int64_t total_bytes = 0;
+  int64_t copy_segments = 0;
+};
+
+// The D2H half of a push: the device blocks staged into a slot's host ids,
+// one future per layer so each layer can be sent as soon as it lands.
+struct PushStage {
+  int64_t slot_idx = -1;
+  std::vector<int64_t> host_block_ids;
+  std::vector<CopyFuture> layer_futures;
+  int64_t copy_segments = 0;
+};
+
+// The receive half: host ids assigned to the local ids and the load plan.
+struct LoadStage {
+  int64_t slot_idx = -1;  // -1 when the caller supplied the host ids
+  std::vector<int64_t> host_block_ids;
+  CopyPlan plan;
 };
 
 // A host-side pool block (kv_cache_manager_base.h PoolBlockRef): the block's
@@ -121,6 +154,33 @@ class KVCacheManager {
                                    int64_t max_major_per_slot);
   StatusOr<KVCacheHostSpan> HostSpan(size_t layer_idx, size_t shard_idx,
                                      int64_t slot_idx, int64_t num_major);
+
+  // Staging-slot pool (kv_cache_manager_with_transfer.cc:1751-1916):
+  // num_slots slots of max_major_per_slot host ids each, allocated locked
+  // from the host block manager once ConfigureHostStagingSlots has set the
+  // slot size. Slots are handed out first-in first-out.
+  Status InitializeSlotPool(int64_t num_slots);
+  StatusOr<StagingSlot> AcquireSlot();
+  void ReleaseSlot(int64_t slot_idx);
+  int64_t num_free_slots();
+  StatusOr<std::vector<int64_t>> SlotBlockIds(int64_t slot_idx);
+  // Per-(layer, shard) contiguous host runs of the slot's first num_blocks
+  // host ids, layer-major.
+  StatusOr<std::vector<KVCacheHostSpan>> LayerSpans(int64_t slot_idx, int64_t num_blocks);
+  // Host ids slot.block_ids[0..n) -> device ids local_block_ids, coalesced.
+  StatusOr<StageResult> IssueH2D(int64_t slot_idx, int64_t num_blocks,
+                                 const std::vector<int64_t>& local_block_ids,
+                                 hipStream_t dep = nullptr);
+  // Acquires a slot and copies device blocks src_block_ids into its host ids
+  // layer by layer (StartPushInternal, :2253-2335). The caller releases the
+  // slot once the staged bytes have been consumed.
+  StatusOr<PushStage> StageForPush(const std::vector<int64_t>& src_block_ids,
+                                   hipStream_t dep = nullptr);
+  // Host ids for a receive (StartRead, :1520-1565): the caller's, or a slot
+  // acquired here with one host id per distinct local id; then the load plan.
+  StatusOr<LoadStage> PrepareLoad(const std::vector<int64_t>& remote_block_ids,
+                                  const std::vector<int64_t>& local_block_ids,
+                                  const std::vector<int64_t>* local_host_block_ids);
 
   // Host block accessors (kv_cache_manager_base.cc:1468-1552,
   // tpu_sync/frameworks/torch/kv_cache_manager.cc:224-267).
@@ -240,6 +300,9 @@ class KVCacheManager {
   std::unique_ptr<LogicalBlockManager> lbm_;
   std::mutex lbm_mu_;
   std::unique_ptr<TransferEngine> engine_;
+  std::mutex slots_mu_;
+  std::vector<StagingSlot> all_slots_;
+  std::deque<int64_t> free_slots_;
   std::mutex pools_mu_;
   std::vector<PoolSpec> pools_;
   bool explicit_pools_ = false;

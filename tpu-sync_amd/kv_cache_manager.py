@@ -225,7 +225,10 @@ class KVCacheManager:
                    model_uid, profile_kernels, transfer_mode, zero_copy_workgroups)
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
+            # kv_cache_manager_with_transfer.cc:483-503: slot geometry, then
+            # the slot pool (every slot's host ids allocated and locked).
             self.configure_host_staging_slots(num_slots, max_blocks)
+            self.initialize_slot_pool(num_slots)
         if raiden_controller_address:
             _capi.check(_capi.load().kvx_manager_register_with_controller(
                 self._h, raiden_controller_address.encode()), "RegisterWorker")
@@ -422,6 +425,93 @@ class KVCacheManager:
         if not ptr or size <= 0:
             return np.zeros(0, np.uint8)
         return np.ctypeslib.as_array((ctypes.c_uint8 * size).from_address(ptr))
+
+    # -- staging-slot pool --------------------------------------------------
+    def initialize_slot_pool(self, num_slots: int) -> None:
+        _capi.check(_capi.load().kvx_manager_initialize_slot_pool(self._h, num_slots),
+                    "InitializeSlotPool")
+
+    def acquire_slot(self) -> int:
+        out = ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_acquire_slot(self._h, ctypes.byref(out)),
+                    "AcquireSlot")
+        return out.value
+
+    def release_slot(self, slot_idx: int) -> None:
+        _capi.load().kvx_manager_release_slot(self._h, slot_idx)
+
+    def num_free_slots(self) -> int:
+        return int(_capi.load().kvx_manager_num_free_slots(self._h))
+
+    def slot_block_ids(self, slot_idx: int) -> List[int]:
+        cap = 4096
+        while True:
+            out, n = (ctypes.c_int64 * cap)(), ctypes.c_int64()
+            _capi.check(_capi.load().kvx_manager_slot_block_ids(self._h, slot_idx, out, cap,
+                                                                ctypes.byref(n)))
+            if n.value <= cap:
+                return list(out[:n.value])
+            cap = n.value
+
+    def layer_spans(self, slot_idx: int, num_blocks: int) -> List[dict]:
+        """Per-(layer, shard) contiguous host runs of a slot's first blocks."""
+        cap = max(self.num_layers * self.num_shards * max(num_blocks, 1), 1)
+        out, n = (_capi.HostSpanC * cap)(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_layer_spans(self._h, slot_idx, num_blocks, out,
+                                                         cap, ctypes.byref(n)), "LayerSpans")
+        keys = ("ptr", "nbytes", "slot_idx", "base_major", "num_major", "layer_idx",
+                "shard_idx")
+        return [{k: getattr(out[i], k) for k in keys} for i in range(n.value)]
+
+    def issue_h2d(self, slot_idx: int, num_blocks: int, local_block_ids: Sequence[int], *,
+                  stream=None) -> dict:
+        """Slot host ids -> device ids: {future, host_spans, total_bytes,
+        copy_segments} (kv_cache_manager_with_transfer.cc:1751-1805)."""
+        ids, n = _capi.i64_array(local_block_ids)
+        out, total, segs = ctypes.c_void_p(), ctypes.c_int64(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_issue_h2d(
+            self._h, slot_idx, num_blocks, ids, n, ctypes.c_void_p(_stream_ptr(stream)),
+            ctypes.byref(out), ctypes.byref(total), ctypes.byref(segs)), "IssueH2D")
+        return {"future": RaidenFuture(out, self, "IssueH2D"),
+                "host_spans": self.layer_spans(slot_idx, num_blocks),
+                "total_bytes": total.value, "copy_segments": segs.value}
+
+    def stage_for_push(self, src_block_ids: Sequence[int], *, stream=None) -> dict:
+        """Acquires a slot and stages device blocks into its host ids, one
+        future per layer; release the slot with release_slot once consumed."""
+        ids, n = _capi.i64_array(src_block_ids)
+        layers = self.num_layers
+        futs = (ctypes.c_void_p * max(layers, 1))()
+        slot, segs = ctypes.c_int64(), ctypes.c_int64()
+        host = (ctypes.c_int64 * max(n, 1))()
+        _capi.check(_capi.load().kvx_manager_stage_for_push(
+            self._h, ids, n, ctypes.c_void_p(_stream_ptr(stream)), ctypes.byref(slot), host,
+            futs, ctypes.byref(segs)), "StageForPush")
+        return {"slot_idx": slot.value, "host_block_ids": list(host[:n]),
+                "layer_futures": [RaidenFuture(ctypes.c_void_p(futs[l]), self, "StageForPush")
+                                  for l in range(layers)],
+                "copy_segments": segs.value}
+
+    def prepare_load(self, remote_block_ids: Sequence[int], local_block_ids: Sequence[int],
+                     local_host_block_ids: Optional[Sequence[int]] = None) -> dict:
+        """Host ids for a receive and its load plan: {slot_idx, host_block_ids,
+        plan} (slot_idx -1 when the caller gave the host ids)."""
+        from .copy_plan import _PlanBuffers
+        r, n = _capi.i64_array(remote_block_ids)
+        l, nl = _capi.i64_array(local_block_ids)
+        if nl != n or (local_host_block_ids is not None and len(local_host_block_ids) != n):
+            raise _capi.KvxError(3, "remote_block_ids, local_block_ids, and "
+                                    "local_host_block_ids must have same length", "StartRead")
+        h = None
+        if local_host_block_ids is not None:
+            h, _ = _capi.i64_array(local_host_block_ids)
+        buf = _PlanBuffers(n)
+        slot = ctypes.c_int64()
+        host = (ctypes.c_int64 * max(n, 1))()
+        _capi.check(_capi.load().kvx_manager_prepare_load(
+            self._h, r, l, n, h, ctypes.byref(slot), host, ctypes.byref(buf.out)), "StartRead")
+        return {"slot_idx": slot.value, "host_block_ids": list(host[:n]),
+                "plan": buf.result(n, remote_block_ids, local_block_ids)}
 
     # -- block pools -------------------------------------------------------
     def register_pools(self, pools: Sequence[Any]) -> dict:
