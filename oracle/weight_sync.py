@@ -19,9 +19,10 @@ numpy restatement of the weight-sync byte movement:
 
 Parity status: expand_entries / nd_shard_slices are pinned by known answers
 derived from the definitions and by closed forms (a column split equals
-numpy column slicing; pack then unpack is the identity); the offset table has
-no reference counterpart (the reference keeps one host buffer per tensor)
-and is pinned by its definition only.
+numpy column slicing; pack then unpack is the identity). offset_table /
+pack: parity unpinned -- the packed host layout has no reference
+counterpart (the reference keeps one host buffer per tensor), so only its
+definition and the byte identity of every tensor's copy check it.
 """
 import itertools
 
