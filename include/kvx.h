@@ -109,7 +109,17 @@ typedef struct kvx_manager_config {
   int32_t transfer_mode;        /* KVX_MODE_*: how short runs cross PCIe */
   int64_t zero_copy_workgroups; /* workgroup cap of a zero-copy launch in both
                                    directions; 0 = 16 for D2H, 64 for H2D */
+  int32_t numa_policy;          /* KVX_NUMA_*: host mirror placement */
+  int32_t numa_node;            /* KVX_NUMA_NODE: the node */
 } kvx_manager_config;
+
+/* Host mirror placement (DetectAndAssignNumaNode,
+ * tpu_sync/core/raiden_manager_base.cc:47-76, and the first-touch allocation
+ * of tpu_sync/core/host_memory_allocator.cc:86-121). AUTO (0): prefer the
+ * GPU's NUMA node; OFF: OS placement; NODE: prefer numa_node. */
+#define KVX_NUMA_AUTO 0
+#define KVX_NUMA_OFF 1
+#define KVX_NUMA_NODE 2
 
 int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out);
 /* Waits for the manager's pending copies, then frees it. */
@@ -439,6 +449,15 @@ int kvx_metadata_shm_region(kvx_metadata_region* m, uint64_t* out_ptr,
 int kvx_metadata_shm_reformat(kvx_metadata_region* m);
 void kvx_metadata_shm_release(kvx_metadata_region* m);
 
+/* NUMA: the node host mirrors were placed on (assigned_numa_node), or -1;
+ * the GPU's node from its PCI function; the node holding a touched host page;
+ * restricting the calling thread to a node's CPUs (the node-pinned issue
+ * threads of NumaThreadPool, tpu_sync/core/numa_thread_pool.h:36-80). */
+int32_t kvx_manager_numa_node(const kvx_manager* m);
+int32_t kvx_gpu_numa_node(int32_t device);
+int32_t kvx_host_page_numa_node(uint64_t addr);
+int kvx_numa_pin_current_thread(int32_t node);
+
 /* ---------------------------------------------------------------------------
  * Copy specs and the staging-slot pool: OffsetsImpl, BuildCoalescedCopySpec,
  * BuildLoadCopyPlan (tpu_sync/core/kv_cache_manager_with_transfer.cc:294-426),
@@ -611,6 +630,7 @@ typedef struct kvx_weight_sync_config {
   int64_t chunk_bytes;         /* device staging chunk, 0 = 256 MiB */
   int64_t staging_chunks;      /* ring depth, 0 = 2 */
   int32_t profile_kernels;
+  int32_t numa_off;            /* 1: OS placement of the host image; 0: GPU's node */
 } kvx_weight_sync_config;
 
 int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** out);

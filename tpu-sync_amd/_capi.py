@@ -54,6 +54,8 @@ class ManagerConfig(ctypes.Structure):
         ("profile_kernels", ctypes.c_int32),
         ("transfer_mode", ctypes.c_int32),
         ("zero_copy_workgroups", ctypes.c_int64),
+        ("numa_policy", ctypes.c_int32),
+        ("numa_node", ctypes.c_int32),
     ]
 
 
@@ -99,6 +101,7 @@ class WeightSyncConfig(ctypes.Structure):
         ("chunk_bytes", ctypes.c_int64),
         ("staging_chunks", ctypes.c_int64),
         ("profile_kernels", ctypes.c_int32),
+        ("numa_off", ctypes.c_int32),
     ]
 
 
@@ -311,6 +314,10 @@ PROTOTYPES = {
                                             ctypes.POINTER(ctypes.c_double), _i64p]),
     "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
                                 ctypes.POINTER(_vp)]),
+    "kvx_manager_numa_node": (_i32, [_vp]),
+    "kvx_gpu_numa_node": (_i32, [_i32]),
+    "kvx_host_page_numa_node": (_i32, [_u64]),
+    "kvx_numa_pin_current_thread": (_int, [_i32]),
     "kvx_offsets_impl": (_int, [_i64p, _i64, _i32, _i64p, _i64p, _i64p, _i64p]),
     "kvx_build_coalesced_copy_spec": (_int, [_i64p, _i64p, _i64, _i64p, _i64p, _i64p,
                                              _i64p]),

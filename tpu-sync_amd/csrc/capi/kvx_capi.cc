@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "../host/kv_cache_store.h"
+#include "../host/numa.h"
 #include "../kernels/block_copy.h"
 #include "capi_internal.h"
 
@@ -119,6 +120,20 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
     return Fail(KVX_INVALID_ARGUMENT, "zero-copy transfers need KVX_HOST_PINNED host memory");
   }
   c.engine.mode = static_cast<kvx::TransferMode>(cfg->transfer_mode);
+  switch (cfg->numa_policy) {
+    case KVX_NUMA_AUTO:
+      c.numa = kvx::ManagerConfig::Numa::kAuto;
+      break;
+    case KVX_NUMA_OFF:
+      c.numa = kvx::ManagerConfig::Numa::kOff;
+      break;
+    case KVX_NUMA_NODE:
+      c.numa = kvx::ManagerConfig::Numa::kNode;
+      c.numa_node = cfg->numa_node;
+      break;
+    default:
+      return Fail(KVX_INVALID_ARGUMENT, "unknown numa_policy");
+  }
   if (cfg->zero_copy_workgroups > 0) {
     c.engine.zero_copy_d2h_workgroups = cfg->zero_copy_workgroups;
     c.engine.zero_copy_h2d_workgroups = cfg->zero_copy_workgroups;
@@ -148,6 +163,20 @@ int kvx_manager_register_with_controller(kvx_manager* m, const char* address) {
 
 int32_t kvx_manager_shm_warm(const kvx_manager* m) {
   return m != nullptr && m->impl->shm_warm() ? 1 : 0;
+}
+
+int32_t kvx_manager_numa_node(const kvx_manager* m) {
+  return m == nullptr ? -1 : m->impl->assigned_numa_node();
+}
+
+int32_t kvx_gpu_numa_node(int32_t device) { return kvx::GpuNumaNode(device); }
+
+int32_t kvx_host_page_numa_node(uint64_t addr) {
+  return addr == 0 ? -1 : kvx::PageNumaNode(reinterpret_cast<const void*>(addr));
+}
+
+int kvx_numa_pin_current_thread(int32_t node) {
+  return Done(kvx::PinCurrentThreadToNumaNode(node));
 }
 
 static int Transfer(bool d2h, kvx_manager* m, const int64_t* src, int64_t n_src,

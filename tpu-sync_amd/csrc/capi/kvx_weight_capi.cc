@@ -48,6 +48,7 @@ int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** 
   if (cfg->chunk_bytes > 0) c.chunk_bytes = cfg->chunk_bytes;
   if (cfg->staging_chunks > 0) c.staging_chunks = static_cast<int>(cfg->staging_chunks);
   c.profile_kernels = cfg->profile_kernels != 0;
+  c.numa_local = cfg->numa_off == 0;
   auto r = kvx::WeightSynchronizer::Create(std::move(c));
   if (!r.ok()) return Fail(r.status());
   *out = new kvx_weight_sync{std::move(r).value()};

@@ -12,12 +12,14 @@
 #include <string>
 
 #include "hip_util.h"
+#include "numa.h"
 
 namespace kvx {
 
-StatusOr<HostBufferAllocation> AllocateMallocHost(size_t bytes) {
+StatusOr<HostBufferAllocation> AllocateMallocHost(size_t bytes, int numa_node) {
   HostBufferAllocation a;
   if (bytes == 0) return a;
+  ScopedNumaPreference prefer(numa_node);
   void* p = nullptr;
   if (posix_memalign(&p, 64, bytes) != 0) {
     return ResourceExhaustedError("Failed to allocate host buffer of size: " +
@@ -30,12 +32,14 @@ StatusOr<HostBufferAllocation> AllocateMallocHost(size_t bytes) {
   return a;
 }
 
-StatusOr<HostBufferAllocation> AllocatePinnedHost(size_t bytes, int device) {
+StatusOr<HostBufferAllocation> AllocatePinnedHost(size_t bytes, int device, int numa_node) {
   HostBufferAllocation a;
   if (bytes == 0) return a;
   DeviceGuard g(device);
+  ScopedNumaPreference prefer(numa_node);
   void* p = nullptr;
-  hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+  hipError_t e = hipHostMalloc(&p, bytes, prefer.active() ? hipHostMallocNumaUser
+                                                          : hipHostMallocDefault);
   if (e != hipSuccess) {
     return ResourceExhaustedError("hipHostMalloc of " + std::to_string(bytes) +
                                   " bytes failed: " + hipGetErrorString(e));
@@ -85,7 +89,7 @@ struct ShmMapping {
 
 StatusOr<HostBufferAllocation> AllocateShmHost(const std::string& name,
                                                const SharedMemoryHeader& expected,
-                                               size_t bytes, bool* warm) {
+                                               size_t bytes, bool* warm, int numa_node) {
   const size_t total =
       (sizeof(SharedMemoryHeader) + ((bytes + 4095) & ~size_t{4095}) + 4095) &
       ~size_t{4095};
@@ -131,6 +135,7 @@ StatusOr<HostBufferAllocation> AllocateShmHost(const std::string& name,
   }
   m->map = map;
   m->size = total;
+  KVX_RETURN_IF_ERROR(PreferNodeForRange(map, total, numa_node));
   auto* h = static_cast<SharedMemoryHeader*>(map);
   if (*warm) {
     ++h->reference_count;

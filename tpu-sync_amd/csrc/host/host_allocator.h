@@ -34,8 +34,12 @@ enum class HostAllocKind : int { kMalloc = 0, kPinned = 1, kShm = 2 };
 using HostBufferAllocator =
     std::function<StatusOr<HostBufferAllocation>(size_t bytes)>;
 
-StatusOr<HostBufferAllocation> AllocateMallocHost(size_t bytes);
-StatusOr<HostBufferAllocation> AllocatePinnedHost(size_t bytes, int device);
+// numa_node >= 0: the pages are allocated and first touched (zeroed) while
+// the calling thread prefers that node; pinned memory then follows the
+// thread's policy (hipHostMallocNumaUser).
+StatusOr<HostBufferAllocation> AllocateMallocHost(size_t bytes, int numa_node = -1);
+StatusOr<HostBufferAllocation> AllocatePinnedHost(size_t bytes, int device,
+                                                  int numa_node = -1);
 
 // Schema record at offset 0 of a shared-memory host pool. The layout is the
 // reference's (tpu_sync/core/host_memory_allocator.h:95-108), so a segment
@@ -68,10 +72,12 @@ std::string ShmSegmentName(const std::string& key, const std::string& server_nam
 // reference count incremented; anything else is unlinked and re-created
 // zero-filled. The allocation points at the payload; releasing the owner
 // decrements the reference count and unmaps, never unlinks. *warm reports
-// which path was taken.
+// which path was taken. numa_node >= 0: pages of the mapping not yet
+// present prefer that node.
 StatusOr<HostBufferAllocation> AllocateShmHost(const std::string& name,
                                                const SharedMemoryHeader& expected,
-                                               size_t bytes, bool* warm);
+                                               size_t bytes, bool* warm,
+                                               int numa_node = -1);
 
 }  // namespace kvx
 

@@ -6,6 +6,7 @@
 #include <string>
 
 #include "hip_util.h"
+#include "numa.h"
 
 namespace kvx {
 
@@ -126,6 +127,18 @@ Status KVCacheManager::Init() {
 
   lbm_ = std::make_unique<LogicalBlockManager>(static_cast<int>(host_blocks_));
 
+  switch (cfg_.numa) {
+    case ManagerConfig::Numa::kAuto:
+      numa_node_ = device_backed ? GpuNumaNode(cfg_.device) : -1;
+      break;
+    case ManagerConfig::Numa::kNode:
+      if (cfg_.numa_node < 0) return InvalidArgumentError("numa_node must be non-negative");
+      numa_node_ = cfg_.numa_node;
+      break;
+    default:
+      numa_node_ = -1;
+  }
+
   // Shared-memory host tier: one segment holds every (layer, shard) mirror
   // back to back, [storage][host_blocks][layer block bytes]. (The
   // reference's shm allocator hands the same mapping to every mirror, which
@@ -155,7 +168,7 @@ Status KVCacheManager::Init() {
     const std::string name = ShmSegmentName(cfg_.shm_key, cfg_.shm_server_name,
                                             device_backed ? cfg_.device : -1);
     KVX_ASSIGN_OR_RETURN(shm, AllocateShmHost(name, want, static_cast<size_t>(total),
-                                              &shm_warm_));
+                                              &shm_warm_, numa_node_));
   }
 
   for (size_t k = 0; k < nstor; ++k) {
@@ -171,11 +184,12 @@ Status KVCacheManager::Init() {
     StatusOr<HostBufferAllocation> a = Status();
     switch (cfg_.host_alloc) {
       case HostAllocKind::kMalloc:
-        a = AllocateMallocHost(static_cast<size_t>(alloc_size));
+        a = AllocateMallocHost(static_cast<size_t>(alloc_size), numa_node_);
         break;
       case HostAllocKind::kPinned:
-        a = device_backed ? AllocatePinnedHost(static_cast<size_t>(alloc_size), cfg_.device)
-                          : AllocateMallocHost(static_cast<size_t>(alloc_size));
+        a = device_backed ? AllocatePinnedHost(static_cast<size_t>(alloc_size), cfg_.device,
+                                               numa_node_)
+                          : AllocateMallocHost(static_cast<size_t>(alloc_size), numa_node_);
         break;
       case HostAllocKind::kShm: {
         HostBufferAllocation part;
@@ -596,8 +610,9 @@ Status KVCacheManager::EnsureHostMirrorCovers(size_t storage_idx, int64_t needed
     }
     const size_t want = static_cast<size_t>(needed_bytes);
     StatusOr<HostBufferAllocation> a =
-        cfg_.host_alloc == HostAllocKind::kPinned ? AllocatePinnedHost(want, cfg_.device)
-                                                  : AllocateMallocHost(want);
+        cfg_.host_alloc == HostAllocKind::kPinned
+            ? AllocatePinnedHost(want, cfg_.device, numa_node_)
+            : AllocateMallocHost(want, numa_node_);
     if (!a.ok()) return a.status();
     if (a->ptr == nullptr || a->size < want) {
       return InternalError(

@@ -53,6 +53,11 @@ struct ManagerConfig {
   std::string shm_key;
   std::string shm_server_name;
   std::string model_uid;
+  // Host mirror placement: kAuto prefers the GPU's NUMA node (device-backed
+  // managers), kOff leaves placement to the OS, kNode prefers numa_node.
+  enum class Numa : int { kAuto = 0, kOff = 1, kNode = 2 };
+  Numa numa = Numa::kAuto;
+  int numa_node = -1;
   EngineOptions engine;
 };
 
@@ -238,6 +243,9 @@ class KVCacheManager {
   // True when the shared-memory host tier attached to a surviving segment.
   bool shm_warm() const { return shm_warm_; }
   int device() const { return cfg_.device; }
+  // The NUMA node host mirrors were placed on (the reference's
+  // assigned_numa_node), or -1.
+  int assigned_numa_node() const { return numa_node_; }
   TransferEngine* engine() { return engine_.get(); }
   Status WaitForPendingWork();
 
@@ -295,6 +303,7 @@ class KVCacheManager {
   size_t allocated_host_bytes_ = 0;
   bool host_kernel_access_ = false;
   bool shm_warm_ = false;
+  int numa_node_ = -1;
   int64_t staging_num_slots_ = 0;
   int64_t staging_max_major_per_slot_ = 0;
   std::unique_ptr<LogicalBlockManager> lbm_;

@@ -5,6 +5,7 @@
 #include <map>
 
 #include "hip_util.h"
+#include "numa.h"
 
 namespace kvx {
 namespace {
@@ -52,13 +53,15 @@ Status WeightSynchronizer::Init() {
   total_ = pos;
   DeviceGuard g(cfg_.device);
   if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  numa_node_ = cfg_.numa_local ? GpuNumaNode(cfg_.device) : -1;
   switch (cfg_.host_alloc) {
     case HostAllocKind::kPinned: {
-      KVX_ASSIGN_OR_RETURN(host_, AllocatePinnedHost(static_cast<size_t>(total_), cfg_.device));
+      KVX_ASSIGN_OR_RETURN(host_, AllocatePinnedHost(static_cast<size_t>(total_), cfg_.device,
+                                                     numa_node_));
       break;
     }
     case HostAllocKind::kMalloc: {
-      KVX_ASSIGN_OR_RETURN(host_, AllocateMallocHost(static_cast<size_t>(total_)));
+      KVX_ASSIGN_OR_RETURN(host_, AllocateMallocHost(static_cast<size_t>(total_), numa_node_));
       break;
     }
     default:

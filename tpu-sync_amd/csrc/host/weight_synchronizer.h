@@ -45,6 +45,8 @@ struct WeightSyncConfig {
   int64_t chunk_bytes = 256ll << 20;  // device staging chunk
   int staging_chunks = 2;
   bool profile_kernels = false;
+  // The host image prefers the GPU's NUMA node (false: OS placement).
+  bool numa_local = true;
 };
 
 class WeightSynchronizer {
@@ -52,6 +54,8 @@ class WeightSynchronizer {
   static StatusOr<std::unique_ptr<WeightSynchronizer>> Create(WeightSyncConfig cfg);
   ~WeightSynchronizer();
 
+  // NUMA node of the host image, or -1.
+  int numa_node() const { return numa_node_; }
   StatusOr<CopyFuture> D2h(hipStream_t dep = nullptr);
   StatusOr<CopyFuture> H2d(hipStream_t dep = nullptr);
   StatusOr<CopyFuture> D2hLayer(int64_t layer, hipStream_t dep = nullptr);
@@ -95,6 +99,7 @@ class WeightSynchronizer {
   WeightSyncConfig cfg_;
   std::vector<int64_t> off_;
   int64_t total_ = 0;
+  int numa_node_ = -1;
   HostBufferAllocation host_;
   std::mutex mu_;
   hipStream_t ks_ = nullptr;

@@ -172,6 +172,8 @@ class KVCacheManager:
       scale_tables: per-layer side tables with the same major dimension (for
         an fp8 cache, [num_blocks, kv_heads] float32 scales); they are block
         arrays num_kv_layers.. and move with every copy of the same block ids.
+      numa: host mirror placement: "auto" (the GPU's NUMA node), "off", or a
+        node number.
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
       The remaining reference arguments (ports, worker id, timeout,
       parallelism, unsafe_skip_buffer_lock) configure its networking, which
@@ -191,7 +193,7 @@ class KVCacheManager:
                  shm_server_name: Optional[str] = None,
                  model_uid: Optional[str] = None, profile_kernels: bool = False,
                  transfer_mode: str = "auto", zero_copy_workgroups: int = 0,
-                 scale_tables: Optional[List[Any]] = None):
+                 scale_tables: Optional[List[Any]] = None, numa: Any = "auto"):
         if host_blocks_to_allocate is None:
             if max_blocks is None or num_slots is None:
                 raise ValueError("Must specify either (max_blocks, num_slots) or"
@@ -222,7 +224,7 @@ class KVCacheManager:
         self._init(device, len(layers), num_shards, ptrs, sizes, major_dim, 0,
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
-                   model_uid, profile_kernels, transfer_mode, zero_copy_workgroups)
+                   model_uid, profile_kernels, transfer_mode, zero_copy_workgroups, numa)
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
             # kv_cache_manager_with_transfer.cc:483-503: slot geometry, then
@@ -234,6 +236,11 @@ class KVCacheManager:
                 self._h, raiden_controller_address.encode()), "RegisterWorker")
 
     @property
+    def assigned_numa_node(self) -> int:
+        """NUMA node the host mirrors were placed on, or -1."""
+        return int(_capi.load().kvx_manager_numa_node(self._h))
+
+    @property
     def shm_warm(self) -> bool:
         """True when the shared-memory host tier attached to a surviving segment."""
         return bool(_capi.load().kvx_manager_shm_warm(self._h))
@@ -241,7 +248,8 @@ class KVCacheManager:
     def _init(self, device, num_layers, num_shards, ptrs, sizes, major_dim,
               slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
               direct_min_bytes, shm_key, shm_server_name, model_uid,
-              profile_kernels=False, transfer_mode="auto", zero_copy_workgroups=0):
+              profile_kernels=False, transfer_mode="auto", zero_copy_workgroups=0,
+              numa="auto"):
         lib = _capi.load()
         kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
                  "shm": _capi.HOST_SHM}
@@ -267,6 +275,12 @@ class KVCacheManager:
         cfg.profile_kernels = int(bool(profile_kernels))
         cfg.transfer_mode = _capi.MODES[transfer_mode]
         cfg.zero_copy_workgroups = zero_copy_workgroups
+        if numa == "auto":
+            cfg.numa_policy = 0
+        elif numa in ("off", None):
+            cfg.numa_policy = 1
+        else:
+            cfg.numa_policy, cfg.numa_node = 2, int(numa)
         h = ctypes.c_void_p()
         _capi.check(lib.kvx_manager_create(ctypes.byref(cfg), ctypes.byref(h)),
                     "KVCacheManager create")

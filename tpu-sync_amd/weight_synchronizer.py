@@ -111,7 +111,7 @@ class WeightSynchronizer:
                  bind_ip: Optional[str] = None, unsafe_skip_buffer_lock: bool = True,
                  auto_h2d: bool = False, *, host_alloc: str = "pinned",
                  chunk_bytes: int = 0, staging_chunks: int = 0,
-                 profile_kernels: bool = False):
+                 profile_kernels: bool = False, numa_local: bool = True):
         del local_port, parallelism, listener_port, bind_ip, unsafe_skip_buffer_lock, auto_h2d
         layers = [list(x) if isinstance(x, (list, tuple)) else [x] for x in device_tensors]
         num_shards = len(layers[0]) if layers else 1
@@ -139,6 +139,7 @@ class WeightSynchronizer:
         cfg.chunk_bytes = chunk_bytes
         cfg.staging_chunks = staging_chunks
         cfg.profile_kernels = int(bool(profile_kernels))
+        cfg.numa_off = 0 if numa_local else 1
         h = ctypes.c_void_p()
         _capi.check(_capi.load().kvx_weight_sync_create(ctypes.byref(cfg), ctypes.byref(h)),
                     "WeightSynchronizer create")
