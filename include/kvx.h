@@ -532,6 +532,76 @@ int kvx_manager_prepare_load(kvx_manager* m, const int64_t* remote_ids,
                              int64_t* out_host_ids, kvx_load_plan_out* out_plan);
 
 /* ---------------------------------------------------------------------------
+ * Transport framing of block pushes (the bytes a peer parses; no network
+ * here): ChunkHeader / ChunkMetadata / block ids / chunk size wire forms
+ * (tpu_sync/transport/lib/chunk.h:22-59, chunk.fbs, chunk_serializer.cc:35-182)
+ * and the block-push stream (tpu_sync/transport/block_transport.cc:152-190,
+ * 304-420, 974-1175). Payload items follow the major order
+ * (KVX_LAYER_MAJOR: layer, shard, block; KVX_BLOCK_MAJOR: block,
+ * layer, shard) -- the order kvx_manager_gather writes -- so each item is one
+ * slice of the gathered staging buffer.
+ * ------------------------------------------------------------------------- */
+typedef struct kvx_chunk_header {
+  uint16_t version;
+  uint8_t op;
+  uint8_t flags;
+  uint16_t buffer_id;
+  uint16_t reserved;
+  uint16_t metadata_size;
+  uint32_t remote_id;
+  uint32_t local_id;
+  uint32_t count_or_size;
+  uint64_t uuid;
+} kvx_chunk_header;
+
+typedef struct kvx_chunk_metadata {
+  uint32_t layer_idx;
+  uint32_t dst_shard_idx;
+  uint64_t dst_offset_bytes;
+  uint64_t size_bytes;
+} kvx_chunk_metadata;
+
+/* 64 wire bytes (magic "RD", version 1). */
+void kvx_chunk_header_serialize(const kvx_chunk_header* h, uint8_t* out64);
+int kvx_chunk_header_deserialize(const uint8_t* bytes, int64_t n, kvx_chunk_header* out);
+void kvx_chunk_metadata_serialize(const kvx_chunk_metadata* m, uint8_t* out24);
+int kvx_chunk_metadata_deserialize(const uint8_t* bytes, int64_t n, int32_t version,
+                                   kvx_chunk_metadata* out);
+/* u32 little-endian per id (out: 4 * n bytes); ids back as signed ints. */
+void kvx_block_ids_serialize(const int64_t* ids, int64_t n, uint8_t* out);
+void kvx_block_ids_deserialize(const uint8_t* bytes, int64_t n_bytes, int64_t* out);
+
+typedef struct kvx_push_item {
+  int64_t layer;
+  int64_t shard;
+  int64_t k;
+  int64_t staging_offset;
+  int64_t size;
+} kvx_push_item;
+
+/* The sender's bytes of one block push of the manager's arrays (all when
+ * layer_idx < 0): the header, for explicit destinations (dst_ids != NULL,
+ * op 6) the destination and source id arrays (4 * n bytes each), and the
+ * payload items with their staging offsets (*out_n_items may exceed
+ * items_cap). */
+int kvx_manager_build_push_frame(kvx_manager* m, uint64_t uuid, uint32_t node_id,
+                                 int64_t layer_idx, int32_t parallelism, int32_t major_order,
+                                 const int64_t* src_ids, const int64_t* dst_ids, int64_t n,
+                                 uint8_t* out_header64, uint8_t* out_dst_ids,
+                                 uint8_t* out_src_ids, kvx_push_item* out_items,
+                                 int64_t items_cap, int64_t* out_n_items,
+                                 int64_t* out_staging_bytes);
+/* Receiver side of a whole op-6 push stream: header and item sizes checked
+ * against the manager's arrays, payload copied into `staging` in the
+ * gather's layout, destination/source ids returned (up to ids_cap). */
+int kvx_manager_parse_push_stream(kvx_manager* m, const uint8_t* stream, int64_t n,
+                                  uint8_t* staging, int64_t staging_cap,
+                                  kvx_chunk_header* out_header, int64_t* out_layer_idx,
+                                  int32_t* out_major_order, int64_t* out_dst_ids,
+                                  int64_t* out_src_ids, int64_t ids_cap, int64_t* out_count,
+                                  int64_t* out_staging_bytes);
+
+/* ---------------------------------------------------------------------------
  * Block pools: byte-level pool/region geometry over a manager's storages
  * (tpu_sync/kv_cache/pool_layout.h:31-164, pool_layout.cc:91-605) and the
  * manager's pool table and pool-block copies

@@ -168,6 +168,34 @@ class HostSpanC(ctypes.Structure):
     ]
 
 
+class ChunkHeaderC(ctypes.Structure):
+    _fields_ = [
+        ("version", ctypes.c_uint16),
+        ("op", ctypes.c_uint8),
+        ("flags", ctypes.c_uint8),
+        ("buffer_id", ctypes.c_uint16),
+        ("reserved", ctypes.c_uint16),
+        ("metadata_size", ctypes.c_uint16),
+        ("remote_id", ctypes.c_uint32),
+        ("local_id", ctypes.c_uint32),
+        ("count_or_size", ctypes.c_uint32),
+        ("uuid", ctypes.c_uint64),
+    ]
+
+
+class ChunkMetadataC(ctypes.Structure):
+    _fields_ = [
+        ("layer_idx", ctypes.c_uint32),
+        ("dst_shard_idx", ctypes.c_uint32),
+        ("dst_offset_bytes", ctypes.c_uint64),
+        ("size_bytes", ctypes.c_uint64),
+    ]
+
+
+class PushItemC(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_int64) for k in ("layer", "shard", "k", "staging_offset", "size")]
+
+
 # kvx_transfer_fn(user, d2h, src, dst, n) -> status
 TRANSFER_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                ctypes.POINTER(ctypes.c_int64),
@@ -318,6 +346,20 @@ PROTOTYPES = {
     "kvx_gpu_numa_node": (_i32, [_i32]),
     "kvx_host_page_numa_node": (_i32, [_u64]),
     "kvx_numa_pin_current_thread": (_int, [_i32]),
+    "kvx_chunk_header_serialize": (None, [ctypes.POINTER(ChunkHeaderC), ctypes.c_char_p]),
+    "kvx_chunk_header_deserialize": (_int, [ctypes.c_char_p, _i64, ctypes.POINTER(ChunkHeaderC)]),
+    "kvx_chunk_metadata_serialize": (None, [ctypes.POINTER(ChunkMetadataC), ctypes.c_char_p]),
+    "kvx_chunk_metadata_deserialize": (_int, [ctypes.c_char_p, _i64, _i32,
+                                              ctypes.POINTER(ChunkMetadataC)]),
+    "kvx_block_ids_serialize": (None, [_i64p, _i64, ctypes.c_char_p]),
+    "kvx_block_ids_deserialize": (None, [ctypes.c_char_p, _i64, _i64p]),
+    "kvx_manager_build_push_frame": (_int, [_vp, _u64, ctypes.c_uint32, _i64, _i32, _i32, _i64p,
+                                            _i64p, _i64, ctypes.c_char_p, ctypes.c_char_p,
+                                            ctypes.c_char_p, ctypes.POINTER(PushItemC), _i64,
+                                            _i64p, _i64p]),
+    "kvx_manager_parse_push_stream": (_int, [_vp, ctypes.c_char_p, _i64, _vp, _i64,
+                                             ctypes.POINTER(ChunkHeaderC), _i64p, _i32p, _i64p,
+                                             _i64p, _i64, _i64p, _i64p]),
     "kvx_offsets_impl": (_int, [_i64p, _i64, _i32, _i64p, _i64p, _i64p, _i64p]),
     "kvx_build_coalesced_copy_spec": (_int, [_i64p, _i64p, _i64, _i64p, _i64p, _i64p,
                                              _i64p]),

@@ -33,6 +33,51 @@ struct PiecePlan {
 
 }  // namespace
 
+StatusOr<StagingLayout> DeviceStagingLayout(const std::vector<int64_t>& block_bytes, int64_t n,
+                                            bool block_major) {
+  if (n < 0) return InvalidArgumentError("negative block count");
+  const size_t S = block_bytes.size();
+  StagingLayout out;
+  out.base.assign(S, 0);
+  out.stride_k.assign(S, 0);
+  if (block_major) {
+    for (size_t s = 1; s < S; ++s) {
+      if (block_bytes[s] != block_bytes[0]) {
+        return InvalidArgumentError("block-major staging needs one block size");
+      }
+    }
+    const int64_t B = S > 0 ? block_bytes[0] : 0;
+    for (size_t s = 0; s < S; ++s) {
+      out.base[s] = static_cast<int64_t>(s) * B;
+      out.stride_k[s] = static_cast<int64_t>(S) * B;
+    }
+    out.total_bytes = static_cast<int64_t>(S) * B * n;
+    return out;
+  }
+  // Groups of equal block size in first-appearance order (as MakeGroups).
+  std::vector<int64_t> sizes;
+  std::vector<std::vector<size_t>> members;
+  for (size_t s = 0; s < S; ++s) {
+    size_t g = 0;
+    while (g < sizes.size() && sizes[g] != block_bytes[s]) ++g;
+    if (g == sizes.size()) {
+      sizes.push_back(block_bytes[s]);
+      members.emplace_back();
+    }
+    members[g].push_back(s);
+  }
+  int64_t off = 0;
+  for (size_t g = 0; g < sizes.size(); ++g) {
+    for (size_t m = 0; m < members[g].size(); ++m) {
+      out.base[members[g][m]] = off + static_cast<int64_t>(m) * n * sizes[g];
+      out.stride_k[members[g][m]] = sizes[g];
+    }
+    off += static_cast<int64_t>(members[g].size()) * n * sizes[g];
+  }
+  out.total_bytes = off;
+  return out;
+}
+
 StatusOr<std::unique_ptr<TransferEngine>> TransferEngine::Create(
     const EngineOptions& opts) {
   if (opts.staging_chunk_bytes <= 0 || opts.staging_chunks <= 0 ||

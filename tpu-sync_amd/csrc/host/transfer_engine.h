@@ -89,6 +89,19 @@ struct EngineOptions {
   int64_t auto_staged_min_run = 32;
 };
 
+// Where DeviceCopy puts block k of storage s in its staging buffer:
+// base[s] + k * stride_k[s]. Storages of equal block size form groups in
+// first-appearance order; layer-major staging is, group after group,
+// [member][n][block]; block-major staging needs one block size and is
+// [n][storage][block].
+struct StagingLayout {
+  std::vector<int64_t> base;
+  std::vector<int64_t> stride_k;
+  int64_t total_bytes = 0;
+};
+StatusOr<StagingLayout> DeviceStagingLayout(const std::vector<int64_t>& block_bytes, int64_t n,
+                                            bool block_major);
+
 // Accumulated duration of the profiled launches of one kernel direction.
 struct KernelTimes {
   int64_t launches = 0;
