@@ -111,7 +111,18 @@ typedef struct kvx_manager_config {
                                    directions; 0 = 16 for D2H, 64 for H2D */
   int32_t numa_policy;          /* KVX_NUMA_*: host mirror placement */
   int32_t numa_node;            /* KVX_NUMA_NODE: the node */
+  int32_t dispatch;             /* KVX_DISPATCH_*: how D2h/H2d are issued */
 } kvx_manager_config;
+
+/* D2h/H2d dispatch (kv_cache_manager_base.cc:452-512, 2575-2630): ENV (0)
+ * queues when RAIDEN_ENABLE_ASYNC_DISPATCH=1; QUEUED plans and issues every
+ * copy on one background thread in submission order and returns a future at
+ * once (its errors, validation included, arrive through the future;
+ * undispatched copies are cancelled by kvx_manager_destroy); INLINE issues
+ * on the calling thread. */
+#define KVX_DISPATCH_ENV 0
+#define KVX_DISPATCH_QUEUED 1
+#define KVX_DISPATCH_INLINE 2
 
 /* Host mirror placement (DetectAndAssignNumaNode,
  * tpu_sync/core/raiden_manager_base.cc:47-76, and the first-touch allocation
@@ -454,6 +465,11 @@ void kvx_metadata_shm_release(kvx_metadata_region* m);
  * restricting the calling thread to a node's CPUs (the node-pinned issue
  * threads of NumaThreadPool, tpu_sync/core/numa_thread_pool.h:36-80). */
 int32_t kvx_manager_numa_node(const kvx_manager* m);
+/* 1 when D2h/H2d are queued to the dispatch thread. The kinds ('D', 'H') of
+ * the last (up to 256) dispatched copies, oldest first, into out (count in
+ * *n_out, which may exceed cap). */
+int32_t kvx_manager_queued_dispatch(const kvx_manager* m);
+int kvx_manager_dispatch_log(kvx_manager* m, char* out, int64_t cap, int64_t* n_out);
 int32_t kvx_gpu_numa_node(int32_t device);
 int32_t kvx_host_page_numa_node(uint64_t addr);
 int kvx_numa_pin_current_thread(int32_t node);

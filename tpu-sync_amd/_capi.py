@@ -56,6 +56,7 @@ class ManagerConfig(ctypes.Structure):
         ("zero_copy_workgroups", ctypes.c_int64),
         ("numa_policy", ctypes.c_int32),
         ("numa_node", ctypes.c_int32),
+        ("dispatch", ctypes.c_int32),
     ]
 
 
@@ -343,6 +344,8 @@ PROTOTYPES = {
     "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
                                 ctypes.POINTER(_vp)]),
     "kvx_manager_numa_node": (_i32, [_vp]),
+    "kvx_manager_queued_dispatch": (_i32, [_vp]),
+    "kvx_manager_dispatch_log": (_int, [_vp, ctypes.c_char_p, _i64, _i64p]),
     "kvx_gpu_numa_node": (_i32, [_i32]),
     "kvx_host_page_numa_node": (_i32, [_u64]),
     "kvx_numa_pin_current_thread": (_int, [_i32]),

@@ -1,6 +1,7 @@
 // extern "C" layer over the C++ manager, futures and block allocator.
 // Each entry point validates its arguments, calls the C++ object and turns
 // a Status into its code plus a thread-local message.
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <optional>
@@ -120,6 +121,19 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
     return Fail(KVX_INVALID_ARGUMENT, "zero-copy transfers need KVX_HOST_PINNED host memory");
   }
   c.engine.mode = static_cast<kvx::TransferMode>(cfg->transfer_mode);
+  switch (cfg->dispatch) {
+    case KVX_DISPATCH_ENV:
+      c.dispatch = kvx::ManagerConfig::Dispatch::kEnv;
+      break;
+    case KVX_DISPATCH_QUEUED:
+      c.dispatch = kvx::ManagerConfig::Dispatch::kQueued;
+      break;
+    case KVX_DISPATCH_INLINE:
+      c.dispatch = kvx::ManagerConfig::Dispatch::kInline;
+      break;
+    default:
+      return Fail(KVX_INVALID_ARGUMENT, "unknown dispatch mode");
+  }
   switch (cfg->numa_policy) {
     case KVX_NUMA_AUTO:
       c.numa = kvx::ManagerConfig::Numa::kAuto;
@@ -167,6 +181,20 @@ int32_t kvx_manager_shm_warm(const kvx_manager* m) {
 
 int32_t kvx_manager_numa_node(const kvx_manager* m) {
   return m == nullptr ? -1 : m->impl->assigned_numa_node();
+}
+
+int32_t kvx_manager_queued_dispatch(const kvx_manager* m) {
+  return m != nullptr && m->impl->queued_dispatch() ? 1 : 0;
+}
+
+int kvx_manager_dispatch_log(kvx_manager* m, char* out, int64_t cap, int64_t* n_out) {
+  if (m == nullptr || n_out == nullptr || BadArray(out, cap)) {
+    return Fail(KVX_INVALID_ARGUMENT, "null argument");
+  }
+  const std::string log = m->impl->DispatchLog();
+  *n_out = static_cast<int64_t>(log.size());
+  std::memcpy(out, log.data(), std::min<size_t>(log.size(), static_cast<size_t>(cap)));
+  return KVX_OK;
 }
 
 int32_t kvx_gpu_numa_node(int32_t device) { return kvx::GpuNumaNode(device); }

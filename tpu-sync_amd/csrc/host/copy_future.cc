@@ -35,9 +35,39 @@ CopyFuture CopyFuture::Join(const std::vector<CopyFuture>& futures) {
   return f;
 }
 
+CopyFuture CopyFuture::Pending() {
+  CopyFuture f;
+  f.state_->done = false;
+  f.state_->pending = true;
+  return f;
+}
+
+void CopyFuture::Fulfill(const CopyFuture& issued) const {
+  std::lock_guard<std::mutex> l(state_->mu);
+  if (!state_->pending) return;
+  if (issued.state_) state_->children.push_back(issued.state_);
+  state_->pending = false;
+  state_->cv.notify_all();
+}
+
+void CopyFuture::Reject(Status status) const {
+  std::lock_guard<std::mutex> l(state_->mu);
+  if (!state_->pending) return;
+  state_->status = std::move(status);
+  state_->pending = false;
+  state_->done = true;
+  state_->cv.notify_all();
+}
+
+void CopyFuture::WaitIssued(const State& s) {
+  std::unique_lock<std::mutex> l(s.mu);
+  s.cv.wait(l, [&s] { return !s.pending; });
+}
+
 bool CopyFuture::StateReady(const State& s) {
   {
     std::lock_guard<std::mutex> l(s.mu);
+    if (s.pending) return false;
     if (s.done) return true;
   }
   for (const auto& c : s.children) {
@@ -54,7 +84,7 @@ Status CopyFuture::StatePoll(const State& s) {
   {
     std::lock_guard<std::mutex> l(s.mu);
     if (!s.status.ok()) return s.status;
-    if (s.done) return OkStatus();
+    if (s.done || s.pending) return OkStatus();
   }
   for (const auto& c : s.children) {
     Status st = StatePoll(*c);
@@ -70,6 +100,7 @@ Status CopyFuture::StatePoll(const State& s) {
 }
 
 Status CopyFuture::StateAwait(State& s) {
+  WaitIssued(s);
   {
     std::lock_guard<std::mutex> l(s.mu);
     if (s.done) return s.status;
@@ -103,6 +134,7 @@ Status CopyFuture::WaitOnStream(hipStream_t stream) const {
   while (!stack.empty()) {
     const State* s = stack.back();
     stack.pop_back();
+    WaitIssued(*s);
     for (const auto& c : s->children) stack.push_back(c.get());
     for (hipEvent_t e : s->events) {
       KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(stream, e, 0));

@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <condition_variable>
 #include <functional>
 #include <memory>
 #include <mutex>
@@ -34,6 +35,13 @@ class CopyFuture {
   // Joins futures: ready when all are, first error wins.
   static CopyFuture Join(const std::vector<CopyFuture>& futures);
 
+  // A future whose copy is issued later (queued dispatch): not ready until
+  // Fulfill hands it the issued copy's future or Reject an error. Await and
+  // WaitOnStream block until then.
+  static CopyFuture Pending();
+  void Fulfill(const CopyFuture& issued) const;
+  void Reject(Status status) const;
+
   bool IsValid() const { return state_ != nullptr; }
   bool IsReady() const;
   Status PollError() const;
@@ -48,9 +56,12 @@ class CopyFuture {
     std::vector<std::shared_ptr<State>> children;
     Status status;
     mutable std::mutex mu;
+    mutable std::condition_variable cv;
+    bool pending = false;  // a queued dispatch has not issued the copy yet
     bool done = false;
     ~State();
   };
+  static void WaitIssued(const State& s);
   static bool StateReady(const State& s);
   static Status StatePoll(const State& s);
   static Status StateAwait(State& s);

@@ -1,6 +1,7 @@
 #include "kv_cache_manager.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <string>
@@ -222,10 +223,36 @@ Status KVCacheManager::Init() {
     // copy kernels may read and write the mirror directly.
     host_kernel_access_ = cfg_.host_alloc == HostAllocKind::kPinned;
   }
+  switch (cfg_.dispatch) {
+    case ManagerConfig::Dispatch::kQueued:
+      queued_ = true;
+      break;
+    case ManagerConfig::Dispatch::kEnv: {
+      const char* env = std::getenv("RAIDEN_ENABLE_ASYNC_DISPATCH");
+      queued_ = env != nullptr && std::string(env) == "1";
+      break;
+    }
+    default:
+      queued_ = false;
+  }
+  if (queued_) {
+    if (engine_) {
+      DeviceGuard g(cfg_.device);
+      KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&dep_proxy_, hipStreamNonBlocking));
+    }
+    worker_ = std::thread(&KVCacheManager::WorkerLoop, this);
+  }
   return OkStatus();
 }
 
-KVCacheManager::~KVCacheManager() { (void)WaitForPendingWork(); }
+KVCacheManager::~KVCacheManager() {
+  StopWorker();
+  (void)WaitForPendingWork();
+  if (dep_proxy_ != nullptr) {
+    DeviceGuard g(cfg_.device);
+    (void)hipStreamDestroy(dep_proxy_);
+  }
+}
 
 Status KVCacheManager::WaitForPendingWork() {
   if (!engine_) return OkStatus();
@@ -259,6 +286,11 @@ StatusOr<CopyFuture> KVCacheManager::Transfer(
     std::optional<int64_t> slot_idx, std::optional<size_t> layer_idx,
     std::optional<size_t> shard_idx, hipStream_t dep) {
   const bool d2h = dir == Direction::kD2H;
+  {
+    std::lock_guard<std::mutex> l(log_mu_);
+    dispatch_log_.push_back(d2h ? 'D' : 'H');
+    if (dispatch_log_.size() > 256) dispatch_log_.erase(0, dispatch_log_.size() - 256);
+  }
   if (!engine_) {
     return FailedPreconditionError(
         d2h ? "D2h requires a device-backed KVCacheManagerBase"
@@ -340,6 +372,9 @@ StatusOr<CopyFuture> KVCacheManager::D2h(const std::vector<int64_t>& src,
                                          std::optional<size_t> layer_idx,
                                          std::optional<size_t> shard_idx,
                                          hipStream_t dep) {
+  if (queued_) {
+    return Enqueue(Direction::kD2H, src, dst, sizes, slot_idx, layer_idx, shard_idx, dep);
+  }
   return Transfer(Direction::kD2H, src, dst, sizes, slot_idx, layer_idx,
                   shard_idx, dep);
 }
@@ -351,8 +386,92 @@ StatusOr<CopyFuture> KVCacheManager::H2d(const std::vector<int64_t>& src,
                                          std::optional<size_t> layer_idx,
                                          std::optional<size_t> shard_idx,
                                          hipStream_t dep) {
+  if (queued_) {
+    return Enqueue(Direction::kH2D, src, dst, sizes, slot_idx, layer_idx, shard_idx, dep);
+  }
   return Transfer(Direction::kH2D, src, dst, sizes, slot_idx, layer_idx,
                   shard_idx, dep);
+}
+
+StatusOr<CopyFuture> KVCacheManager::Enqueue(Direction dir, const std::vector<int64_t>& src,
+                                             const std::vector<int64_t>& dst,
+                                             const std::vector<int64_t>& sizes,
+                                             std::optional<int64_t> slot_idx,
+                                             std::optional<size_t> layer_idx,
+                                             std::optional<size_t> shard_idx,
+                                             hipStream_t dep) {
+  QueuedCopy q{dir, src, dst, sizes, slot_idx, layer_idx, shard_idx, nullptr,
+               CopyFuture::Pending()};
+  if (dep != nullptr && engine_) {
+    // The copy is ordered after the work on `dep` at submission time.
+    DeviceGuard g(cfg_.device);
+    KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&q.dep_event, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(q.dep_event, dep);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(q.dep_event);
+      return HipStatus(e, "hipEventRecord(dep)");
+    }
+  }
+  CopyFuture f = q.future;
+  {
+    std::lock_guard<std::mutex> l(queue_mu_);
+    if (shutdown_) {
+      if (q.dep_event != nullptr) (void)hipEventDestroy(q.dep_event);
+      return CancelledError("KVCacheManagerBase is shutting down");
+    }
+    queue_.push_back(std::move(q));
+  }
+  queue_cv_.notify_one();
+  return f;
+}
+
+void KVCacheManager::WorkerLoop() {
+  while (true) {
+    QueuedCopy q;
+    {
+      std::unique_lock<std::mutex> l(queue_mu_);
+      queue_cv_.wait(l, [this] { return shutdown_ || !queue_.empty(); });
+      if (shutdown_ && queue_.empty()) return;
+      q = std::move(queue_.front());
+      queue_.pop_front();
+    }
+    hipStream_t dep = nullptr;
+    if (q.dep_event != nullptr) {
+      DeviceGuard g(cfg_.device);
+      if (hipStreamWaitEvent(dep_proxy_, q.dep_event, 0) == hipSuccess) dep = dep_proxy_;
+      (void)hipEventDestroy(q.dep_event);
+    }
+    StatusOr<CopyFuture> r = Transfer(q.dir, q.src, q.dst, q.sizes, q.slot_idx, q.layer_idx,
+                                      q.shard_idx, dep);
+    if (r.ok()) {
+      q.future.Fulfill(*r);
+    } else {
+      q.future.Reject(r.status());
+    }
+  }
+}
+
+void KVCacheManager::StopWorker() {
+  if (!worker_.joinable()) return;
+  {
+    std::lock_guard<std::mutex> l(queue_mu_);
+    shutdown_ = true;
+    // Copies not yet dispatched are cancelled, as the reference's destructor does.
+    while (!queue_.empty()) {
+      QueuedCopy& q = queue_.front();
+      if (q.dep_event != nullptr) (void)hipEventDestroy(q.dep_event);
+      q.future.Reject(
+          CancelledError("KVCacheManagerBase destroyed before task dispatch completed"));
+      queue_.pop_front();
+    }
+  }
+  queue_cv_.notify_all();
+  worker_.join();
+}
+
+std::string KVCacheManager::DispatchLog() {
+  std::lock_guard<std::mutex> l(log_mu_);
+  return dispatch_log_;
 }
 
 StatusOr<std::pair<std::vector<int>, CopyFuture>>
@@ -909,8 +1028,10 @@ StatusOr<StageResult> KVCacheManager::IssueH2D(int64_t slot_idx, int64_t num_blo
   for (const KVCacheHostSpan& s : r.host_spans) r.total_bytes += static_cast<int64_t>(s.nbytes);
   r.copy_segments = static_cast<int64_t>(spec.sizes.size());
   if (spec.sizes.empty()) return r;
-  KVX_ASSIGN_OR_RETURN(r.future, H2d(spec.src_offsets, spec.dst_offsets, spec.sizes,
-                                     std::nullopt, std::nullopt, std::nullopt, dep));
+  // The reference issues through H2dSyncDispatch here, whatever the dispatch mode.
+  KVX_ASSIGN_OR_RETURN(r.future, Transfer(Direction::kH2D, spec.src_offsets, spec.dst_offsets,
+                                          spec.sizes, std::nullopt, std::nullopt,
+                                          std::nullopt, dep));
   return r;
 }
 
@@ -937,8 +1058,9 @@ StatusOr<PushStage> KVCacheManager::StageForPush(const std::vector<int64_t>& src
   st.copy_segments = static_cast<int64_t>(spec->sizes.size());
   if (spec->sizes.empty()) return st;
   for (int64_t l = 0; l < num_layers_; ++l) {
-    StatusOr<CopyFuture> f = D2h(spec->src_offsets, spec->dst_offsets, spec->sizes,
-                                 std::nullopt, static_cast<size_t>(l), std::nullopt, dep);
+    StatusOr<CopyFuture> f =
+        Transfer(Direction::kD2H, spec->src_offsets, spec->dst_offsets, spec->sizes,
+                 std::nullopt, static_cast<size_t>(l), std::nullopt, dep);
     if (!f.ok()) return fail(f.status());
     st.layer_futures.push_back(*f);
   }

@@ -15,12 +15,14 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <condition_variable>
 #include <cstdint>
 #include <deque>
 #include <memory>
 #include <mutex>
 #include <optional>
 #include <string>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -58,6 +60,12 @@ struct ManagerConfig {
   enum class Numa : int { kAuto = 0, kOff = 1, kNode = 2 };
   Numa numa = Numa::kAuto;
   int numa_node = -1;
+  // D2h/H2d dispatch (kv_cache_manager_base.cc:452-512): kEnv follows
+  // RAIDEN_ENABLE_ASYNC_DISPATCH=1; kQueued plans and issues every copy on
+  // one background thread in submission order and returns at once (errors,
+  // validation included, then arrive through the future).
+  enum class Dispatch : int { kEnv = 0, kQueued = 1, kInline = 2 };
+  Dispatch dispatch = Dispatch::kEnv;
   EngineOptions engine;
 };
 
@@ -247,6 +255,10 @@ class KVCacheManager {
   // assigned_numa_node), or -1.
   int assigned_numa_node() const { return numa_node_; }
   TransferEngine* engine() { return engine_.get(); }
+  bool queued_dispatch() const { return queued_; }
+  // The kinds ('D' = D2h, 'H' = H2d) of the last dispatched copies, oldest
+  // first (at most 256).
+  std::string DispatchLog();
   Status WaitForPendingWork();
 
  private:
@@ -284,6 +296,14 @@ class KVCacheManager {
                                       const std::vector<int64_t>& block_ids,
                                       std::optional<size_t> shard_idx, bool d2h,
                                       hipStream_t dep);
+  StatusOr<CopyFuture> Enqueue(Direction dir, const std::vector<int64_t>& src,
+                               const std::vector<int64_t>& dst,
+                               const std::vector<int64_t>& sizes,
+                               std::optional<int64_t> slot_idx,
+                               std::optional<size_t> layer_idx,
+                               std::optional<size_t> shard_idx, hipStream_t dep);
+  void WorkerLoop();
+  void StopWorker();
   StatusOr<CopyFuture> DeviceCopy(bool gather, const std::vector<int64_t>& ids,
                                   uint64_t staging, int64_t staging_bytes,
                                   bool block_major,
@@ -309,6 +329,23 @@ class KVCacheManager {
   std::unique_ptr<LogicalBlockManager> lbm_;
   std::mutex lbm_mu_;
   std::unique_ptr<TransferEngine> engine_;
+  struct QueuedCopy {
+    Direction dir;
+    std::vector<int64_t> src, dst, sizes;
+    std::optional<int64_t> slot_idx;
+    std::optional<size_t> layer_idx, shard_idx;
+    hipEvent_t dep_event = nullptr;  // recorded on the caller's stream at submission
+    CopyFuture future;
+  };
+  bool queued_ = false;
+  std::thread worker_;
+  std::mutex queue_mu_;
+  std::condition_variable queue_cv_;
+  std::deque<QueuedCopy> queue_;
+  bool shutdown_ = false;
+  hipStream_t dep_proxy_ = nullptr;  // carries submission-time dependencies
+  std::mutex log_mu_;
+  std::string dispatch_log_;
   std::mutex slots_mu_;
   std::vector<StagingSlot> all_slots_;
   std::deque<int64_t> free_slots_;

@@ -174,6 +174,10 @@ class KVCacheManager:
         arrays num_kv_layers.. and move with every copy of the same block ids.
       numa: host mirror placement: "auto" (the GPU's NUMA node), "off", or a
         node number.
+      dispatch: "env" (queued when RAIDEN_ENABLE_ASYNC_DISPATCH=1), "queued"
+        (d2h/h2d return at once; one background thread plans and issues the
+        copies in submission order, errors arrive through the future) or
+        "inline".
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
       The remaining reference arguments (ports, worker id, timeout,
       parallelism, unsafe_skip_buffer_lock) configure its networking, which
@@ -193,7 +197,8 @@ class KVCacheManager:
                  shm_server_name: Optional[str] = None,
                  model_uid: Optional[str] = None, profile_kernels: bool = False,
                  transfer_mode: str = "auto", zero_copy_workgroups: int = 0,
-                 scale_tables: Optional[List[Any]] = None, numa: Any = "auto"):
+                 scale_tables: Optional[List[Any]] = None, numa: Any = "auto",
+                 dispatch: str = "env"):
         if host_blocks_to_allocate is None:
             if max_blocks is None or num_slots is None:
                 raise ValueError("Must specify either (max_blocks, num_slots) or"
@@ -224,7 +229,8 @@ class KVCacheManager:
         self._init(device, len(layers), num_shards, ptrs, sizes, major_dim, 0,
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
-                   model_uid, profile_kernels, transfer_mode, zero_copy_workgroups, numa)
+                   model_uid, profile_kernels, transfer_mode, zero_copy_workgroups, numa,
+                   dispatch)
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
             # kv_cache_manager_with_transfer.cc:483-503: slot geometry, then
@@ -234,6 +240,17 @@ class KVCacheManager:
         if raiden_controller_address:
             _capi.check(_capi.load().kvx_manager_register_with_controller(
                 self._h, raiden_controller_address.encode()), "RegisterWorker")
+
+    @property
+    def queued_dispatch(self) -> bool:
+        return bool(_capi.load().kvx_manager_queued_dispatch(self._h))
+
+    def dispatch_log(self) -> str:
+        """Kinds of the last dispatched copies ('D' = d2h, 'H' = h2d), oldest first."""
+        buf = ctypes.create_string_buffer(256)
+        n = ctypes.c_int64()
+        _capi.check(_capi.load().kvx_manager_dispatch_log(self._h, buf, 256, ctypes.byref(n)))
+        return buf.raw[:min(n.value, 256)].decode()
 
     @property
     def assigned_numa_node(self) -> int:
@@ -249,7 +266,7 @@ class KVCacheManager:
               slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
               direct_min_bytes, shm_key, shm_server_name, model_uid,
               profile_kernels=False, transfer_mode="auto", zero_copy_workgroups=0,
-              numa="auto"):
+              numa="auto", dispatch="env"):
         lib = _capi.load()
         kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
                  "shm": _capi.HOST_SHM}
@@ -275,6 +292,7 @@ class KVCacheManager:
         cfg.profile_kernels = int(bool(profile_kernels))
         cfg.transfer_mode = _capi.MODES[transfer_mode]
         cfg.zero_copy_workgroups = zero_copy_workgroups
+        cfg.dispatch = {"env": 0, "queued": 1, "inline": 2}[dispatch]
         if numa == "auto":
             cfg.numa_policy = 0
         elif numa in ("off", None):
