@@ -62,12 +62,14 @@ def parse_args():
                    help="skip the per-mode, one-direction and PCIe-peak measurements")
     p.add_argument("--mode", default="auto", choices=["auto", "staged", "zero_copy"],
                    help="transfer mode of the headline offload/reload loop")
-    p.add_argument("--configs", default="fp8,weights,zipf",
+    p.add_argument("--configs", default="fp8,weights,pools,zipf",
                    help="comma list of extra workloads to measure after the headline "
-                        "(fp8, weights, zipf; empty for none)")
+                        "(fp8, weights, pools, zipf; empty for none)")
     p.add_argument("--zipf-host-blocks", type=int, default=2048,
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks")
     p.add_argument("--zipf-batches", type=int, default=24)
+    p.add_argument("--zipf-docs", type=int, default=8,
+                   help="documents whose hash-chain prefixes the churn requests")
     p.add_argument("--rocpd-summary", metavar="DB",
                    help="print per-kernel (name, grid) duration statistics of a "
                         "rocprofv3 results database and exit")
@@ -375,12 +377,71 @@ def bench_weight_sync(torch, pkg, dev, args):
     return out
 
 
+def bench_pools(torch, pkg, dev, args, rng):
+    """Pool-addressed copies of a sparse (FA-like) pool: per block 4 head
+    groups of 64 tokens x (K 256 B + V 256 B) packed at 70 KiB pitch inside a
+    320 KiB block stride (40 % live). 32 storages x 512 blocks; each step
+    copies 128 random blocks of every pool device->host, then host->device,
+    moving only the live bytes (one strided-copy launch per pool over the
+    pinned mirror), against whole-block copies of the same ids."""
+    L, NB, stride = 32, 512, 327680
+    regions = tuple(pkg.RegionSpec("fa%d" % g, g * 71680, 512, 256, 64, 2) for g in range(4))
+    live = sum(r.live_bytes for r in regions)
+    log(f"pools: allocating {L} x {NB} x {stride} B storages")
+    pools = [torch.empty(NB, stride, dtype=torch.uint8, device=dev) for _ in range(L)]
+    for p in pools:
+        p.random_(0, 256)
+    mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=NB)
+    specs = [pkg.PoolSpec("fa", l, 0, stride, NB, regions) for l in range(L)]
+    mgr.register_pools(specs)
+    n = 128
+
+    def timed(fn, reps):
+        fn()
+        mgr.wait_for_pending_work()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        mgr.wait_for_pending_work()
+        return (time.perf_counter() - t0) / reps
+
+    ids = sorted(rng.choice(NB, n, replace=False).tolist())
+    reps = max(3, args.steps // 2)
+
+    def pool_copy(d2h):
+        fn = mgr.d2h_pool_blocks if d2h else mgr.h2d_pool_blocks
+        futs = [fn(l, ids) for l in range(L)]
+        for f in futs:
+            f.Await()
+
+    t_d2h = timed(lambda: pool_copy(True), reps)
+    t_h2d = timed(lambda: pool_copy(False), reps)
+    t_dense = timed(lambda: mgr.d2h(ids, ids).Await(), reps)
+    live_bytes = L * n * live
+    out = {"workload": "FA-like sparse pool (4 head groups x 32 KiB live per 320 KiB block), "
+                       f"{L} storages x {NB} blocks, {n} random blocks per copy",
+           "live_fraction": round(live / stride, 3),
+           "pool_d2h_live_gbps": round(live_bytes / t_d2h / 1e9, 2),
+           "pool_h2d_live_gbps": round(live_bytes / t_h2d / 1e9, 2),
+           "pool_d2h_ms": round(t_d2h * 1e3, 3),
+           "whole_block_d2h_ms": round(t_dense * 1e3, 3),
+           "speedup_vs_whole_blocks": round(t_dense / t_d2h, 2)}
+    log(f"pools: {out}")
+    mgr.close()
+    del pools
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_zipf_store(torch, pkg, dev, args, rng):
     """Llama-3-70B-shaped KV (80 layers, K and V: 160 storages of 12000 x 32
     KiB blocks, 58.6 GiB) with a host tier of pinned blocks behind the
-    KVCacheStore; prefix-cache churn: batches of 64-2048 block hashes drawn
-    Zipf(1.1); hits are loaded into device blocks, misses inserted and saved
-    (evicting LRU entries once the host tier is full)."""
+    KVCacheStore; prefix-cache churn: each request is a prefix of one of
+    --zipf-docs documents' block-hash chains (document drawn Zipf(1.1), length 64-2048
+    blocks log-uniform). Lookup returns the cached prefix, which is loaded
+    into device blocks; the rest is inserted and saved (evicting LRU entries
+    once the host tier is full). Load (H2D) and save (D2H) of a request are
+    issued together and polled together."""
     L, P, bb = 80, 12000, 32768
     host_blocks = args.zipf_host_blocks
     S = 2 * L
@@ -396,58 +457,62 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
                              staging_chunks=args.chunks,
                              raiden_controller_address=store.raiden_controller_address)
     rid = store.raiden_id
-    universe = 8 * host_blocks
-    # Zipf(1.1) over the universe by inverse CDF.
-    w = 1.0 / np.arange(1, universe + 1) ** 1.1
+    docs = args.zipf_docs
+    w = 1.0 / np.arange(1, docs + 1) ** 1.1
     cdf = np.cumsum(w) / w.sum()
 
-    def poll(fn, want):
-        while True:
-            done, failed = fn()[:2]
-            if failed:
-                raise RuntimeError(f"store transfer failed: {len(failed)} blocks")
-            if len(done) >= want:
-                return
+    def poll_all(want_load, want_save):
+        got_l = got_s = 0
+        while got_l < want_load or got_s < want_save:
+            if got_l < want_load:
+                done, failed = store.poll_load_status()[:2]
+                if failed:
+                    raise RuntimeError(f"store load failed: {len(failed)} blocks")
+                got_l += len(done)
+            if got_s < want_save:
+                done, failed = store.poll_save_status()[:2]
+                if failed:
+                    raise RuntimeError(f"store save failed: {len(failed)} blocks")
+                got_s += len(done)
 
-    moved = saved = loaded = hits = asked = 0
+    moved = saved = loaded = hits = asked = skipped = 0
     t_run = 0.0
     for step in range(args.zipf_batches):
+        doc = int(np.searchsorted(cdf, rng.random()))
         nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
-        keys = np.unique(np.searchsorted(cdf, rng.random(nb)))
-        hashes = [b"z%08d" % k for k in keys]
+        chain = [b"d%03d:%05d" % (doc, i) for i in range(nb)]
+        dev_ids = rng.permutation(P)[:nb].tolist()
         t0 = time.perf_counter()
-        found = store.lookup(hashes, pin_found=False)
-        hit_set = {h for h, _ in found}
-        # lookup() answers up to the first miss; pin and load every resident
-        # hash individually.
-        res = [h for h in hashes if h in hit_set or store.lookup([h], pin_found=False)]
-        res_set = set(res)
-        miss = [h for h in hashes if h not in res_set]
-        dev_ids = rng.permutation(P)[:len(hashes)].tolist()
-        if res:
-            got = [h for h in res if store.lookup([h])]
-            if got:
-                assert store.load(got, dev_ids[:len(got)])
-                poll(store.poll_load_status, len(got))
-                loaded += len(got)
-        if miss:
-            sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM)
-                  for d in dev_ids[len(res):len(res) + len(miss)]]
-            if store.insert(miss, sl, on_host=False):
-                if store.save(miss):
-                    poll(store.poll_save_status, len(miss))
-                    saved += len(miss)
-                else:
-                    store.release(miss)
+        found = store.lookup(chain, pin_found=True)
+        k = len(found)
+        rest = chain[k:]
+        if k:
+            assert store.load(chain[:k], dev_ids[:k])
+        n_save = 0
+        if rest:
+            sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
+            if store.insert(rest, sl, on_host=False):
+                if store.save(rest):
+                    n_save = len(rest)
+                else:  # a block past the prefix is still cached (a hole)
+                    store.release(rest)
+                    skipped += len(rest)
+            else:
+                skipped += len(rest)
+        poll_all(k, n_save)
         t_run += time.perf_counter() - t0
-        hits += len(res)
-        asked += len(hashes)
+        loaded += k
+        saved += n_save
+        hits += k
+        asked += nb
     moved = (saved + loaded) * S * bb
-    out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), Zipf(1.1) "
-                       "prefix-cache churn through the KV store",
+    out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
+                       "churn through the KV store: requests are prefixes (64-2048 blocks) of "
+                       f"{docs} documents' hash chains, document drawn Zipf(1.1)",
            "host_tier_blocks": host_blocks,
            "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
            "batches": args.zipf_batches, "blocks_saved": saved, "blocks_loaded": loaded,
+           "blocks_skipped": skipped,
            "hit_rate": round(hits / max(asked, 1), 4),
            "gbps": round(moved / t_run / 1e9, 2),
            "blocks_per_s": round((saved + loaded) / t_run, 1)}
@@ -609,6 +674,8 @@ def main():
         configs["fp8_kv_scales"] = bench_fp8_scales(torch, pkg, dev, args, rng)
     if "weights" in wanted:
         configs["weight_sync_pack"] = bench_weight_sync(torch, pkg, dev, args)
+    if "pools" in wanted:
+        configs["sparse_pool_copies"] = bench_pools(torch, pkg, dev, args, rng)
     if "zipf" in wanted:
         configs["llama3_70b_zipf_churn"] = bench_zipf_store(torch, pkg, dev, args, rng)
 

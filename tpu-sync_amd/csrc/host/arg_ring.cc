@@ -87,7 +87,7 @@ Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {
 }
 
 Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
-                                hipStream_t stream) {
+                                hipStream_t stream, uint32_t max_workgroups) {
   if (copies.empty()) return OkStatus();
   const int vec = StridedVectorBytes(copies);
   std::vector<StridedEntryDev> table;
@@ -107,7 +107,7 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
   KVX_RETURN_IF_ERROR(ring.Upload(off, bytes, stream));
   KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
       reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
-      static_cast<uint32_t>(table.size()), grid, vec, stream));
+      static_cast<uint32_t>(table.size()), grid, vec, stream, max_workgroups));
   return ring.Commit(off, bytes, stream);
 }
 

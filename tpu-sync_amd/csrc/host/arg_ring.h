@@ -53,10 +53,10 @@ class ArgRing {
 };
 
 // Uploads the table and tile map of `copies` through `ring` and launches the
-// strided-copy kernel on `stream`; the ring region stays reserved until the
-// launch ends.
+// strided-copy kernel on `stream` (at most max_workgroups workgroups when
+// > 0); the ring region stays reserved until the launch ends.
 Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
-                                hipStream_t stream);
+                                hipStream_t stream, uint32_t max_workgroups = 0);
 
 }  // namespace kvx
 

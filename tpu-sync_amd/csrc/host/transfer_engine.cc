@@ -504,7 +504,11 @@ StatusOr<CopyFuture> TransferEngine::CopyExtents(
     extent_args_ = std::move(ring);
   }
   KVX_RETURN_IF_ERROR(WaitDep(dep, ks));
-  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(*extent_args_, copies, ks));
+  // PCIe-bound: a few dozen workgroups keep the link busy (see the
+  // zero-copy caps).
+  const int64_t cap = d2h ? opts_.zero_copy_d2h_workgroups : opts_.zero_copy_h2d_workgroups;
+  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(*extent_args_, copies, ks,
+                                               static_cast<uint32_t>(cap > 0 ? cap : 0)));
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, ks));
   ++stats_.kernel_launches;

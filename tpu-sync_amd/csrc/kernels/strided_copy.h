@@ -56,9 +56,12 @@ bool BuildStridedTable(const std::vector<StridedCopy>& copies, int vec_bytes,
 int StridedVectorBytes(const std::vector<StridedCopy>& copies);
 
 // Launches the copy of a device-resident table of `n` entries (built by
-// BuildStridedTable) on `stream`.
+// BuildStridedTable, `tiles` from its *grid) on `stream`. max_workgroups > 0
+// caps the grid (each workgroup then walks tiles with a stride of the grid),
+// for copies bound by PCIe rather than HBM.
 hipError_t LaunchStridedCopy(const StridedEntryDev* table_dev, uint32_t n,
-                             uint32_t grid, int vec_bytes, hipStream_t stream);
+                             uint32_t tiles, int vec_bytes, hipStream_t stream,
+                             uint32_t max_workgroups = 0);
 
 }  // namespace kvx
 

@@ -33,12 +33,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct KArgs {
   const StridedEntryDev* table;
-  const uint32_t* tile_entry;  // workgroup -> entry index
+  const uint32_t* tile_entry;  // tile -> entry index
+  uint32_t tiles;
 };
 
+// Moves tile `wg` (one entry's rows, or one slice of a long row).
 template <typename V>
-__global__ __launch_bounds__(kThreads) void strided_copy_kernel(KArgs a) {
-  const uint32_t wg = blockIdx.x;
+__device__ __forceinline__ void copy_tile(const KArgs& a, uint32_t wg) {
   const uint32_t e = ((const KVX_CONST uint32_t*)a.tile_entry)[wg];
   const KVX_CONST StridedEntryDev* ent = (const KVX_CONST StridedEntryDev*)a.table + e;
   const uint64_t src = ent->src;
@@ -89,6 +90,13 @@ __global__ __launch_bounds__(kThreads) void strided_copy_kernel(KArgs a) {
       __builtin_nontemporal_store(r[u], (KVX_GLOBAL V*)(dst + doff[u]));
     }
   }
+}
+
+// One tile per workgroup, or (capped grid) tiles blockIdx.x, + gridDim.x, ...
+// The loop bound is uniform, so every wave leaves it together.
+template <typename V>
+__global__ __launch_bounds__(kThreads) void strided_copy_kernel(KArgs a) {
+  for (uint32_t t = blockIdx.x; t < a.tiles; t += gridDim.x) copy_tile<V>(a, t);
 }
 
 }  // namespace
@@ -145,13 +153,15 @@ bool BuildStridedTable(const std::vector<StridedCopy>& copies, int vec_bytes,
 }
 
 hipError_t LaunchStridedCopy(const StridedEntryDev* table_dev, uint32_t n,
-                             uint32_t grid, int vec_bytes, hipStream_t stream) {
-  (void)n;
-  if (grid == 0) return hipSuccess;
+                             uint32_t tiles, int vec_bytes, hipStream_t stream,
+                             uint32_t max_workgroups) {
+  if (tiles == 0) return hipSuccess;
   KArgs a;
   a.table = table_dev;
   // The tile -> entry map follows the table in the same device allocation.
   a.tile_entry = reinterpret_cast<const uint32_t*>(table_dev + n);
+  a.tiles = tiles;
+  const uint32_t grid = max_workgroups > 0 && max_workgroups < tiles ? max_workgroups : tiles;
   switch (vec_bytes) {
     case 16:
       hipLaunchKernelGGL(strided_copy_kernel<u32x4>, dim3(grid), dim3(kThreads), 0, stream, a);
