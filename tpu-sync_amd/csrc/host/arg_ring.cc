@@ -16,11 +16,18 @@ ArgRing::~ArgRing() {
     (void)hipEventSynchronize(s.done);
     (void)hipEventDestroy(s.done);
   }
+  if (upload_ != nullptr) {
+    (void)hipStreamSynchronize(upload_);
+    (void)hipStreamDestroy(upload_);
+  }
   if (host_ != nullptr) (void)hipHostFree(host_);
   if (dev_ != 0) (void)hipFree(reinterpret_cast<void*>(dev_));
 }
 
-Status ArgRing::Init(int64_t bytes) { return Grow(bytes); }
+Status ArgRing::Init(int64_t bytes) {
+  KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&upload_, hipStreamNonBlocking));
+  return Grow(bytes);
+}
 
 Status ArgRing::Grow(int64_t bytes) {
   for (Slice& s : inflight_) {
@@ -46,7 +53,9 @@ Status ArgRing::Grow(int64_t bytes) {
 
 StatusOr<int64_t> ArgRing::Alloc(int64_t bytes) {
   bytes = AlignUp(std::max<int64_t>(bytes, 1));
-  if (bytes > size_) KVX_RETURN_IF_ERROR(Grow(bytes));
+  // Room for several requests of this size, so a launch can be prepared
+  // while the previous ones still read their tables.
+  if (bytes > size_) KVX_RETURN_IF_ERROR(Grow(4 * bytes));
   int64_t start = head_;
   if (start + bytes > size_) start = 0;
   const int64_t end = start + bytes;
@@ -69,9 +78,19 @@ StatusOr<int64_t> ArgRing::Alloc(int64_t bytes) {
 }
 
 Status ArgRing::Upload(int64_t off, int64_t bytes, hipStream_t stream) {
+  if (upload_ == nullptr) {
+    KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(dev_ + off), host_ + off,
+                                           bytes, hipMemcpyHostToDevice, stream));
+    return OkStatus();
+  }
   KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(dev_ + off), host_ + off,
-                                         bytes, hipMemcpyHostToDevice, stream));
-  return OkStatus();
+                                         bytes, hipMemcpyHostToDevice, upload_));
+  hipEvent_t e = nullptr;
+  KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  Status st = HipStatus(hipEventRecord(e, upload_), "hipEventRecord(upload)");
+  if (st.ok()) st = HipStatus(hipStreamWaitEvent(stream, e, 0), "hipStreamWaitEvent(upload)");
+  (void)hipEventDestroy(e);
+  return st;
 }
 
 Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {
