@@ -154,7 +154,7 @@ def test_register_pools_grows_host_mirror(kvx, cuda):
     assert h.size >= 256
     assert np.array_equal(h[:64], np.arange(64, dtype=np.uint8))
     assert mgr.get_block_ref(0, 3)["ptr"] == \
-        kvx._capi.load().kvx_manager_block_array_host_ptr(mgr._h, 0, 0) + 3 * 64
+        kvx._capi.load().kvx_manager_host_ptr(mgr._h, 0, 0) + 3 * 64
     mgr.d2h_pool_blocks(0, [3]).Await()
     assert np.array_equal(mgr.host_view(0)[192:256], u8(shards[0])[192:256])
     # A pool past the device storage is refused (the device size bounds it).

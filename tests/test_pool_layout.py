@@ -320,7 +320,7 @@ def test_pool_block_ref_pointer_math(kvx):
     g = GOLD["manager_block_ref"]
     m = host_mgr(kvx, g["num_layers"], g["slice"], g["host_blocks"])
     m.register_pools([mgr_pool(kvx, *p) for p in g["pools"]])
-    base = kvx._capi.load().kvx_manager_block_array_host_ptr(m._h, 0, 0)
+    base = kvx._capi.load().kvx_manager_host_ptr(m._h, 0, 0)
     for pool_idx, block_id, off in g["refs"]:
         ref = m.get_block_ref(pool_idx, block_id)
         assert ref["ptr"] == base + off
@@ -350,7 +350,7 @@ def test_pool_indices_with_tag_and_base_stride(kvx):
     g = GOLD["manager_base_stride"]
     m = host_mgr(kvx, g["num_layers"], g["slice"], g["host_blocks"])
     m.register_pools([mgr_pool(kvx, *p) for p in g["pools"]])
-    base1 = kvx._capi.load().kvx_manager_block_array_host_ptr(m._h, 1, 0)
+    base1 = kvx._capi.load().kvx_manager_host_ptr(m._h, 1, 0)
     pool_idx, block_id, off = g["ref"]
     assert m.get_block_ref(pool_idx, block_id)["ptr"] == base1 + off
 
@@ -382,3 +382,37 @@ def test_python_admission_surface(kvx):
         m.h2d_pool_blocks(pool_idx=0, block_ids=[0])
     with pytest.raises(ValueError, match="invalid pool 0"):
         m.register_pools([P.PoolSpec("x", 0, 0, 0, 1, (P.RegionSpec("r", 0, 1, 1, 1),))])
+
+
+def test_delegate_addressing_follows_pools(kvx):
+    """Block arrays become pools once registered (kv_cache_manager_base.cc:
+    1470-1523, 2321-2395, 2530-2548), with the reference tests' answers."""
+    lib = kvx._capi.load()
+    g = GOLD["delegate_base_stride"]
+    m = host_mgr(kvx, g["num_layers"], g["slice"], g["host_blocks"])
+    assert m.num_block_arrays() == 2 and m.block_bytes(1) == 128
+    legacy = m.get_block_chunks(1, 0, [1, 3], 200)
+    s1 = m.get_host_pointer(1)
+    assert legacy == [(s1 + 128, 128), (s1 + 3 * 128, 72)]
+    m.register_pools([mgr_pool(kvx, *p) for p in g["pools"]])
+    assert m.num_block_arrays() == 1 and m.block_bytes(0) == 64
+    pool_idx, block_id, off = g["block_ptr"]
+    assert lib.kvx_manager_block_array_block_ptr(m._h, pool_idx, 0, block_id) == s1 + off
+    assert lib.kvx_manager_block_array_block_ptr(m._h, 0, 0, 4) == 0  # past the pool
+    assert m.get_block_array_host_pointer(0) == s1 + 128
+    assert m.get_block_chunks(0, 0, g["chunks_ids"], g["chunks_total"]) == \
+        [(s1 + o, n) for o, n in g["chunks"]]
+    assert m.get_block_chunks(0, 0, [4], 64) == []  # out of the pool: no chunks
+    assert m.get_block_chunks(3, 0, [0], 64) == []
+    g = GOLD["delegate_aliased"]
+    m = host_mgr(kvx, g["num_layers"], g["slice"], g["host_blocks"])
+    m.register_pools([mgr_pool(kvx, *p) for p in g["pools"]])
+    s0 = m.get_host_pointer(0)
+    assert m.get_block_array_host_size(0) == g["block_array_size"]
+    assert m.get_block_ref(0, 1)["ptr"] == s0 + g["ref_block1"]
+    assert m.get_block_chunks(0, 0, g["chunks_ids"], g["chunks_total"]) == \
+        [(s0 + o, n) for o, n in g["chunks"]]
+    g = GOLD["delegate_two_pools"]
+    m = host_mgr(kvx, g["num_layers"], g["slice"], g["host_blocks"])
+    m.register_pools([mgr_pool(kvx, *p) for p in g["pools"]])
+    assert m.num_block_arrays() == g["num_block_arrays"]

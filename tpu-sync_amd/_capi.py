@@ -344,6 +344,11 @@ PROTOTYPES = {
     "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
                                 ctypes.POINTER(_vp)]),
     "kvx_manager_numa_node": (_i32, [_vp]),
+    "kvx_manager_host_ptr": (_u64, [_vp, _i64, _i64]),
+    "kvx_manager_host_size": (_i64, [_vp, _i64, _i64]),
+    "kvx_manager_block_array_block_ptr": (_u64, [_vp, _i64, _i64, _i64]),
+    "kvx_manager_block_chunks": (_int, [_vp, _i64, _i64, _i64p, _i64, _i64, _u64p, _i64p, _i64,
+                                        _i64p]),
     "kvx_manager_queued_dispatch": (_i32, [_vp]),
     "kvx_manager_dispatch_log": (_int, [_vp, ctypes.c_char_p, _i64, _i64p]),
     "kvx_gpu_numa_node": (_i32, [_i32]),

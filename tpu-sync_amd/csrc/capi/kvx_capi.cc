@@ -390,6 +390,40 @@ int64_t kvx_manager_layer_block_byte_size(const kvx_manager* m, int64_t layer_id
   if (m == nullptr || layer_idx < 0) return -1;
   return m->impl->LayerBlockByteSize(static_cast<size_t>(layer_idx));
 }
+uint64_t kvx_manager_host_ptr(kvx_manager* m, int64_t layer_idx, int64_t shard_idx) {
+  if (m == nullptr || layer_idx < 0 || shard_idx < 0) return 0;
+  return reinterpret_cast<uint64_t>(
+      m->impl->GetHostPointer(static_cast<size_t>(layer_idx), static_cast<size_t>(shard_idx)));
+}
+int64_t kvx_manager_host_size(kvx_manager* m, int64_t layer_idx, int64_t shard_idx) {
+  if (m == nullptr || layer_idx < 0 || shard_idx < 0) return 0;
+  return static_cast<int64_t>(
+      m->impl->GetHostSize(static_cast<size_t>(layer_idx), static_cast<size_t>(shard_idx)));
+}
+uint64_t kvx_manager_block_array_block_ptr(kvx_manager* m, int64_t block_array_idx,
+                                           int64_t shard_idx, int64_t block_id) {
+  if (m == nullptr || block_array_idx < 0 || shard_idx < 0) return 0;
+  return reinterpret_cast<uint64_t>(m->impl->GetBlockHostPointer(
+      static_cast<size_t>(block_array_idx), static_cast<size_t>(shard_idx), block_id));
+}
+int kvx_manager_block_chunks(kvx_manager* m, int64_t block_array_idx, int64_t shard_idx,
+                             const int64_t* block_ids, int64_t n, int64_t total_bytes,
+                             uint64_t* out_ptrs, int64_t* out_sizes, int64_t cap,
+                             int64_t* n_out) {
+  if (m == nullptr || n_out == nullptr || BadArray(block_ids, n) || BadArray(out_ptrs, cap) ||
+      BadArray(out_sizes, cap) || block_array_idx < 0 || shard_idx < 0 || total_bytes < 0) {
+    return Fail(KVX_INVALID_ARGUMENT, "invalid argument");
+  }
+  const auto chunks = m->impl->GetBlockChunks(
+      static_cast<size_t>(block_array_idx), static_cast<size_t>(shard_idx),
+      std::vector<int64_t>(block_ids, block_ids + n), static_cast<size_t>(total_bytes));
+  *n_out = static_cast<int64_t>(chunks.size());
+  for (int64_t i = 0; i < *n_out && i < cap; ++i) {
+    out_ptrs[i] = reinterpret_cast<uint64_t>(chunks[static_cast<size_t>(i)].ptr);
+    out_sizes[i] = static_cast<int64_t>(chunks[static_cast<size_t>(i)].size);
+  }
+  return KVX_OK;
+}
 int64_t kvx_manager_num_block_arrays(const kvx_manager* m) {
   return m ? static_cast<int64_t>(m->impl->num_block_arrays()) : -1;
 }

@@ -638,7 +638,21 @@ int64_t KVCacheManager::LayerBlockByteSize(size_t layer_idx) const {
   return layer_block_bytes_[layer_idx];
 }
 
+size_t KVCacheManager::num_block_arrays() const {
+  std::lock_guard<std::mutex> l(pools_mu_);
+  return explicit_pools_ ? pools_.size() : static_cast<size_t>(num_layers_);
+}
+
 size_t KVCacheManager::block_bytes(size_t block_array_idx) const {
+  {
+    std::lock_guard<std::mutex> l(pools_mu_);
+    if (explicit_pools_) {
+      if (block_array_idx >= pools_.size() || pools_[block_array_idx].block_stride_bytes <= 0) {
+        return 0;
+      }
+      return static_cast<size_t>(pools_[block_array_idx].block_stride_bytes);
+    }
+  }
   const int64_t per_layer = LayerBlockByteSize(block_array_idx);
   if (per_layer > 0) return static_cast<size_t>(per_layer);
   return bytes_per_block();
@@ -646,12 +660,91 @@ size_t KVCacheManager::block_bytes(size_t block_array_idx) const {
 
 uint8_t* KVCacheManager::GetBlockArrayHostPointer(size_t block_array_idx,
                                                   size_t shard_idx) {
-  return GetHostPointer(block_array_idx, shard_idx);
+  PoolSpec p;
+  {
+    std::lock_guard<std::mutex> l(pools_mu_);
+    if (!explicit_pools_) return GetHostPointer(block_array_idx, shard_idx);
+    if (block_array_idx >= pools_.size()) return nullptr;
+    p = pools_[block_array_idx];
+  }
+  uint8_t* base = GetHostPointer(p.storage_index, shard_idx);
+  return base == nullptr ? nullptr : base + p.base_offset_bytes;
 }
 
 size_t KVCacheManager::GetBlockArrayHostSize(size_t block_array_idx,
                                              size_t shard_idx) {
-  return GetHostSize(block_array_idx, shard_idx);
+  PoolSpec p;
+  {
+    std::lock_guard<std::mutex> l(pools_mu_);
+    if (!explicit_pools_) return GetHostSize(block_array_idx, shard_idx);
+    if (block_array_idx >= pools_.size()) return 0;
+    p = pools_[block_array_idx];
+  }
+  const size_t storage = GetHostSize(p.storage_index, shard_idx);
+  const int64_t end = p.storage_extent_end_bytes();
+  if (end < p.base_offset_bytes || static_cast<uint64_t>(end) > storage ||
+      static_cast<size_t>(p.base_offset_bytes) > storage) {
+    return 0;
+  }
+  return static_cast<size_t>(end - p.base_offset_bytes);
+}
+
+uint8_t* KVCacheManager::GetBlockHostPointer(size_t block_array_idx, size_t shard_idx,
+                                             int64_t block_id) {
+  {
+    std::lock_guard<std::mutex> l(pools_mu_);
+    if (explicit_pools_ && (block_array_idx >= pools_.size() || block_id < 0 ||
+                            block_id >= pools_[block_array_idx].num_blocks)) {
+      return nullptr;
+    }
+  }
+  uint8_t* base = GetBlockArrayHostPointer(block_array_idx, shard_idx);
+  if (base == nullptr || block_id < 0) return nullptr;
+  return base + static_cast<size_t>(block_id) * block_bytes(block_array_idx);
+}
+
+std::vector<KVCacheManager::BlockChunk> KVCacheManager::GetBlockChunks(
+    size_t block_array_idx, size_t shard_idx, const std::vector<int64_t>& block_ids,
+    size_t total_bytes) {
+  std::vector<BlockChunk> chunks;
+  size_t acc = 0;
+  PoolSpec p;
+  bool pools = false;
+  {
+    std::lock_guard<std::mutex> l(pools_mu_);
+    pools = explicit_pools_;
+    if (pools) {
+      if (block_array_idx >= pools_.size()) return {};
+      p = pools_[block_array_idx];
+    }
+  }
+  if (pools) {
+    for (int64_t id : block_ids) {
+      if (id < 0 || id >= p.num_blocks) return {};
+    }
+    uint8_t* storage_base = GetHostPointer(p.storage_index, shard_idx);
+    if (storage_base == nullptr) return {};
+    for (int64_t id : block_ids) {
+      if (acc >= total_bytes) break;
+      StatusOr<std::vector<PoolBlockCopyExtent>> ext = ComputePoolBlockCopyExtents(p, {id});
+      if (!ext.ok()) return {};
+      for (const PoolBlockCopyExtent& e : *ext) {
+        if (acc >= total_bytes) break;
+        const size_t size = std::min(static_cast<size_t>(e.size_bytes), total_bytes - acc);
+        chunks.push_back(BlockChunk{storage_base + e.offset_bytes, size});
+        acc += size;
+      }
+    }
+    return chunks;
+  }
+  const size_t bb = block_bytes(block_array_idx);
+  for (int64_t id : block_ids) {
+    if (acc >= total_bytes) break;
+    const size_t size = std::min(bb, total_bytes - acc);
+    chunks.push_back(BlockChunk{GetBlockHostPointer(block_array_idx, shard_idx, id), size});
+    acc += size;
+  }
+  return chunks;
 }
 
 StatusOr<uintptr_t> KVCacheManager::GetBlockHostPointerValue(size_t layer_idx,

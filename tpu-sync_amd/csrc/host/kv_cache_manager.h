@@ -236,10 +236,25 @@ class KVCacheManager {
   LogicalBlockManager* host_block_manager() const { return lbm_.get(); }
   std::mutex& host_block_mutex() { return lbm_mu_; }
   size_t bytes_per_block() const { return static_cast<size_t>(slice_byte_size_); }
-  size_t num_block_arrays() const { return static_cast<size_t>(num_layers_); }
+  // Block-array addressing of the transport delegate
+  // (kv_cache_manager_base.cc:1470-1523, 2321-2395, 2530-2548): the layers,
+  // or -- once RegisterPools has succeeded -- the pools (a pool's blocks start
+  // at its base offset and stride at its block stride). GetBlockChunks lists
+  // the host ranges that carry `total_bytes` of the given blocks: whole
+  // blocks, or each pool block's live extents (the reference's path without
+  // a registered transfer plan; plans belong to its network transport).
+  size_t num_block_arrays() const;
   size_t block_bytes(size_t block_array_idx) const;
   uint8_t* GetBlockArrayHostPointer(size_t block_array_idx, size_t shard_idx);
   size_t GetBlockArrayHostSize(size_t block_array_idx, size_t shard_idx);
+  uint8_t* GetBlockHostPointer(size_t block_array_idx, size_t shard_idx, int64_t block_id);
+  struct BlockChunk {
+    uint8_t* ptr = nullptr;
+    size_t size = 0;
+  };
+  std::vector<BlockChunk> GetBlockChunks(size_t block_array_idx, size_t shard_idx,
+                                         const std::vector<int64_t>& block_ids,
+                                         size_t total_bytes);
   int64_t LayerBlockByteSize(size_t layer_idx) const;
   size_t GetAllocatedHostDramBytes() const { return allocated_host_bytes_; }
 
@@ -349,7 +364,7 @@ class KVCacheManager {
   std::mutex slots_mu_;
   std::vector<StagingSlot> all_slots_;
   std::deque<int64_t> free_slots_;
-  std::mutex pools_mu_;
+  mutable std::mutex pools_mu_;
   std::vector<PoolSpec> pools_;
   bool explicit_pools_ = false;
 };

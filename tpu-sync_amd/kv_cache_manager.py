@@ -452,8 +452,8 @@ class KVCacheManager:
         """numpy uint8 view of one (layer, shard) host mirror (no copy)."""
         import numpy as np
         lib = _capi.load()
-        ptr = lib.kvx_manager_block_array_host_ptr(self._h, layer_idx, shard_idx)
-        size = lib.kvx_manager_block_array_host_size(self._h, layer_idx, shard_idx)
+        ptr = lib.kvx_manager_host_ptr(self._h, layer_idx, shard_idx)
+        size = lib.kvx_manager_host_size(self._h, layer_idx, shard_idx)
         if not ptr or size <= 0:
             return np.zeros(0, np.uint8)
         return np.ctypeslib.as_array((ctypes.c_uint8 * size).from_address(ptr))
@@ -671,6 +671,35 @@ class KVCacheManager:
 
     def layer_block_byte_size(self, layer_idx: int) -> int:
         return _capi.load().kvx_manager_layer_block_byte_size(self._h, layer_idx)
+
+    def get_host_pointer(self, layer_idx: int, shard_idx: int = 0) -> int:
+        return int(_capi.load().kvx_manager_host_ptr(self._h, layer_idx, shard_idx))
+
+    def get_host_size(self, layer_idx: int, shard_idx: int = 0) -> int:
+        return int(_capi.load().kvx_manager_host_size(self._h, layer_idx, shard_idx))
+
+    def get_block_array_host_pointer(self, block_array_idx: int, shard_idx: int = 0) -> int:
+        return int(_capi.load().kvx_manager_block_array_host_ptr(self._h, block_array_idx,
+                                                                 shard_idx))
+
+    def get_block_array_host_size(self, block_array_idx: int, shard_idx: int = 0) -> int:
+        return int(_capi.load().kvx_manager_block_array_host_size(self._h, block_array_idx,
+                                                                  shard_idx))
+
+    def get_block_chunks(self, block_array_idx: int, shard_idx: int, block_ids: Sequence[int],
+                         total_bytes: int) -> List[Tuple[int, int]]:
+        """(host pointer, size) ranges carrying total_bytes of the blocks."""
+        ids, n = _capi.i64_array(block_ids)
+        cap = 256
+        while True:
+            ptrs, sizes = (ctypes.c_uint64 * cap)(), (ctypes.c_int64 * cap)()
+            got = ctypes.c_int64()
+            _capi.check(_capi.load().kvx_manager_block_chunks(
+                self._h, block_array_idx, shard_idx, ids, n, total_bytes, ptrs, sizes, cap,
+                ctypes.byref(got)))
+            if got.value <= cap:
+                return [(ptrs[i], sizes[i]) for i in range(got.value)]
+            cap = got.value
 
     def num_block_arrays(self) -> int:
         return _capi.load().kvx_manager_num_block_arrays(self._h)
