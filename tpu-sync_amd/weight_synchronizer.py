@@ -239,6 +239,20 @@ class WeightSynchronizer:
     def push_weights(self, peers: List[str]) -> None:
         raise NotImplementedError("networked weight pushes are not part of this build")
 
+    # The reference's listener accessors (tpu_sync/api/torch/weight_synchronizer.py:
+    # 95-108): Optional ports, None when no listener runs -- none does here.
+    @property
+    def local_port(self) -> Optional[int]:
+        return None
+
+    @property
+    def listener_port(self) -> Optional[int]:
+        return None
+
+    @property
+    def is_listener_active(self) -> bool:
+        return False
+
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
         if h and _capi._lib is not None:
