@@ -68,6 +68,8 @@ def parse_args():
     p.add_argument("--zipf-host-blocks", type=int, default=2048,
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks")
     p.add_argument("--zipf-batches", type=int, default=24)
+    p.add_argument("--zipf-host-alloc", default="pinned", choices=["pinned", "shm"],
+                   help="host tier memory: pinned (hipHostMalloc) or a /dev/shm segment")
     p.add_argument("--zipf-docs", type=int, default=8,
                    help="documents whose hash-chain prefixes the churn requests")
     p.add_argument("--rocpd-summary", metavar="DB",
@@ -452,10 +454,14 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
         p.random_(0, 256)
     store = pkg.KVCacheStore(capacity=host_blocks, num_shards=1, store_server_ip="127.0.0.1",
                              metadata_shm_key="")
+    tier = {}
+    if args.zipf_host_alloc == "shm":
+        tier = {"host_alloc": "shm", "shm_key": f"kvx_bench_{os.getpid()}"}
     mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=host_blocks,
                              staging_chunk_bytes=args.chunk_mib << 20,
                              staging_chunks=args.chunks,
-                             raiden_controller_address=store.raiden_controller_address)
+                             raiden_controller_address=store.raiden_controller_address,
+                             **tier)
     rid = store.raiden_id
     docs = args.zipf_docs
     w = 1.0 / np.arange(1, docs + 1) ** 1.1
@@ -509,7 +515,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
                        "churn through the KV store: requests are prefixes (64-2048 blocks) of "
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
-           "host_tier_blocks": host_blocks,
+           "host_tier_blocks": host_blocks, "host_tier_memory": args.zipf_host_alloc,
            "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
            "batches": args.zipf_batches, "blocks_saved": saved, "blocks_loaded": loaded,
            "blocks_skipped": skipped,
@@ -519,6 +525,12 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     log(f"zipf: {out}")
     mgr.close()
     store.close()
+    if tier:
+        # The library never unlinks a host-tier segment (it outlives the
+        # process by design); the benchmark removes its own.
+        seg = f"/dev/shm/{tier['shm_key']}_dev_{dev.index or 0}"
+        if os.path.exists(seg):
+            os.unlink(seg)
     del pools
     torch.cuda.empty_cache()
     return out

@@ -112,6 +112,9 @@ typedef struct kvx_manager_config {
   int32_t numa_policy;          /* KVX_NUMA_*: host mirror placement */
   int32_t numa_node;            /* KVX_NUMA_NODE: the node */
   int32_t dispatch;             /* KVX_DISPATCH_*: how D2h/H2d are issued */
+  int32_t host_copy_threads;    /* pageable host mirrors (malloc, shm): host
+                                   threads of the pinned bounce lanes; 0 = 8,
+                                   -1 = per-run pageable hipMemcpyAsync */
 } kvx_manager_config;
 
 /* D2h/H2d dispatch (kv_cache_manager_base.cc:452-512, 2575-2630): ENV (0)
@@ -246,7 +249,7 @@ int kvx_manager_wait_for_pending_work(kvx_manager* m);
 /* Counters of what the transfer engine issued: out[0..6] = direct copies,
  * staged copies, hipMemcpyAsync calls, kernel launches, staging chunks,
  * zero-copy copies, pool-extent kernel copies. */
-int kvx_manager_engine_stats(kvx_manager* m, int64_t* out7);
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out8);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the
  * gather (gather = 1) or scatter (gather = 0) kernels so far. Waits for the

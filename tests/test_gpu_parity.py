@@ -96,11 +96,18 @@ PATHS = {
     "staged": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                    transfer_mode="staged"),
     "zero_copy": dict(direct_min_bytes=1 << 40, transfer_mode="zero_copy"),
+    # Pageable mirror through the pinned bounce lanes: 2 slots of 64 KiB, so
+    # slots are drained and refilled inside one copy; 3 host threads.
+    "bounce": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                   host_alloc="malloc", host_copy_threads=3),
+    # Pageable mirror left to the runtime's per-run hipMemcpyAsync.
+    "pageable": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                     host_alloc="malloc", host_copy_threads=-1),
 }
 MODES = ["staged", "zero_copy"]
 
 
-@pytest.mark.parametrize("path", ["direct", "staged", "zero_copy"])
+@pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "pageable"])
 @pytest.mark.parametrize("bb", [32768, 1024, 48, 36, 3])
 def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
     rng = np.random.default_rng(bb * 7 + len(path))
@@ -123,9 +130,10 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
         assert mir.transfer(d2h, src, dst, sizes, layer, shard) == 0
         mir.check(mgr, dev)
     stats = mgr.engine_stats()
-    if path == "staged":
+    if path in ("staged", "bounce", "pageable"):
         assert stats["direct_copies"] == 0 and stats["staged_copies"] == 12
         assert stats["chunks"] > 12 or bb < 1024
+        assert stats["bounce_copies"] == (12 if path == "bounce" else 0)
     elif path == "zero_copy":
         assert stats["zero_copy_copies"] == 12 and stats["memcpy_calls"] == 0
     else:
@@ -508,6 +516,42 @@ def test_llama3_8b_pool_full_size_round_trip(kvx, cuda, mode):
     stats = mgr.engine_stats()
     key = "staged_copies" if mode == "staged" else "zero_copy_copies"
     assert stats[key] == 2 and stats["kernel_launches"] >= 2
+    mgr.close()
+
+
+@pytest.mark.parametrize("threads", [1, 0])
+def test_bounce_lanes_overlap_and_drain(kvx, oracle, cuda, threads):
+    """Pageable mirror: 8 offloads and 8 reloads of disjoint host ranges are
+    issued without waiting (the two lanes run them concurrently, each in
+    submission order); wait_for_pending_work drains both lanes, then device
+    and host equal the oracle's. threads=1: the issuing thread alone copies."""
+    rng = np.random.default_rng(41 + threads)
+    layers, blocks, bb, hb = 4, 64, 16384, 64
+    host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
+    mgr = make_mgr(kvx, dev, hb, host_alloc="malloc", staging_chunk_bytes=1 << 18,
+                   staging_chunks=3, direct_min_bytes=1 << 40, host_copy_threads=threads)
+    mir = Mirror(host, hb)
+    # Host blocks 32..63 hold data to reload; 0..31 receive offloads.
+    for l in range(layers):
+        fill = rng.integers(0, 256, 32 * bb, dtype=np.uint8)
+        mgr.host_view(l)[32 * bb:] = fill
+        mir.host[l][32 * bb:] = fill
+    futs = []
+    for i in range(8):
+        src = [int(x) for x in rng.choice(32, 4, replace=False)]
+        print(f"threads={threads} round {i} offload {src} -> {4 * i}..", flush=True)
+        futs.append(mgr.d2h(src, [4 * i + k for k in range(4)], [1] * 4))
+        assert mir.transfer(True, src, [4 * i + k for k in range(4)], [1] * 4) == 0
+        hsrc = [32 + int(x) for x in rng.choice(32, 4, replace=False)]
+        dst = [32 + 4 * i + k for k in range(4)]
+        futs.append(mgr.h2d(hsrc, dst, [1] * 4))
+        assert mir.transfer(False, hsrc, dst, [1] * 4) == 0
+    mgr.wait_for_pending_work()
+    for f in futs:
+        assert f.is_ready()
+        f.Await()
+    mir.check(mgr, dev)
+    assert mgr.engine_stats()["bounce_copies"] == 16
     mgr.close()
 
 

@@ -57,6 +57,7 @@ class ManagerConfig(ctypes.Structure):
         ("numa_policy", ctypes.c_int32),
         ("numa_node", ctypes.c_int32),
         ("dispatch", ctypes.c_int32),
+        ("host_copy_threads", ctypes.c_int32),
     ]
 
 

@@ -148,6 +148,12 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
     default:
       return Fail(KVX_INVALID_ARGUMENT, "unknown numa_policy");
   }
+  if (cfg->host_copy_threads > 64) {
+    return Fail(KVX_INVALID_ARGUMENT, "host_copy_threads must be at most 64");
+  }
+  if (cfg->host_copy_threads != 0) {
+    c.engine.host_copy_threads = cfg->host_copy_threads < 0 ? 0 : cfg->host_copy_threads;
+  }
   if (cfg->zero_copy_workgroups > 0) {
     c.engine.zero_copy_d2h_workgroups = cfg->zero_copy_workgroups;
     c.engine.zero_copy_h2d_workgroups = cfg->zero_copy_workgroups;
@@ -450,19 +456,20 @@ int kvx_manager_wait_for_pending_work(kvx_manager* m) {
   if (m == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager");
   return Done(m->impl->WaitForPendingWork());
 }
-int kvx_manager_engine_stats(kvx_manager* m, int64_t* out7) {
-  if (m == nullptr || out7 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+int kvx_manager_engine_stats(kvx_manager* m, int64_t* out8) {
+  if (m == nullptr || out8 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
   if (m->impl->engine() == nullptr) {
     return Fail(KVX_FAILED_PRECONDITION, "CPU-only manager has no transfer engine");
   }
   kvx::EngineStats s = m->impl->engine()->stats();
-  out7[0] = s.direct_copies;
-  out7[1] = s.staged_copies;
-  out7[2] = s.memcpy_calls;
-  out7[3] = s.kernel_launches;
-  out7[4] = s.chunks;
-  out7[5] = s.zero_copy_copies;
-  out7[6] = s.extent_kernel_copies;
+  out8[0] = s.direct_copies;
+  out8[1] = s.staged_copies;
+  out8[2] = s.memcpy_calls;
+  out8[3] = s.kernel_launches;
+  out8[4] = s.chunks;
+  out8[5] = s.zero_copy_copies;
+  out8[6] = s.extent_kernel_copies;
+  out8[7] = s.bounce_copies;
   return KVX_OK;
 }
 

@@ -6,15 +6,39 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cerrno>
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "hip_util.h"
 #include "numa.h"
 
 namespace kvx {
+namespace {
+
+// Writes one byte per 4 KiB page so the pages exist (on the preferred node)
+// before the first copy lands; up to 8 threads of at least 256 MiB each.
+void FirstTouch(uint8_t* p, size_t bytes) {
+  constexpr size_t kPage = 4096;
+  constexpr size_t kMinShare = 256u << 20;
+  const size_t hw = std::max(1u, std::thread::hardware_concurrency());
+  const size_t n = std::max<size_t>(1, std::min<size_t>({8, hw, bytes / kMinShare}));
+  const size_t share = (bytes / n + kPage - 1) / kPage * kPage;
+  auto touch = [p, bytes](size_t lo, size_t hi) {
+    volatile uint8_t* v = p;
+    for (size_t i = lo; i < hi && i < bytes; i += kPage) v[i] = 0;
+  };
+  std::vector<std::thread> ts;
+  for (size_t t = 1; t < n; ++t) ts.emplace_back(touch, t * share, (t + 1) * share);
+  touch(0, share);
+  for (std::thread& t : ts) t.join();
+}
+
+}  // namespace
 
 StatusOr<HostBufferAllocation> AllocateMallocHost(size_t bytes, int numa_node) {
   HostBufferAllocation a;
@@ -155,6 +179,9 @@ StatusOr<HostBufferAllocation> AllocateShmHost(const std::string& name,
     h->itemsize = expected.itemsize;
     h->total_payload_bytes = bytes;
     h->reference_count = 1;
+    // host_memory_allocator.cc:388-392: a fresh segment is faulted in at
+    // creation, so copies never pay the page faults.
+    FirstTouch(static_cast<uint8_t*>(map) + sizeof(SharedMemoryHeader), bytes);
   }
   HostBufferAllocation a;
   a.ptr = static_cast<uint8_t*>(map) + sizeof(SharedMemoryHeader);

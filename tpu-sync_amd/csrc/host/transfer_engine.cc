@@ -1,8 +1,11 @@
 #include "transfer_engine.h"
 
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <cstring>
 #include <numeric>
+#include <thread>
 
 #include "../kernels/block_copy.h"
 #include "../kernels/strided_copy.h"
@@ -78,6 +81,126 @@ StatusOr<StagingLayout> DeviceStagingLayout(const std::vector<int64_t>& block_by
   return out;
 }
 
+// Pinned bounce buffers of a pageable lane (one per staging-ring slot) and
+// the host threads that move bytes between them and pageable host memory.
+struct TransferEngine::Bounce {
+  struct Segment {
+    uint8_t* dst;
+    const uint8_t* src;
+    size_t bytes;
+  };
+  std::vector<uint8_t*> bufs;
+  std::vector<hipEvent_t> dma_done;  // last DMA into (D2H) or out of (H2D) bufs[k]
+  std::vector<bool> used;
+  std::vector<std::vector<Segment>> owed;  // D2H: host copies still due from bufs[k]
+  std::deque<size_t> order;                // D2H: slots with copies owed, oldest first
+
+  // A fixed pool of threads running parallel memcpy batches.
+  explicit Bounce(int threads) {
+    for (int t = 0; t < threads; ++t) workers.emplace_back([this] { Work(); });
+  }
+  ~Bounce() {
+    {
+      std::lock_guard<std::mutex> l(mu);
+      stop = true;
+    }
+    cv.notify_all();
+    for (std::thread& t : workers) t.join();
+    for (uint8_t* b : bufs) (void)hipHostFree(b);
+    for (hipEvent_t e : dma_done) (void)hipEventDestroy(e);
+  }
+  // Copies every segment (split into pieces of at most 4 MiB) with the pool
+  // and the calling thread; returns when all are done.
+  void Copy(const std::vector<Segment>& segs) {
+    constexpr size_t kPiece = 4u << 20;
+    std::vector<Segment> pieces;
+    for (const Segment& s : segs) {
+      for (size_t o = 0; o < s.bytes; o += kPiece) {
+        pieces.push_back(Segment{s.dst + o, s.src + o, std::min(kPiece, s.bytes - o)});
+      }
+    }
+    if (pieces.empty()) return;
+    {
+      std::lock_guard<std::mutex> l(mu);
+      batch = &pieces;
+      next.store(0);
+      left = pieces.size();
+      ++generation;
+    }
+    cv.notify_all();
+    Drain(&pieces);
+    std::unique_lock<std::mutex> l(mu);
+    done_cv.wait(l, [this] { return left == 0 && active == 0; });
+    batch = nullptr;
+  }
+
+ private:
+  void Drain(std::vector<Segment>* p) {
+    size_t finished = 0;
+    for (size_t i = next.fetch_add(1); i < p->size(); i = next.fetch_add(1)) {
+      const Segment& s = (*p)[i];
+      std::memcpy(s.dst, s.src, s.bytes);
+      ++finished;
+    }
+    if (finished > 0) {
+      std::lock_guard<std::mutex> l(mu);
+      left -= finished;
+      if (left == 0 && active == 0) done_cv.notify_all();
+    }
+  }
+  void Work() {
+    uint64_t seen = 0;
+    while (true) {
+      std::vector<Segment>* p = nullptr;
+      {
+        std::unique_lock<std::mutex> l(mu);
+        cv.wait(l, [&] { return stop || (generation != seen && batch != nullptr); });
+        if (stop) return;
+        seen = generation;
+        p = batch;
+        ++active;
+      }
+      Drain(p);
+      std::lock_guard<std::mutex> l(mu);
+      if (--active == 0 && left == 0) done_cv.notify_all();
+    }
+  }
+  std::vector<std::thread> workers;
+  std::mutex mu;
+  std::condition_variable cv, done_cv;
+  std::vector<Segment>* batch = nullptr;
+  std::atomic<size_t> next{0};
+  size_t left = 0;
+  int active = 0;  // workers inside Drain of the current batch
+  uint64_t generation = 0;
+  bool stop = false;
+};
+
+// One direction of pageable-host copies: a worker thread runs queued copies
+// in order on the lane's own streams, staging ring, argument ring and bounce
+// buffers, so a save and a load through /dev/shm overlap.
+struct TransferEngine::PageableLane {
+  struct Job {
+    Direction dir;
+    std::vector<StorageView> storages;
+    std::vector<int64_t> cdev, chost;
+    hipEvent_t dep_event = nullptr;
+    CopyFuture future;
+  };
+  std::thread worker;
+  std::mutex mu;
+  std::condition_variable cv, idle_cv;
+  std::deque<Job> jobs;
+  bool stop = false;
+  bool running = false;
+  hipStream_t ks = nullptr, cs = nullptr;
+  Ring ring;
+  ArgRing args;
+  std::unique_ptr<Bounce> bounce;
+};
+
+TransferEngine::TransferEngine(const EngineOptions& opts) : opts_(opts) {}
+
 StatusOr<std::unique_ptr<TransferEngine>> TransferEngine::Create(
     const EngineOptions& opts) {
   if (opts.staging_chunk_bytes <= 0 || opts.staging_chunks <= 0 ||
@@ -116,7 +239,29 @@ Status TransferEngine::Init() {
 }
 
 TransferEngine::~TransferEngine() {
+  // Pageable lanes finish their queued copies, then release their memory.
+  for (std::unique_ptr<PageableLane>& lane : lanes_) {
+    if (!lane) continue;
+    {
+      std::lock_guard<std::mutex> l(lane->mu);
+      lane->stop = true;
+    }
+    lane->cv.notify_all();
+    lane->worker.join();
+  }
   DeviceGuard g(opts_.device);
+  for (std::unique_ptr<PageableLane>& lane : lanes_) {
+    if (!lane) continue;
+    (void)hipStreamSynchronize(lane->ks);
+    (void)hipStreamSynchronize(lane->cs);
+    for (uint64_t b : lane->ring.bufs) (void)hipFree(reinterpret_cast<void*>(b));
+    for (hipEvent_t e : lane->ring.ready) (void)hipEventDestroy(e);
+    for (hipEvent_t e : lane->ring.free) (void)hipEventDestroy(e);
+    lane->bounce.reset();
+    (void)hipStreamDestroy(lane->ks);
+    (void)hipStreamDestroy(lane->cs);
+    lane.reset();
+  }
   for (hipStream_t s :
        {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
     if (s != nullptr) (void)hipStreamSynchronize(s);
@@ -148,7 +293,20 @@ EngineStats TransferEngine::stats() const {
 }
 
 Status TransferEngine::Synchronize() {
+  {
+    std::lock_guard<std::mutex> l(lanes_mu_);
+    for (std::unique_ptr<PageableLane>& lane : lanes_) {
+      if (!lane) continue;
+      std::unique_lock<std::mutex> ll(lane->mu);
+      lane->idle_cv.wait(ll, [&] { return lane->jobs.empty() && !lane->running; });
+    }
+  }
   DeviceGuard g(opts_.device);
+  for (std::unique_ptr<PageableLane>& lane : lanes_) {
+    if (!lane) continue;
+    KVX_HIP_RETURN_IF_ERROR(hipStreamSynchronize(lane->ks));
+    KVX_HIP_RETURN_IF_ERROR(hipStreamSynchronize(lane->cs));
+  }
   for (hipStream_t s :
        {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
     KVX_HIP_RETURN_IF_ERROR(hipStreamSynchronize(s));
@@ -311,13 +469,26 @@ StatusOr<CopyFuture> TransferEngine::Copy(
     if (s > 0) min_run = std::min(min_run, s);
   }
   if (total == 0 || storages.empty()) return CopyFuture();
-  int64_t min_block = INT64_MAX;
-  for (const StorageView& s : storages) min_block = std::min(min_block, s.block_bytes);
+  int64_t min_block = INT64_MAX, max_block = 0;
+  bool host_ok = true;
+  for (const StorageView& s : storages) {
+    min_block = std::min(min_block, s.block_bytes);
+    max_block = std::max(max_block, s.block_bytes);
+    host_ok = host_ok && s.host_kernel_access;
+  }
+  if (!host_ok && opts_.host_copy_threads > 0 && opts_.mode != TransferMode::kZeroCopy &&
+      max_block <= opts_.staging_chunk_bytes) {
+    // Pageable host memory: the runtime would bounce every run through its
+    // own small pinned buffers one call at a time; the lane moves whole
+    // staging chunks with one DMA each and spreads the host side over
+    // several threads.
+    std::vector<int64_t> cdev, chost;
+    KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
+    return CopyPageable(dir, storages, cdev, chost, dep);
+  }
   if (min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) {
     return CopyDirect(dir, storages, src, dst, sizes, dep);
   }
-  bool host_ok = true;
-  for (const StorageView& s : storages) host_ok = host_ok && s.host_kernel_access;
   std::vector<int64_t> cdev, chost;
   KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
   bool zero_copy = opts_.mode == TransferMode::kZeroCopy;
@@ -595,6 +766,24 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
     const std::vector<int64_t>& cdev, const std::vector<int64_t>& chost,
     hipStream_t dep) {
   const bool d2h = dir == Direction::kD2H;
+  std::lock_guard<std::mutex> l(mu_);
+  DeviceGuard dg(opts_.device);
+  LaneView lane;
+  lane.ks = d2h ? gather_stream_ : scatter_stream_;
+  lane.cs = d2h ? d2h_stream_ : h2d_stream_;
+  lane.ring = d2h ? &out_ring_ : &in_ring_;
+  hipEvent_t done = nullptr;
+  KVX_RETURN_IF_ERROR(StagedOnLane(lane, dir, storages, cdev, chost, dep, &done));
+  ++stats_.staged_copies;
+  return CopyFuture::FromEvents({done}, {});
+}
+
+Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
+                                    const std::vector<StorageView>& storages,
+                                    const std::vector<int64_t>& cdev,
+                                    const std::vector<int64_t>& chost, hipStream_t dep,
+                                    hipEvent_t* done) {
+  const bool d2h = dir == Direction::kD2H;
   const int64_t n = static_cast<int64_t>(cdev.size());
   std::vector<HostRun> runs;
   for (int64_t i = 0; i < n;) {
@@ -614,38 +803,53 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
       return InvalidArgumentError("copy too large for one plan");
     }
   }
+  hipStream_t ks = lane.ks;
+  hipStream_t cs = lane.cs;
+  Ring& ring = *lane.ring;
+  Bounce* bounce = lane.bounce;
 
-  std::lock_guard<std::mutex> l(mu_);
-  DeviceGuard dg(opts_.device);
-  hipStream_t ks = d2h ? gather_stream_ : scatter_stream_;
-  hipStream_t cs = d2h ? d2h_stream_ : h2d_stream_;
-  Ring& ring = d2h ? out_ring_ : in_ring_;
+  // Counters, folded into stats_ at the end (under mu_ for a pageable lane).
+  int64_t memcpys = 0, nchunks = 0, launches = 0;
 
-  // 4. Arguments: compact device ids, then one base-address table per group.
+  // Arguments: compact device ids, then one base-address table per group.
   int64_t arg_bytes = AlignUp(n * 8, kArgAlign);
   std::vector<int64_t> table_off(groups.size());
   for (size_t gi = 0; gi < groups.size(); ++gi) {
     table_off[gi] = arg_bytes;
     arg_bytes += AlignUp(static_cast<int64_t>(groups[gi].members.size()) * 8, kArgAlign);
   }
-  KVX_ASSIGN_OR_RETURN(int64_t aoff, ArgAlloc(arg_bytes));
-  std::memcpy(arg_host_ + aoff, cdev.data(), n * 8);
+  int64_t aoff = 0;
+  uint8_t* arg_host = nullptr;
+  uint64_t arg_dev = 0;
+  if (lane.args != nullptr) {
+    KVX_ASSIGN_OR_RETURN(aoff, lane.args->Alloc(arg_bytes));
+    arg_host = lane.args->host(aoff);
+    arg_dev = lane.args->dev(aoff);
+  } else {
+    KVX_ASSIGN_OR_RETURN(aoff, ArgAlloc(arg_bytes));
+    arg_host = arg_host_ + aoff;
+    arg_dev = arg_dev_ + aoff;
+  }
+  std::memcpy(arg_host, cdev.data(), n * 8);
   uint64_t align_acc = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
-    uint64_t* t = reinterpret_cast<uint64_t*>(arg_host_ + aoff + table_off[gi]);
+    uint64_t* t = reinterpret_cast<uint64_t*>(arg_host + table_off[gi]);
     for (size_t m = 0; m < groups[gi].members.size(); ++m) {
       t[m] = storages[groups[gi].members[m]].dev;
       align_acc |= t[m];
     }
-    groups[gi].table_dev = arg_dev_ + aoff + table_off[gi];
+    groups[gi].table_dev = arg_dev + table_off[gi];
   }
-  KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(arg_dev_ + aoff),
-                                         arg_host_ + aoff, arg_bytes,
-                                         hipMemcpyHostToDevice, ks));
+  if (lane.args != nullptr) {
+    KVX_RETURN_IF_ERROR(lane.args->Upload(aoff, arg_bytes, ks));
+  } else {
+    KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(arg_dev), arg_host,
+                                           arg_bytes, hipMemcpyHostToDevice, ks));
+  }
   KVX_RETURN_IF_ERROR(WaitDep(dep, ks));
-  const int64_t* ids_dev = reinterpret_cast<const int64_t*>(arg_dev_ + aoff);
+  const int64_t* ids_dev = reinterpret_cast<const int64_t*>(arg_dev);
 
-  // 5. Chunk plan over the layer-major staging layout of all groups.
+  // Chunk plan over the layer-major staging layout of all groups.
   const int64_t cap = opts_.staging_chunk_bytes;
   std::vector<std::vector<PiecePlan>> chunks;
   {
@@ -672,7 +876,9 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
     if (!cur.empty()) chunks.push_back(std::move(cur));
   }
 
-  auto issue_memcpys = [&](const PiecePlan& p, uint64_t buf) -> Status {
+  // Calls fn(host pointer, offset in the chunk buffer, bytes) for every
+  // host-run segment of piece p.
+  auto for_each_segment = [&](const PiecePlan& p, auto fn) -> Status {
     const Group& gr = groups[p.group];
     const int64_t B = gr.block_bytes;
     const int64_t wlo = p.f0 / n;
@@ -690,18 +896,57 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
         const int64_t b = std::min(it->i0 + it->len, ihi);
         if (a >= b) continue;
         uint8_t* host = s.host + (it->host0 + (a - it->i0)) * B;
-        void* stg = reinterpret_cast<void*>(buf + p.buf_off + (w * n + a - p.f0) * B);
-        const size_t bytes = static_cast<size_t>((b - a) * B);
-        if (d2h) {
-          KVX_HIP_RETURN_IF_ERROR(
-              hipMemcpyAsync(host, stg, bytes, hipMemcpyDeviceToHost, cs));
-        } else {
-          KVX_HIP_RETURN_IF_ERROR(
-              hipMemcpyAsync(stg, host, bytes, hipMemcpyHostToDevice, cs));
-        }
-        ++stats_.memcpy_calls;
+        const int64_t off = p.buf_off + (w * n + a - p.f0) * B;
+        KVX_RETURN_IF_ERROR(fn(host, off, static_cast<size_t>((b - a) * B)));
       }
     }
+    return OkStatus();
+  };
+
+  auto issue_memcpys = [&](const PiecePlan& p, uint64_t buf) -> Status {
+    return for_each_segment(p, [&](uint8_t* host, int64_t off, size_t bytes) -> Status {
+      void* stg = reinterpret_cast<void*>(buf + static_cast<uint64_t>(off));
+      if (d2h) {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host, stg, bytes, hipMemcpyDeviceToHost, cs));
+      } else {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(stg, host, bytes, hipMemcpyHostToDevice, cs));
+      }
+      ++memcpys;
+      return OkStatus();
+    });
+  };
+
+  // Host copies between pageable host memory and bounce buffer `bb`.
+  auto bounce_segments = [&](const std::vector<PiecePlan>& ch, uint8_t* bb,
+                             std::vector<Bounce::Segment>* out) -> Status {
+    for (const PiecePlan& p : ch) {
+      KVX_RETURN_IF_ERROR(
+          for_each_segment(p, [&](uint8_t* host, int64_t off, size_t bytes) -> Status {
+            if (d2h) {
+              out->push_back(Bounce::Segment{host, bb + off, bytes});
+            } else {
+              out->push_back(Bounce::Segment{bb + off, host, bytes});
+            }
+            return OkStatus();
+          }));
+    }
+    return OkStatus();
+  };
+  auto chunk_bytes = [&](const std::vector<PiecePlan>& ch) {
+    int64_t end = 0;
+    for (const PiecePlan& p : ch) {
+      end = std::max(end, p.buf_off + p.nb * groups[p.group].block_bytes);
+    }
+    return end;
+  };
+  // D2H: finish the host copies owed from the oldest bounce slot.
+  auto drain_oldest = [&]() -> Status {
+    const size_t k = bounce->order.front();
+    bounce->order.pop_front();
+    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(bounce->dma_done[k]));
+    bounce->Copy(bounce->owed[k]);
+    bounce->owed[k].clear();
+    bounce->used[k] = false;
     return OkStatus();
   };
 
@@ -727,12 +972,19 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
         acc |= static_cast<uint64_t>(p.buf_off);
       }
       const int vec = LaunchVectorBytes(cl, acc);
-      KVX_RETURN_IF_ERROR(LaunchCopy(cl, d2h, vec, ks));
+      if (lane.args != nullptr) {
+        // A pageable lane runs outside mu_: launch without profiling samples.
+        KVX_HIP_RETURN_IF_ERROR(LaunchBlockCopy(
+            cl, d2h ? CopyDir::kGather : CopyDir::kScatter, vec, ks));
+        ++launches;
+      } else {
+        KVX_RETURN_IF_ERROR(LaunchCopy(cl, d2h, vec, ks));
+      }
     }
     return OkStatus();
   };
 
-  // 6. Pipeline the chunks through the staging ring.
+  // Pipeline the chunks through the staging ring.
   for (const std::vector<PiecePlan>& ch : chunks) {
     const size_t k = ring.next;
     ring.next = (ring.next + 1) % ring.bufs.size();
@@ -742,24 +994,172 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
       KVX_RETURN_IF_ERROR(launch(ch, buf));
       KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], ks));
       KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.ready[k], 0));
-      for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
+      if (bounce != nullptr) {
+        // One DMA of the whole chunk into pinned memory; host threads move
+        // the runs into place once it lands (a few chunks later).
+        while (bounce->used[k]) KVX_RETURN_IF_ERROR(drain_oldest());
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(bounce->bufs[k], reinterpret_cast<void*>(buf),
+                                               static_cast<size_t>(chunk_bytes(ch)),
+                                               hipMemcpyDeviceToHost, cs));
+        KVX_HIP_RETURN_IF_ERROR(hipEventRecord(bounce->dma_done[k], cs));
+        ++memcpys;
+        KVX_RETURN_IF_ERROR(bounce_segments(ch, bounce->bufs[k], &bounce->owed[k]));
+        bounce->used[k] = true;
+        bounce->order.push_back(k);
+      } else {
+        for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
+      }
       KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], cs));
     } else {
+      if (bounce != nullptr) {
+        // Host threads fill the pinned slot (once its last DMA is done),
+        // then one DMA moves the whole chunk.
+        if (bounce->used[k]) KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(bounce->dma_done[k]));
+        std::vector<Bounce::Segment> segs;
+        KVX_RETURN_IF_ERROR(bounce_segments(ch, bounce->bufs[k], &segs));
+        bounce->Copy(segs);
+      }
       if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.free[k], 0));
-      for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
+      if (bounce != nullptr) {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(buf), bounce->bufs[k],
+                                               static_cast<size_t>(chunk_bytes(ch)),
+                                               hipMemcpyHostToDevice, cs));
+        KVX_HIP_RETURN_IF_ERROR(hipEventRecord(bounce->dma_done[k], cs));
+        ++memcpys;
+        bounce->used[k] = true;
+      } else {
+        for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
+      }
       KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], cs));
       KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.ready[k], 0));
       KVX_RETURN_IF_ERROR(launch(ch, buf));
       KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], ks));
     }
     ring.used[k] = true;
-    ++stats_.chunks;
+    ++nchunks;
   }
-  KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, ks));
-  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
-  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, d2h ? cs : ks));
-  ++stats_.staged_copies;
-  return CopyFuture::FromEvents({done}, {});
+  if (lane.args != nullptr) {
+    KVX_RETURN_IF_ERROR(lane.args->Commit(aoff, arg_bytes, ks));
+    std::lock_guard<std::mutex> l(mu_);
+    stats_.memcpy_calls += memcpys;
+    stats_.chunks += nchunks;
+    stats_.kernel_launches += launches;
+  } else {
+    KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, ks));
+    stats_.memcpy_calls += memcpys;
+    stats_.chunks += nchunks;
+  }
+  if (d2h && bounce != nullptr) {
+    while (!bounce->order.empty()) KVX_RETURN_IF_ERROR(drain_oldest());
+    *done = nullptr;  // every byte is in host memory
+    return OkStatus();
+  }
+  KVX_ASSIGN_OR_RETURN(*done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(*done, d2h ? cs : ks));
+  return OkStatus();
+}
+
+StatusOr<TransferEngine::PageableLane*> TransferEngine::Lane(Direction dir) {
+  std::lock_guard<std::mutex> l(lanes_mu_);
+  std::unique_ptr<PageableLane>& slot = lanes_[static_cast<int>(dir)];
+  if (slot) return slot.get();
+  DeviceGuard g(opts_.device);
+  auto lane = std::make_unique<PageableLane>();
+  KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&lane->ks, hipStreamNonBlocking));
+  KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&lane->cs, hipStreamNonBlocking));
+  KVX_RETURN_IF_ERROR(lane->args.Init(1 << 20));
+  // The thread that issues the lane's copies takes part in every host copy.
+  lane->bounce = std::make_unique<Bounce>(opts_.host_copy_threads - 1);
+  for (int k = 0; k < opts_.staging_chunks; ++k) {
+    void* d = nullptr;
+    KVX_HIP_RETURN_IF_ERROR(hipMalloc(&d, opts_.staging_chunk_bytes));
+    lane->ring.bufs.push_back(reinterpret_cast<uint64_t>(d));
+    KVX_ASSIGN_OR_RETURN(hipEvent_t ready, NewEvent());
+    KVX_ASSIGN_OR_RETURN(hipEvent_t free_ev, NewEvent());
+    lane->ring.ready.push_back(ready);
+    lane->ring.free.push_back(free_ev);
+    lane->ring.used.push_back(false);
+    void* h = nullptr;
+    KVX_HIP_RETURN_IF_ERROR(hipHostMalloc(&h, opts_.staging_chunk_bytes, hipHostMallocDefault));
+    lane->bounce->bufs.push_back(static_cast<uint8_t*>(h));
+    KVX_ASSIGN_OR_RETURN(hipEvent_t dma, NewEvent());
+    lane->bounce->dma_done.push_back(dma);
+    lane->bounce->used.push_back(false);
+    lane->bounce->owed.emplace_back();
+  }
+  PageableLane* raw = lane.get();
+  lane->worker = std::thread([this, raw] { LaneLoop(raw); });
+  slot = std::move(lane);
+  return raw;
+}
+
+void TransferEngine::LaneLoop(PageableLane* lane) {
+  while (true) {
+    PageableLane::Job job;
+    {
+      std::unique_lock<std::mutex> l(lane->mu);
+      lane->cv.wait(l, [lane] { return lane->stop || !lane->jobs.empty(); });
+      if (lane->jobs.empty()) return;  // stopping, queue drained
+      job = std::move(lane->jobs.front());
+      lane->jobs.pop_front();
+      lane->running = true;
+    }
+    Status st = OkStatus();
+    hipEvent_t done = nullptr;
+    {
+      DeviceGuard g(opts_.device);
+      if (job.dep_event != nullptr) {
+        st = HipStatus(hipStreamWaitEvent(lane->ks, job.dep_event, 0), "dep wait");
+        if (st.ok()) st = HipStatus(hipStreamWaitEvent(lane->cs, job.dep_event, 0), "dep wait");
+        (void)hipEventDestroy(job.dep_event);
+      }
+      if (st.ok()) {
+        LaneView v;
+        v.ks = lane->ks;
+        v.cs = lane->cs;
+        v.ring = &lane->ring;
+        v.args = &lane->args;
+        v.bounce = lane->bounce.get();
+        st = StagedOnLane(v, job.dir, job.storages, job.cdev, job.chost, nullptr, &done);
+      }
+    }
+    if (st.ok()) {
+      {
+        std::lock_guard<std::mutex> l(mu_);
+        ++stats_.staged_copies;
+        ++stats_.bounce_copies;
+      }
+      job.future.Fulfill(done != nullptr ? CopyFuture::FromEvents({done}, {}) : CopyFuture());
+    } else {
+      job.future.Reject(st);
+    }
+    {
+      std::lock_guard<std::mutex> l(lane->mu);
+      lane->running = false;
+    }
+    lane->idle_cv.notify_all();
+  }
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyPageable(Direction dir,
+                                                  const std::vector<StorageView>& storages,
+                                                  const std::vector<int64_t>& cdev,
+                                                  const std::vector<int64_t>& chost,
+                                                  hipStream_t dep) {
+  KVX_ASSIGN_OR_RETURN(PageableLane * lane, Lane(dir));
+  PageableLane::Job job{dir, storages, cdev, chost, nullptr, CopyFuture::Pending()};
+  if (dep != nullptr) {
+    DeviceGuard g(opts_.device);
+    KVX_ASSIGN_OR_RETURN(job.dep_event, NewEvent());
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(job.dep_event, dep));
+  }
+  CopyFuture f = job.future;
+  {
+    std::lock_guard<std::mutex> l(lane->mu);
+    lane->jobs.push_back(std::move(job));
+  }
+  lane->cv.notify_one();
+  return f;
 }
 
 StatusOr<CopyFuture> TransferEngine::DeviceCopy(

@@ -87,6 +87,11 @@ struct EngineOptions {
   int64_t zero_copy_h2d_workgroups = 64;
   // kAuto stages a copy whose host runs average at least this many blocks.
   int64_t auto_staged_min_run = 32;
+  // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
+  // bounce buffers that this many host threads fill and drain, one lane per
+  // direction with its own streams and staging ring (0: leave such copies to
+  // the runtime's pageable hipMemcpyAsync).
+  int host_copy_threads = 8;
 };
 
 // Where DeviceCopy puts block k of storage s in its staging buffer:
@@ -118,6 +123,7 @@ struct EngineStats {
   int64_t chunks = 0;
   int64_t zero_copy_copies = 0;
   int64_t extent_kernel_copies = 0;
+  int64_t bounce_copies = 0;  // copies through the pageable-host lanes
 };
 
 class TransferEngine {
@@ -195,8 +201,20 @@ class TransferEngine {
     int64_t end = 0;
     hipEvent_t done = nullptr;
   };
+  struct Bounce;        // pinned bounce buffers + host copier of one lane
+  struct PageableLane;  // per direction: worker thread, streams, rings
+  // Where a staged copy runs: the engine's own streams and ring (args ==
+  // nullptr: the engine's argument ring, mu_ held; bounce == nullptr: the
+  // host regions are pinned) or a pageable lane's.
+  struct LaneView {
+    hipStream_t ks = nullptr;
+    hipStream_t cs = nullptr;
+    Ring* ring = nullptr;
+    ArgRing* args = nullptr;
+    Bounce* bounce = nullptr;
+  };
 
-  explicit TransferEngine(const EngineOptions& opts) : opts_(opts) {}
+  explicit TransferEngine(const EngineOptions& opts);
   Status Init();
   // Reserves `bytes` of the pinned/device argument ring; waits on the host
   // only if the region is still read by an earlier, unfinished copy.
@@ -217,6 +235,17 @@ class TransferEngine {
                                   const std::vector<int64_t>& cdev,
                                   const std::vector<int64_t>& chost,
                                   hipStream_t dep);
+  // The staged pipeline on `lane`; *done receives the completion event, or
+  // nullptr when the copy is complete on return (D2H through bounce buffers).
+  Status StagedOnLane(const LaneView& lane, Direction dir,
+                      const std::vector<StorageView>& storages,
+                      const std::vector<int64_t>& cdev, const std::vector<int64_t>& chost,
+                      hipStream_t dep, hipEvent_t* done);
+  StatusOr<CopyFuture> CopyPageable(Direction dir, const std::vector<StorageView>& storages,
+                                    const std::vector<int64_t>& cdev,
+                                    const std::vector<int64_t>& chost, hipStream_t dep);
+  StatusOr<PageableLane*> Lane(Direction dir);
+  void LaneLoop(PageableLane* lane);
   StatusOr<CopyFuture> CopyZeroCopy(Direction dir,
                                     const std::vector<StorageView>& storages,
                                     const std::vector<int64_t>& cdev,
@@ -257,6 +286,8 @@ class TransferEngine {
   int64_t arg_head_ = 0;
   std::deque<ArgSlice> arg_inflight_;
   std::unique_ptr<ArgRing> extent_args_;  // strided tables of CopyExtents
+  std::mutex lanes_mu_;
+  std::unique_ptr<PageableLane> lanes_[2];  // by Direction
   EngineStats stats_;
 };
 

@@ -179,6 +179,9 @@ class KVCacheManager:
         copies in submission order, errors arrive through the future) or
         "inline".
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
+      host_copy_threads: a pageable host mirror ("malloc", "shm") moves
+        through pinned bounce buffers that this many host threads fill and
+        drain (0: 8; -1: per-run pageable copies by the HIP runtime).
       The remaining reference arguments (ports, worker id, timeout,
       parallelism, unsafe_skip_buffer_lock) configure its networking, which
       this single-GPU build does not have; they are accepted and ignored.
@@ -198,7 +201,7 @@ class KVCacheManager:
                  model_uid: Optional[str] = None, profile_kernels: bool = False,
                  transfer_mode: str = "auto", zero_copy_workgroups: int = 0,
                  scale_tables: Optional[List[Any]] = None, numa: Any = "auto",
-                 dispatch: str = "env"):
+                 dispatch: str = "env", host_copy_threads: int = 0):
         if host_blocks_to_allocate is None:
             if max_blocks is None or num_slots is None:
                 raise ValueError("Must specify either (max_blocks, num_slots) or"
@@ -230,7 +233,7 @@ class KVCacheManager:
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
                    model_uid, profile_kernels, transfer_mode, zero_copy_workgroups, numa,
-                   dispatch)
+                   dispatch, host_copy_threads)
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
             # kv_cache_manager_with_transfer.cc:483-503: slot geometry, then
@@ -266,7 +269,7 @@ class KVCacheManager:
               slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
               direct_min_bytes, shm_key, shm_server_name, model_uid,
               profile_kernels=False, transfer_mode="auto", zero_copy_workgroups=0,
-              numa="auto", dispatch="env"):
+              numa="auto", dispatch="env", host_copy_threads=0):
         lib = _capi.load()
         kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
                  "shm": _capi.HOST_SHM}
@@ -293,6 +296,7 @@ class KVCacheManager:
         cfg.transfer_mode = _capi.MODES[transfer_mode]
         cfg.zero_copy_workgroups = zero_copy_workgroups
         cfg.dispatch = {"env": 0, "queued": 1, "inline": 2}[dispatch]
+        cfg.host_copy_threads = host_copy_threads
         if numa == "auto":
             cfg.numa_policy = 0
         elif numa in ("off", None):
@@ -781,10 +785,10 @@ class KVCacheManager:
         _capi.check(_capi.load().kvx_manager_wait_for_pending_work(self._h))
 
     def engine_stats(self) -> dict:
-        out = (ctypes.c_int64 * 7)()
+        out = (ctypes.c_int64 * 8)()
         _capi.check(_capi.load().kvx_manager_engine_stats(self._h, out))
         keys = ("direct_copies", "staged_copies", "memcpy_calls", "kernel_launches",
-                "chunks", "zero_copy_copies", "extent_kernel_copies")
+                "chunks", "zero_copy_copies", "extent_kernel_copies", "bounce_copies")
         return dict(zip(keys, list(out)))
 
     def kernel_times(self, gather: bool = True, reset: bool = False) -> dict:
