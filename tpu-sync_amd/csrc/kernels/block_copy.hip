@@ -193,6 +193,55 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
   }
 }
 
+// The common launch (one piece of large blocks, no second paged side, one
+// block per workgroup) without the piece selection: the workgroup reads the
+// block id and the storage base with two independent scalar loads and starts
+// its vector loads after one wait. With kInterleave (a scatter over whole
+// storages) consecutive workgroups take the same block index of consecutive
+// storages, so the writes in flight at any moment spread over every storage
+// instead of crowding one: 3 points of HBM bandwidth on random destinations.
+struct FastParams {
+  uint64_t storages;
+  uint64_t staging;
+  const int64_t* ids;
+  int32_t* error;
+  int64_t stride_w;
+  int64_t stride_i;
+  int64_t pool_blocks;
+  uint32_t f0;
+  uint32_t n;
+  uint32_t elems;
+  uint32_t wstorages;  // kInterleave: storages in the launch (f0 = w0 * n)
+};
+
+template <typename V, bool kGather, int kUnroll, bool kInterleave>
+__global__ __launch_bounds__(kThreads) void block_copy_fast_kernel(FastParams P) {
+  const uint32_t g = blockIdx.x;
+  uint32_t w, i;
+  if (kInterleave) {
+    i = g / P.wstorages;
+    w = P.f0 / P.n + (g - i * P.wstorages);
+  } else {
+    const uint32_t f = P.f0 + g;
+    w = f / P.n;
+    i = f - w * P.n;
+  }
+  const int64_t id = uniform_load<int64_t>(reinterpret_cast<uint64_t>(P.ids), i);
+  const uint64_t base = uniform_load<uint64_t>(P.storages, w);
+  if (bad_id(id, P.pool_blocks)) {
+    if (threadIdx.x == 0 && P.error != nullptr) atomicOr(P.error, 1);
+    return;
+  }
+  KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(id) * P.elems;
+  KVX_GLOBAL V* stg = gptr<V>(P.staging + w * static_cast<uint64_t>(P.stride_w) +
+                              i * static_cast<uint64_t>(P.stride_i));
+  if (kGather) {
+    copy_whole_block<V, kUnroll>(pool, stg, P.elems);
+  } else {
+    copy_whole_block<V, kUnroll>(stg, pool, P.elems);
+  }
+}
+
 // Blocks per workgroup: one for blocks of >= 2 vectors per lane, otherwise
 // enough blocks to give each lane about 8 vectors.
 uint32_t BlocksPerWorkgroup(uint64_t elems) {
@@ -263,9 +312,45 @@ bool BuildParams(const CopyLaunch& l, int vec_bytes, KParams* P,
   return true;
 }
 
+// The fast kernel's parameters when the launch qualifies (one whole-block
+// piece, bpw 1, no second paged side).
+bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, bool* interleave) {
+  const KPiece& p = K.p[0];
+  if (K.npieces != 1 || !p.whole || p.bpw != 1 || p.others != 0) return false;
+  *F = FastParams{};
+  F->storages = p.storages;
+  F->staging = p.staging;
+  F->ids = K.ids;
+  F->error = K.error;
+  F->stride_w = p.stride_w;
+  F->stride_i = p.stride_i;
+  F->pool_blocks = p.pool_blocks;
+  F->f0 = p.f0;
+  F->n = K.n;
+  F->elems = p.elems;
+  *interleave = dir == CopyDir::kScatter && p.f0 % K.n == 0 && p.nblocks % K.n == 0 &&
+                p.nblocks / K.n >= 2;
+  F->wstorages = *interleave ? p.nblocks / K.n : 0;
+  return true;
+}
+
 template <typename V, int kUnroll>
-hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir,
-                  hipStream_t stream) {
+hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, hipStream_t stream) {
+  FastParams F;
+  bool interleave = false;
+  if (BuildFastParams(P, dir, &F, &interleave)) {
+    if (dir == CopyDir::kGather) {
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, true, kUnroll, false>), dim3(grid),
+                         dim3(kThreads), 0, stream, F);
+    } else if (interleave) {
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, true>), dim3(grid),
+                         dim3(kThreads), 0, stream, F);
+    } else {
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, false>), dim3(grid),
+                         dim3(kThreads), 0, stream, F);
+    }
+    return hipGetLastError();
+  }
   if (dir == CopyDir::kGather) {
     hipLaunchKernelGGL((block_copy_kernel<V, true, kUnroll>), dim3(grid),
                        dim3(kThreads), 0, stream, P);
