@@ -4,6 +4,7 @@ the same seeded inputs, bit-exact. Covers the direct and the staged
 kernel, layer/shard/slot restrictions, the reference's e2e known answers,
 device gather/scatter, bad ids, and a full-size Llama-3-8B pool round trip.
 """
+import os
 import threading
 
 import numpy as np
@@ -519,17 +520,22 @@ def test_llama3_8b_pool_full_size_round_trip(kvx, cuda, mode):
     mgr.close()
 
 
-@pytest.mark.parametrize("threads", [1, 0])
-def test_bounce_lanes_overlap_and_drain(kvx, oracle, cuda, threads):
-    """Pageable mirror: 8 offloads and 8 reloads of disjoint host ranges are
-    issued without waiting (the two lanes run them concurrently, each in
-    submission order); wait_for_pending_work drains both lanes, then device
-    and host equal the oracle's. threads=1: the issuing thread alone copies."""
+@pytest.mark.parametrize("threads,alloc", [(1, "malloc"), (0, "shm")])
+def test_bounce_lanes_overlap_and_drain(kvx, oracle, cuda, threads, alloc):
+    """Pageable mirror (malloc, or a /dev/shm segment): 8 offloads and 8
+    reloads of disjoint host ranges are issued without waiting (the two lanes
+    run them concurrently, each in submission order); wait_for_pending_work
+    drains both lanes, then device and host equal the oracle's. threads=1:
+    the issuing thread alone copies."""
     rng = np.random.default_rng(41 + threads)
     layers, blocks, bb, hb = 4, 64, 16384, 64
     host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
-    mgr = make_mgr(kvx, dev, hb, host_alloc="malloc", staging_chunk_bytes=1 << 18,
-                   staging_chunks=3, direct_min_bytes=1 << 40, host_copy_threads=threads)
+    tier = {}
+    if alloc == "shm":
+        tier = {"shm_key": f"kvx_test_bounce_{os.getpid()}"}
+    mgr = make_mgr(kvx, dev, hb, host_alloc=alloc, staging_chunk_bytes=1 << 18,
+                   staging_chunks=3, direct_min_bytes=1 << 40, host_copy_threads=threads,
+                   **tier)
     mir = Mirror(host, hb)
     # Host blocks 32..63 hold data to reload; 0..31 receive offloads.
     for l in range(layers):
@@ -553,6 +559,10 @@ def test_bounce_lanes_overlap_and_drain(kvx, oracle, cuda, threads):
     mir.check(mgr, dev)
     assert mgr.engine_stats()["bounce_copies"] == 16
     mgr.close()
+    if tier:
+        for name in os.listdir("/dev/shm"):
+            if name.startswith(tier["shm_key"]):
+                os.unlink(os.path.join("/dev/shm", name))
 
 
 def test_zero_copy_needs_pinned_host(kvx, cuda):
