@@ -68,6 +68,9 @@ def parse_args():
     p.add_argument("--zipf-host-blocks", type=int, default=2048,
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks")
     p.add_argument("--zipf-batches", type=int, default=24)
+    p.add_argument("--pools-host-alloc", default="pinned", choices=["pinned", "malloc"],
+                   help="host mirror of the sparse-pool config (malloc: pageable, through "
+                        "the bounce lanes)")
     p.add_argument("--zipf-host-alloc", default="pinned", choices=["pinned", "shm"],
                    help="host tier memory: pinned (hipHostMalloc) or a /dev/shm segment")
     p.add_argument("--zipf-docs", type=int, default=8,
@@ -385,7 +388,9 @@ def bench_pools(torch, pkg, dev, args, rng):
     320 KiB block stride (40 % live). 32 storages x 512 blocks; each step
     copies 128 random blocks of every pool device->host, then host->device,
     moving only the live bytes (one strided-copy launch per pool over the
-    pinned mirror), against whole-block copies of the same ids."""
+    pinned mirror; with a malloc mirror the live bytes are packed into staging
+    chunks and cross PCIe through the bounce lanes), against whole-block
+    copies of the same ids."""
     L, NB, stride = 32, 512, 327680
     regions = tuple(pkg.RegionSpec("fa%d" % g, g * 71680, 512, 256, 64, 2) for g in range(4))
     live = sum(r.live_bytes for r in regions)
@@ -393,7 +398,8 @@ def bench_pools(torch, pkg, dev, args, rng):
     pools = [torch.empty(NB, stride, dtype=torch.uint8, device=dev) for _ in range(L)]
     for p in pools:
         p.random_(0, 256)
-    mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=NB)
+    mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=NB,
+                             host_alloc=args.pools_host_alloc)
     specs = [pkg.PoolSpec("fa", l, 0, stride, NB, regions) for l in range(L)]
     mgr.register_pools(specs)
     n = 128
@@ -423,6 +429,7 @@ def bench_pools(torch, pkg, dev, args, rng):
     out = {"workload": "FA-like sparse pool (4 head groups x 32 KiB live per 320 KiB block), "
                        f"{L} storages x {NB} blocks, {n} random blocks per copy",
            "live_fraction": round(live / stride, 3),
+           "host_mirror": args.pools_host_alloc,
            "pool_d2h_live_gbps": round(live_bytes / t_d2h / 1e9, 2),
            "pool_h2d_live_gbps": round(live_bytes / t_h2d / 1e9, 2),
            "pool_d2h_ms": round(t_d2h * 1e3, 3),

@@ -3,9 +3,10 @@ kv_cache_manager_base.cc:1801-1872) move exactly the live bytes named by the
 oracle's copy extents (oracle/pool_layout.py) between HBM and the host
 mirror, at the same byte offsets on both sides, and nothing else: padding
 bytes keep a sentinel on the receiving side. Covers the strided-copy kernel
-path (pinned mirror, short extents), the DMA path (malloc mirror, or extents
-of at least direct_min_bytes), shard selection, the implicit opaque pools and
-host-mirror growth on registration."""
+path (pinned mirror, short extents), the bounce lane (malloc mirror: live
+bytes packed into staging chunks), the DMA path (extents of at least
+direct_min_bytes, or a malloc mirror left to the runtime), shard selection,
+the implicit opaque pools and host-mirror growth on registration."""
 import numpy as np
 import pytest
 
@@ -54,15 +55,23 @@ SPARSE = {"tag": "sparse", "base": 0, "block_stride": 4096, "num_blocks": 96,
           "regions": [("k", 0, 80, 32, 40, 1), ("s", 3216, 16, 8, 4, 1)]}
 
 
-@pytest.mark.parametrize("host_alloc", ["pinned", "malloc"])
+@pytest.mark.parametrize("host_alloc", ["pinned", "malloc", "malloc_runtime"])
 @pytest.mark.parametrize("pool", [FA, SPARSE], ids=["fa", "sparse"])
 def test_pool_copies_move_exactly_the_live_bytes(kvx, cuda, host_alloc, pool):
+    """pinned: the strided kernel reads/writes the mapped mirror; malloc: the
+    bounce lane (staging chunks of 48 KiB, so extents split across chunks);
+    malloc_runtime: one pageable hipMemcpyAsync per (storage, extent)."""
     rng = np.random.default_rng(11)
     nbytes = O.storage_extent_end(pool) + 1000
     nbytes += (-nbytes) % pool["block_stride"]
     major = nbytes // pool["block_stride"]
     shards = device_storages(cuda, rng, 2, nbytes, major)
-    mgr = kvx.KVCacheManager([shards], host_blocks_to_allocate=major, host_alloc=host_alloc)
+    kw = {"host_alloc": host_alloc}
+    if host_alloc == "malloc":
+        kw.update(staging_chunk_bytes=48 << 10, staging_chunks=2)
+    elif host_alloc == "malloc_runtime":
+        kw.update(host_alloc="malloc", host_copy_threads=-1)
+    mgr = kvx.KVCacheManager([shards], host_blocks_to_allocate=major, **kw)
     mgr.register_pools([spec(kvx, pool)])
     hv = [mgr.host_view(0, s) for s in range(2)]
     for h in hv:
@@ -73,6 +82,9 @@ def test_pool_copies_move_exactly_the_live_bytes(kvx, cuda, host_alloc, pool):
     after = mgr.engine_stats()
     if host_alloc == "pinned":
         assert after["extent_kernel_copies"] == before["extent_kernel_copies"] + 1
+    elif host_alloc == "malloc":
+        # Packed into staging chunks, one DMA per chunk through a bounce lane.
+        assert after["bounce_copies"] == before["bounce_copies"] + 1
     else:
         assert after["memcpy_calls"] - before["memcpy_calls"] == \
             2 * len(O.copy_extents(pool, ids))

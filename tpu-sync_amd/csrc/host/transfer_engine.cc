@@ -93,7 +93,36 @@ struct TransferEngine::Bounce {
   std::vector<hipEvent_t> dma_done;  // last DMA into (D2H) or out of (H2D) bufs[k]
   std::vector<bool> used;
   std::vector<std::vector<Segment>> owed;  // D2H: host copies still due from bufs[k]
+  std::vector<std::vector<CopyFuture>> waiters;  // D2H: copies complete once bufs[k] drains
   std::deque<size_t> order;                // D2H: slots with copies owed, oldest first
+
+  // D2H: waits for the oldest slot's DMA, moves its bytes into place and
+  // completes the copies waiting on it.
+  Status DrainOldest() {
+    const size_t k = order.front();
+    order.pop_front();
+    Status st = HipStatus(hipEventSynchronize(dma_done[k]), "bounce buffer DMA");
+    if (st.ok()) Copy(owed[k]);
+    owed[k].clear();
+    used[k] = false;
+    for (const CopyFuture& f : waiters[k]) {
+      if (st.ok()) {
+        f.Fulfill(CopyFuture());
+      } else {
+        f.Reject(st);
+      }
+    }
+    waiters[k].clear();
+    return st;
+  }
+  Status DrainAll() {
+    Status first = OkStatus();
+    while (!order.empty()) {
+      Status st = DrainOldest();
+      if (first.ok() && !st.ok()) first = st;
+    }
+    return first;
+  }
 
   // A fixed pool of threads running parallel memcpy batches.
   explicit Bounce(int threads) {
@@ -184,6 +213,7 @@ struct TransferEngine::PageableLane {
     Direction dir;
     std::vector<StorageView> storages;
     std::vector<int64_t> cdev, chost;
+    std::vector<ByteExtent> extents;  // non-empty: a pool-extent copy
     hipEvent_t dep_event = nullptr;
     CopyFuture future;
   };
@@ -484,7 +514,7 @@ StatusOr<CopyFuture> TransferEngine::Copy(
     // several threads.
     std::vector<int64_t> cdev, chost;
     KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
-    return CopyPageable(dir, storages, cdev, chost, dep);
+    return CopyPageable(dir, storages, cdev, chost, {}, dep);
   }
   if (min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) {
     return CopyDirect(dir, storages, src, dst, sizes, dep);
@@ -626,9 +656,20 @@ StatusOr<CopyFuture> TransferEngine::CopyExtents(
   const bool d2h = dir == Direction::kD2H;
   bool kernel = opts_.mode != TransferMode::kStaged;
   bool any_short = false;
-  for (const ByteExtent& e : extents) any_short |= e.bytes < opts_.direct_min_bytes;
-  for (const StorageView& s : storages) kernel &= s.host_kernel_access;
-  kernel &= any_short;
+  int64_t total = 0;
+  for (const ByteExtent& e : extents) {
+    any_short |= e.bytes < opts_.direct_min_bytes;
+    total += e.bytes;
+  }
+  bool host_ok = true;
+  for (const StorageView& s : storages) host_ok = host_ok && s.host_kernel_access;
+  if (total == 0 || storages.empty()) return CopyFuture();
+  if (!host_ok && opts_.host_copy_threads > 0) {
+    // Pageable host memory: live bytes packed into staging chunks and
+    // moved through a bounce lane.
+    return CopyPageable(dir, storages, {}, {}, extents, dep);
+  }
+  kernel &= host_ok && any_short;
   std::lock_guard<std::mutex> l(mu_);
   DeviceGuard g(opts_.device);
   if (!kernel) {
@@ -778,6 +819,95 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
   return CopyFuture::FromEvents({done}, {});
 }
 
+Status TransferEngine::PipelineChunks(const LaneView& lane, Direction dir,
+                                      const std::vector<ChunkWork>& chunks, int64_t* memcpys) {
+  const bool d2h = dir == Direction::kD2H;
+  hipStream_t ks = lane.ks;
+  hipStream_t cs = lane.cs;
+  Ring& ring = *lane.ring;
+  Bounce* bounce = lane.bounce;
+
+  // Pinned host: one DMA per segment straight between staging and host.
+  auto issue_memcpys = [&](const ChunkWork& ch, uint64_t buf) -> Status {
+    for (const HostSegment& s : ch.segs) {
+      void* stg = reinterpret_cast<void*>(buf + static_cast<uint64_t>(s.off));
+      const size_t bytes = static_cast<size_t>(s.bytes);
+      if (d2h) {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(s.host, stg, bytes, hipMemcpyDeviceToHost, cs));
+      } else {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(stg, s.host, bytes, hipMemcpyHostToDevice, cs));
+      }
+      ++*memcpys;
+    }
+    return OkStatus();
+  };
+  // Host copies between pageable host memory and bounce buffer `bb`.
+  auto bounce_segments = [&](const ChunkWork& ch, uint8_t* bb,
+                             std::vector<Bounce::Segment>* out) {
+    for (const HostSegment& s : ch.segs) {
+      const size_t bytes = static_cast<size_t>(s.bytes);
+      if (d2h) {
+        out->push_back(Bounce::Segment{s.host, bb + s.off, bytes});
+      } else {
+        out->push_back(Bounce::Segment{bb + s.off, s.host, bytes});
+      }
+    }
+  };
+  for (const ChunkWork& ch : chunks) {
+    const size_t k = ring.next;
+    ring.next = (ring.next + 1) % ring.bufs.size();
+    const uint64_t buf = ring.bufs[k];
+    if (d2h) {
+      if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.free[k], 0));
+      KVX_RETURN_IF_ERROR(ch.kernel(buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], ks));
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.ready[k], 0));
+      if (bounce != nullptr) {
+        // One DMA of the whole chunk into pinned memory; host threads move
+        // the segments into place once it lands (a few chunks later).
+        while (bounce->used[k]) KVX_RETURN_IF_ERROR(bounce->DrainOldest());
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(bounce->bufs[k], reinterpret_cast<void*>(buf),
+                                               static_cast<size_t>(ch.bytes),
+                                               hipMemcpyDeviceToHost, cs));
+        KVX_HIP_RETURN_IF_ERROR(hipEventRecord(bounce->dma_done[k], cs));
+        ++*memcpys;
+        bounce_segments(ch, bounce->bufs[k], &bounce->owed[k]);
+        bounce->used[k] = true;
+        bounce->order.push_back(k);
+      } else {
+        KVX_RETURN_IF_ERROR(issue_memcpys(ch, buf));
+      }
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], cs));
+    } else {
+      if (bounce != nullptr) {
+        // Host threads fill the pinned slot (once its last DMA is done),
+        // then one DMA moves the whole chunk.
+        if (bounce->used[k]) KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(bounce->dma_done[k]));
+        std::vector<Bounce::Segment> segs;
+        bounce_segments(ch, bounce->bufs[k], &segs);
+        bounce->Copy(segs);
+      }
+      if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.free[k], 0));
+      if (bounce != nullptr) {
+        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(buf), bounce->bufs[k],
+                                               static_cast<size_t>(ch.bytes),
+                                               hipMemcpyHostToDevice, cs));
+        KVX_HIP_RETURN_IF_ERROR(hipEventRecord(bounce->dma_done[k], cs));
+        ++*memcpys;
+        bounce->used[k] = true;
+      } else {
+        KVX_RETURN_IF_ERROR(issue_memcpys(ch, buf));
+      }
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], cs));
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.ready[k], 0));
+      KVX_RETURN_IF_ERROR(ch.kernel(buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], ks));
+    }
+    ring.used[k] = true;
+  }
+  return OkStatus();
+}
+
 Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
                                     const std::vector<StorageView>& storages,
                                     const std::vector<int64_t>& cdev,
@@ -805,11 +935,9 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
   }
   hipStream_t ks = lane.ks;
   hipStream_t cs = lane.cs;
-  Ring& ring = *lane.ring;
-  Bounce* bounce = lane.bounce;
 
   // Counters, folded into stats_ at the end (under mu_ for a pageable lane).
-  int64_t memcpys = 0, nchunks = 0, launches = 0;
+  int64_t memcpys = 0, launches = 0;
 
   // Arguments: compact device ids, then one base-address table per group.
   int64_t arg_bytes = AlignUp(n * 8, kArgAlign);
@@ -851,7 +979,7 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
 
   // Chunk plan over the layer-major staging layout of all groups.
   const int64_t cap = opts_.staging_chunk_bytes;
-  std::vector<std::vector<PiecePlan>> chunks;
+  std::vector<std::vector<PiecePlan>> plans;
   {
     std::vector<PiecePlan> cur;
     int64_t used = 0;
@@ -862,7 +990,7 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
       while (f < F) {
         int64_t fit = (cap - used) / B;
         if (fit == 0) {
-          chunks.push_back(std::move(cur));
+          plans.push_back(std::move(cur));
           cur.clear();
           used = 0;
           continue;
@@ -873,12 +1001,11 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
         f += take;
       }
     }
-    if (!cur.empty()) chunks.push_back(std::move(cur));
+    if (!cur.empty()) plans.push_back(std::move(cur));
   }
 
-  // Calls fn(host pointer, offset in the chunk buffer, bytes) for every
-  // host-run segment of piece p.
-  auto for_each_segment = [&](const PiecePlan& p, auto fn) -> Status {
+  // Host-run segments of piece p: (host pointer, offset in the chunk, bytes).
+  auto add_segments = [&](const PiecePlan& p, std::vector<HostSegment>* out) {
     const Group& gr = groups[p.group];
     const int64_t B = gr.block_bytes;
     const int64_t wlo = p.f0 / n;
@@ -895,59 +1022,10 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
         const int64_t a = std::max(it->i0, ilo);
         const int64_t b = std::min(it->i0 + it->len, ihi);
         if (a >= b) continue;
-        uint8_t* host = s.host + (it->host0 + (a - it->i0)) * B;
-        const int64_t off = p.buf_off + (w * n + a - p.f0) * B;
-        KVX_RETURN_IF_ERROR(fn(host, off, static_cast<size_t>((b - a) * B)));
+        out->push_back(HostSegment{s.host + (it->host0 + (a - it->i0)) * B,
+                                   p.buf_off + (w * n + a - p.f0) * B, (b - a) * B});
       }
     }
-    return OkStatus();
-  };
-
-  auto issue_memcpys = [&](const PiecePlan& p, uint64_t buf) -> Status {
-    return for_each_segment(p, [&](uint8_t* host, int64_t off, size_t bytes) -> Status {
-      void* stg = reinterpret_cast<void*>(buf + static_cast<uint64_t>(off));
-      if (d2h) {
-        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host, stg, bytes, hipMemcpyDeviceToHost, cs));
-      } else {
-        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(stg, host, bytes, hipMemcpyHostToDevice, cs));
-      }
-      ++memcpys;
-      return OkStatus();
-    });
-  };
-
-  // Host copies between pageable host memory and bounce buffer `bb`.
-  auto bounce_segments = [&](const std::vector<PiecePlan>& ch, uint8_t* bb,
-                             std::vector<Bounce::Segment>* out) -> Status {
-    for (const PiecePlan& p : ch) {
-      KVX_RETURN_IF_ERROR(
-          for_each_segment(p, [&](uint8_t* host, int64_t off, size_t bytes) -> Status {
-            if (d2h) {
-              out->push_back(Bounce::Segment{host, bb + off, bytes});
-            } else {
-              out->push_back(Bounce::Segment{bb + off, host, bytes});
-            }
-            return OkStatus();
-          }));
-    }
-    return OkStatus();
-  };
-  auto chunk_bytes = [&](const std::vector<PiecePlan>& ch) {
-    int64_t end = 0;
-    for (const PiecePlan& p : ch) {
-      end = std::max(end, p.buf_off + p.nb * groups[p.group].block_bytes);
-    }
-    return end;
-  };
-  // D2H: finish the host copies owed from the oldest bounce slot.
-  auto drain_oldest = [&]() -> Status {
-    const size_t k = bounce->order.front();
-    bounce->order.pop_front();
-    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(bounce->dma_done[k]));
-    bounce->Copy(bounce->owed[k]);
-    bounce->owed[k].clear();
-    bounce->used[k] = false;
-    return OkStatus();
   };
 
   auto launch = [&](const std::vector<PiecePlan>& ps, uint64_t buf) -> Status {
@@ -984,60 +1062,19 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
     return OkStatus();
   };
 
-  // Pipeline the chunks through the staging ring.
-  for (const std::vector<PiecePlan>& ch : chunks) {
-    const size_t k = ring.next;
-    ring.next = (ring.next + 1) % ring.bufs.size();
-    const uint64_t buf = ring.bufs[k];
-    if (d2h) {
-      if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.free[k], 0));
-      KVX_RETURN_IF_ERROR(launch(ch, buf));
-      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], ks));
-      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.ready[k], 0));
-      if (bounce != nullptr) {
-        // One DMA of the whole chunk into pinned memory; host threads move
-        // the runs into place once it lands (a few chunks later).
-        while (bounce->used[k]) KVX_RETURN_IF_ERROR(drain_oldest());
-        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(bounce->bufs[k], reinterpret_cast<void*>(buf),
-                                               static_cast<size_t>(chunk_bytes(ch)),
-                                               hipMemcpyDeviceToHost, cs));
-        KVX_HIP_RETURN_IF_ERROR(hipEventRecord(bounce->dma_done[k], cs));
-        ++memcpys;
-        KVX_RETURN_IF_ERROR(bounce_segments(ch, bounce->bufs[k], &bounce->owed[k]));
-        bounce->used[k] = true;
-        bounce->order.push_back(k);
-      } else {
-        for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
-      }
-      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], cs));
-    } else {
-      if (bounce != nullptr) {
-        // Host threads fill the pinned slot (once its last DMA is done),
-        // then one DMA moves the whole chunk.
-        if (bounce->used[k]) KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(bounce->dma_done[k]));
-        std::vector<Bounce::Segment> segs;
-        KVX_RETURN_IF_ERROR(bounce_segments(ch, bounce->bufs[k], &segs));
-        bounce->Copy(segs);
-      }
-      if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, ring.free[k], 0));
-      if (bounce != nullptr) {
-        KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(buf), bounce->bufs[k],
-                                               static_cast<size_t>(chunk_bytes(ch)),
-                                               hipMemcpyHostToDevice, cs));
-        KVX_HIP_RETURN_IF_ERROR(hipEventRecord(bounce->dma_done[k], cs));
-        ++memcpys;
-        bounce->used[k] = true;
-      } else {
-        for (const PiecePlan& p : ch) KVX_RETURN_IF_ERROR(issue_memcpys(p, buf));
-      }
-      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], cs));
-      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(ks, ring.ready[k], 0));
-      KVX_RETURN_IF_ERROR(launch(ch, buf));
-      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[k], ks));
+  std::vector<ChunkWork> chunks(plans.size());
+  for (size_t k = 0; k < plans.size(); ++k) {
+    ChunkWork& ch = chunks[k];
+    for (const PiecePlan& p : plans[k]) {
+      ch.bytes = std::max(ch.bytes, p.buf_off + p.nb * groups[p.group].block_bytes);
+      add_segments(p, &ch.segs);
     }
-    ring.used[k] = true;
-    ++nchunks;
+    const std::vector<PiecePlan>* plan = &plans[k];
+    ch.kernel = [&launch, plan](uint64_t buf) { return launch(*plan, buf); };
   }
+  KVX_RETURN_IF_ERROR(PipelineChunks(lane, dir, chunks, &memcpys));
+
+  const int64_t nchunks = static_cast<int64_t>(chunks.size());
   if (lane.args != nullptr) {
     KVX_RETURN_IF_ERROR(lane.args->Commit(aoff, arg_bytes, ks));
     std::lock_guard<std::mutex> l(mu_);
@@ -1049,13 +1086,85 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
     stats_.memcpy_calls += memcpys;
     stats_.chunks += nchunks;
   }
-  if (d2h && bounce != nullptr) {
-    while (!bounce->order.empty()) KVX_RETURN_IF_ERROR(drain_oldest());
-    *done = nullptr;  // every byte is in host memory
+  if (d2h && lane.bounce != nullptr) {
+    *done = nullptr;  // complete once its bounce slots drain
     return OkStatus();
   }
   KVX_ASSIGN_OR_RETURN(*done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(*done, d2h ? cs : ks));
+  return OkStatus();
+}
+
+Status TransferEngine::ExtentsOnLane(const LaneView& lane, Direction dir,
+                                     const std::vector<StorageView>& storages,
+                                     const std::vector<ByteExtent>& extents, hipEvent_t* done) {
+  const bool d2h = dir == Direction::kD2H;
+  const int64_t cap = opts_.staging_chunk_bytes;
+  // Every (storage, extent) piece packed into staging chunks at 16-byte
+  // aligned offsets, split where a chunk fills. The strided kernel packs
+  // (D2H) or unpacks (H2D) a chunk; staging offsets are relative until the
+  // chunk's buffer is known.
+  std::vector<ChunkWork> chunks;
+  std::vector<std::vector<StridedCopy>> tables;
+  ChunkWork cur;
+  std::vector<StridedCopy> tab;
+  int64_t used = 0;
+  auto flush = [&]() {
+    if (!cur.segs.empty()) {
+      cur.bytes = used;
+      chunks.push_back(std::move(cur));
+      tables.push_back(std::move(tab));
+    }
+    cur = ChunkWork();
+    tab.clear();
+    used = 0;
+  };
+  for (const StorageView& s : storages) {
+    for (const ByteExtent& e : extents) {
+      int64_t off = e.offset;
+      int64_t left = e.bytes;
+      while (left > 0) {
+        if (used >= cap) {
+          flush();
+          continue;
+        }
+        const int64_t take = std::min(left, cap - used);
+        cur.segs.push_back(HostSegment{s.host + off, used, take});
+        StridedCopy c;
+        const uint64_t dev = s.dev + static_cast<uint64_t>(off);
+        c.src = d2h ? dev : static_cast<uint64_t>(used);
+        c.dst = d2h ? static_cast<uint64_t>(used) : dev;
+        c.size = take;
+        tab.push_back(c);
+        used = AlignUp(used + take, 16);
+        off += take;
+        left -= take;
+      }
+    }
+  }
+  flush();
+  for (size_t k = 0; k < chunks.size(); ++k) {
+    const std::vector<StridedCopy>* t = &tables[k];
+    chunks[k].kernel = [&lane, d2h, t](uint64_t buf) -> Status {
+      std::vector<StridedCopy> copies = *t;
+      for (StridedCopy& c : copies) (d2h ? c.dst : c.src) += buf;
+      return LaunchStridedThroughRing(*lane.args, copies, lane.ks);
+    };
+  }
+  int64_t memcpys = 0;
+  KVX_RETURN_IF_ERROR(PipelineChunks(lane, dir, chunks, &memcpys));
+  {
+    std::lock_guard<std::mutex> l(mu_);
+    stats_.memcpy_calls += memcpys;
+    stats_.chunks += static_cast<int64_t>(chunks.size());
+    stats_.kernel_launches += static_cast<int64_t>(chunks.size());
+  }
+  if (d2h) {
+    *done = nullptr;  // complete once its bounce slots drain
+    return OkStatus();
+  }
+  KVX_ASSIGN_OR_RETURN(*done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(*done, lane.ks));
   return OkStatus();
 }
 
@@ -1086,6 +1195,7 @@ StatusOr<TransferEngine::PageableLane*> TransferEngine::Lane(Direction dir) {
     lane->bounce->dma_done.push_back(dma);
     lane->bounce->used.push_back(false);
     lane->bounce->owed.emplace_back();
+    lane->bounce->waiters.emplace_back();
   }
   PageableLane* raw = lane.get();
   lane->worker = std::thread([this, raw] { LaneLoop(raw); });
@@ -1094,6 +1204,7 @@ StatusOr<TransferEngine::PageableLane*> TransferEngine::Lane(Direction dir) {
 }
 
 void TransferEngine::LaneLoop(PageableLane* lane) {
+  Bounce* b = lane->bounce.get();
   while (true) {
     PageableLane::Job job;
     {
@@ -1119,19 +1230,38 @@ void TransferEngine::LaneLoop(PageableLane* lane) {
         v.cs = lane->cs;
         v.ring = &lane->ring;
         v.args = &lane->args;
-        v.bounce = lane->bounce.get();
-        st = StagedOnLane(v, job.dir, job.storages, job.cdev, job.chost, nullptr, &done);
+        v.bounce = b;
+        st = job.extents.empty()
+                 ? StagedOnLane(v, job.dir, job.storages, job.cdev, job.chost, nullptr, &done)
+                 : ExtentsOnLane(v, job.dir, job.storages, job.extents, &done);
       }
     }
-    if (st.ok()) {
+    if (!st.ok()) {
+      job.future.Reject(st);
+    } else {
       {
         std::lock_guard<std::mutex> l(mu_);
         ++stats_.staged_copies;
         ++stats_.bounce_copies;
       }
-      job.future.Fulfill(done != nullptr ? CopyFuture::FromEvents({done}, {}) : CopyFuture());
-    } else {
-      job.future.Reject(st);
+      if (done == nullptr && !b->order.empty()) {
+        // D2H: the last bytes still sit in bounce buffers; the copy
+        // completes when its newest slot drains (slots drain in order), so
+        // the next copy's DMA overlaps these host copies.
+        b->waiters[b->order.back()].push_back(job.future);
+      } else {
+        job.future.Fulfill(done != nullptr ? CopyFuture::FromEvents({done}, {}) : CopyFuture());
+      }
+    }
+    bool idle;
+    {
+      std::lock_guard<std::mutex> l(lane->mu);
+      idle = lane->jobs.empty();
+    }
+    if (idle) {
+      // Nothing queued: finish every owed host copy now.
+      DeviceGuard g(opts_.device);
+      (void)b->DrainAll();  // failures reach the waiting copies' futures
     }
     {
       std::lock_guard<std::mutex> l(lane->mu);
@@ -1145,9 +1275,10 @@ StatusOr<CopyFuture> TransferEngine::CopyPageable(Direction dir,
                                                   const std::vector<StorageView>& storages,
                                                   const std::vector<int64_t>& cdev,
                                                   const std::vector<int64_t>& chost,
+                                                  const std::vector<ByteExtent>& extents,
                                                   hipStream_t dep) {
   KVX_ASSIGN_OR_RETURN(PageableLane * lane, Lane(dir));
-  PageableLane::Job job{dir, storages, cdev, chost, nullptr, CopyFuture::Pending()};
+  PageableLane::Job job{dir, storages, cdev, chost, extents, nullptr, CopyFuture::Pending()};
   if (dep != nullptr) {
     DeviceGuard g(opts_.device);
     KVX_ASSIGN_OR_RETURN(job.dep_event, NewEvent());

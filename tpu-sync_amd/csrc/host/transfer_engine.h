@@ -22,6 +22,7 @@
 
 #include <cstdint>
 #include <deque>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <vector>
@@ -153,11 +154,13 @@ class TransferEngine {
                                 hipStream_t dep);
 
   // Copies `extents` of every storage between its device buffer and its
-  // host region, the same offsets on both sides. Extents shorter than
-  // direct_min_bytes go through one strided-copy kernel that reads and
-  // writes the page-locked host region directly (no staging); otherwise, or
-  // when the host region is not mapped for the GPU, one hipMemcpyAsync per
-  // (storage, extent). The caller has validated every range.
+  // host region, the same offsets on both sides. With a page-locked host
+  // region, extents shorter than direct_min_bytes go through one
+  // strided-copy kernel that reads and writes it directly (no staging),
+  // longer ones through one hipMemcpyAsync per (storage, extent). A pageable
+  // host region (host_copy_threads > 0) goes through a bounce lane: the
+  // strided kernel packs the live bytes into staging chunks, one DMA per
+  // chunk, host threads place them. The caller has validated every range.
   StatusOr<CopyFuture> CopyExtents(Direction dir,
                                    const std::vector<StorageView>& storages,
                                    const std::vector<ByteExtent>& extents,
@@ -241,9 +244,33 @@ class TransferEngine {
                       const std::vector<StorageView>& storages,
                       const std::vector<int64_t>& cdev, const std::vector<int64_t>& chost,
                       hipStream_t dep, hipEvent_t* done);
+  // One staging chunk of a pipelined copy: its bytes in the chunk buffer,
+  // the host side as segments, the device side as a kernel between the
+  // storages and the chunk buffer (its address is the argument).
+  struct HostSegment {
+    uint8_t* host;
+    int64_t off;  // in the chunk buffer
+    int64_t bytes;
+  };
+  struct ChunkWork {
+    int64_t bytes = 0;
+    std::vector<HostSegment> segs;
+    std::function<Status(uint64_t)> kernel;
+  };
+  // Runs `chunks` through the lane's staging ring (and bounce buffers); D2H
+  // through bounce buffers has every byte in host memory on return.
+  Status PipelineChunks(const LaneView& lane, Direction dir, const std::vector<ChunkWork>& chunks,
+                        int64_t* memcpys);
+  // Pool extents through a pageable lane (*done as StagedOnLane).
+  Status ExtentsOnLane(const LaneView& lane, Direction dir,
+                       const std::vector<StorageView>& storages,
+                       const std::vector<ByteExtent>& extents, hipEvent_t* done);
+  // Queues a block copy (cdev/chost) or a pool-extent copy (extents) on the
+  // pageable lane of `dir`.
   StatusOr<CopyFuture> CopyPageable(Direction dir, const std::vector<StorageView>& storages,
                                     const std::vector<int64_t>& cdev,
-                                    const std::vector<int64_t>& chost, hipStream_t dep);
+                                    const std::vector<int64_t>& chost,
+                                    const std::vector<ByteExtent>& extents, hipStream_t dep);
   StatusOr<PageableLane*> Lane(Direction dir);
   void LaneLoop(PageableLane* lane);
   StatusOr<CopyFuture> CopyZeroCopy(Direction dir,
