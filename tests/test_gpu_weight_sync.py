@@ -169,4 +169,15 @@ def test_llama3_8b_parameter_set_round_trip_and_column_split(kvx, cuda):
     for m, bounds, chunk in outs:
         for b, c in zip(bounds, chunk):
             assert torch.equal(c.view(torch.int16), m[:, b[1][0]:b[1][1]].view(torch.int16))
+    # The same split again through a prepared plan, twice, into cleared outputs.
+    plan = kvx.StridedPlan(entries)
+    for _ in range(2):
+        for _, _, chunk in outs:
+            for c in chunk:
+                c.zero_()
+        kvx.copy_strided(plan, device=0).Await()
+        torch.cuda.synchronize()
+        for m, bounds, chunk in outs:
+            for b, c in zip(bounds, chunk):
+                assert torch.equal(c.view(torch.int16), m[:, b[1][0]:b[1][1]].view(torch.int16))
     ws.close()

@@ -61,6 +61,23 @@ def test_column_split_entries_equal_numpy_slicing(kvx):
             assert np.array_equal(o.numpy(), w.numpy()[:, b[1][0]:b[1][1]])
 
 
+def test_strided_plan_holds_the_entries(kvx):
+    """A StridedPlan is the C-ABI entry array of its entries, field by field
+    (offsets folded into the addresses)."""
+    rng = np.random.default_rng(3)
+    entries = [kvx.StridedEntry(int(rng.integers(1, 1 << 47)), int(rng.integers(1, 1 << 47)),
+                                int(rng.integers(1, 1 << 20)), int(rng.integers(1, 5000)),
+                                int(rng.integers(0, 1 << 30)), int(rng.integers(0, 1 << 30)))
+               for _ in range(300)]
+    plan = kvx.StridedPlan(entries)
+    assert plan.n == 300
+    for e, a in zip(entries, plan._arr):
+        assert (a.src, a.dst, a.size_bytes, a.count, a.src_stride_bytes,
+                a.dst_stride_bytes) == e.as_tuple()
+        assert a.src_offset_bytes == 0 and a.dst_offset_bytes == 0
+    assert kvx.StridedPlan([]).n == 0
+
+
 def test_offset_table_definition():
     offs, total = W.offset_table([10, 256, 1, 0, 300])
     assert offs == [0, 256, 512, 768, 768] and total == 1280

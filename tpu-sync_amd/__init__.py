@@ -11,13 +11,13 @@ from .kv_cache_store import (BlockStatus, KVCacheMetadata, KVCacheMetadataShmReg
                              KVCacheStore, LRUCache, RaidenBlockId, RaidenId)
 from . import copy_plan, pool_layout, transport
 from .pool_layout import PoolSpec, RegionSpec
-from .weight_synchronizer import (StridedEntry, WeightSynchronizer, column_split_entries,
-                                  compute_nd_shard_slices, copy_strided)
+from .weight_synchronizer import (StridedEntry, StridedPlan, WeightSynchronizer,
+                                  column_split_entries, compute_nd_shard_slices, copy_strided)
 
 __all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError",
            "KVCacheStore", "RaidenId", "RaidenBlockId", "BlockStatus", "LRUCache",
            "KVCacheMetadata", "KVCacheMetadataShmRegion", "WeightSynchronizer",
-           "StridedEntry", "copy_strided", "column_split_entries",
+           "StridedEntry", "StridedPlan", "copy_strided", "column_split_entries",
            "compute_nd_shard_slices", "pool_layout", "copy_plan", "transport", "PoolSpec", "RegionSpec",
            "library_path"]
 
