@@ -253,19 +253,24 @@ Status TransferEngine::Init() {
       hipStreamCreateWithFlags(&h2d_stream_, hipStreamNonBlocking));
   KVX_HIP_RETURN_IF_ERROR(
       hipStreamCreateWithFlags(&scatter_stream_, hipStreamNonBlocking));
-  for (Ring* r : {&out_ring_, &in_ring_}) {
-    for (int k = 0; k < opts_.staging_chunks; ++k) {
-      void* p = nullptr;
-      KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, opts_.staging_chunk_bytes));
-      r->bufs.push_back(reinterpret_cast<uint64_t>(p));
-      KVX_ASSIGN_OR_RETURN(hipEvent_t ready, NewEvent());
-      KVX_ASSIGN_OR_RETURN(hipEvent_t free_ev, NewEvent());
-      r->ready.push_back(ready);
-      r->free.push_back(free_ev);
-      r->used.push_back(false);
-    }
-  }
   return GrowArgRing(opts_.arg_ring_bytes);
+}
+
+Status TransferEngine::EnsureRing(Ring* r) {
+  // Allocated on first use: a manager whose copies all go zero-copy or
+  // through the pageable lanes never holds these chunks.
+  if (!r->bufs.empty()) return OkStatus();
+  for (int k = 0; k < opts_.staging_chunks; ++k) {
+    void* p = nullptr;
+    KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, opts_.staging_chunk_bytes));
+    r->bufs.push_back(reinterpret_cast<uint64_t>(p));
+    KVX_ASSIGN_OR_RETURN(hipEvent_t ready, NewEvent());
+    KVX_ASSIGN_OR_RETURN(hipEvent_t free_ev, NewEvent());
+    r->ready.push_back(ready);
+    r->free.push_back(free_ev);
+    r->used.push_back(false);
+  }
+  return OkStatus();
 }
 
 TransferEngine::~TransferEngine() {
@@ -813,6 +818,7 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
   lane.ks = d2h ? gather_stream_ : scatter_stream_;
   lane.cs = d2h ? d2h_stream_ : h2d_stream_;
   lane.ring = d2h ? &out_ring_ : &in_ring_;
+  KVX_RETURN_IF_ERROR(EnsureRing(lane.ring));
   hipEvent_t done = nullptr;
   KVX_RETURN_IF_ERROR(StagedOnLane(lane, dir, storages, cdev, chost, dep, &done));
   ++stats_.staged_copies;

@@ -286,6 +286,7 @@ class TransferEngine {
                           std::vector<int64_t>* dev_ids,
                           std::vector<int64_t>* host_ids);
   StatusOr<hipEvent_t> NewEvent();
+  Status EnsureRing(Ring* r);
   // Launches one block-copy kernel, bracketed by timing events when
   // profiling is on.
   Status LaunchCopy(const CopyLaunch& l, bool gather, int vec,
