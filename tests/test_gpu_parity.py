@@ -109,7 +109,7 @@ MODES = ["staged", "zero_copy"]
 
 
 @pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "pageable"])
-@pytest.mark.parametrize("bb", [32768, 1024, 48, 36, 3])
+@pytest.mark.parametrize("bb", [32768, 61424, 12992, 1024, 48, 36, 3])
 def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
     rng = np.random.default_rng(bb * 7 + len(path))
     layers, shards, blocks, hb = 3, 2, 40, 30
@@ -216,10 +216,14 @@ def test_reference_known_answers_dtypes(kvx, cuda, golden):
                 mgr.close()
 
 
+@pytest.mark.parametrize("bb", [2048, 12992])
 @pytest.mark.parametrize("block_major", [False, True])
-def test_device_gather_scatter_match_oracle(kvx, oracle, cuda, block_major):
+def test_device_gather_scatter_match_oracle(kvx, oracle, cuda, block_major, bb):
+    """bb 2048: many blocks per workgroup; bb 12992 (812 vectors): one block
+    per workgroup on the single-piece fast path, its 4/2/1-vector tail, and
+    the scatter's storage-interleaved order."""
     rng = np.random.default_rng(8)
-    L, P, bb = 6, 96, 2048
+    L, P = 6, 96
     host, dev = dev_pools(rng, cuda, L, 1, P, bb)
     mgr = make_mgr(kvx, dev, 4)
     ids = rng.choice(P, size=40, replace=False)

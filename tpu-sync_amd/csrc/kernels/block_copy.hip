@@ -93,7 +93,23 @@ __device__ __forceinline__ void copy_whole_block(const KVX_GLOBAL V* __restrict_
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) st_nt(r[u], dst + k + u * kThreads);
   }
-  for (; k < elems; k += kThreads) st_nt(ld_nt(src + k), dst + k);
+  // The tail (all of a 16 KiB block) still keeps 4, then 2 loads in flight.
+  if (k + 3 * kThreads < elems) {
+    V r[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r[u] = ld_nt(src + k + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) st_nt(r[u], dst + k + u * kThreads);
+    k += 4 * kThreads;
+  }
+  if (k + kThreads < elems) {
+    const V r0 = ld_nt(src + k);
+    const V r1 = ld_nt(src + k + kThreads);
+    st_nt(r0, dst + k);
+    st_nt(r1, dst + k + kThreads);
+    k += 2 * kThreads;
+  }
+  if (k < elems) st_nt(ld_nt(src + k), dst + k);
 }
 
 __device__ __forceinline__ KPiece select_piece(const KParams& P, uint32_t wg) {
