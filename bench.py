@@ -456,7 +456,8 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     host_blocks = args.zipf_host_blocks
     S = 2 * L
     log(f"zipf: allocating {S} x {P} x {bb} B pool ({S * P * bb / 2**30:.1f} GiB), "
-        f"{host_blocks} host blocks ({host_blocks * S * bb / 2**30:.1f} GiB pinned)")
+        f"{host_blocks} host blocks ({host_blocks * S * bb / 2**30:.1f} GiB "
+        f"{args.zipf_host_alloc})")
     pools = [torch.empty(P, bb, dtype=torch.uint8, device=dev) for _ in range(S)]
     for p in pools:
         p.random_(0, 256)
