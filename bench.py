@@ -490,7 +490,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
                     raise RuntimeError(f"store save failed: {len(failed)} blocks")
                 got_s += len(done)
 
-    moved = saved = loaded = hits = asked = skipped = 0
+    moved = saved = loaded = hits = asked = skipped = device_hits = 0
     t_run = 0.0
     for step in range(args.zipf_batches):
         doc = int(np.searchsorted(cdf, rng.random()))
@@ -501,22 +501,32 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
         found = store.lookup(chain, pin_found=True)
         k = len(found)
         rest = chain[k:]
-        if k:
-            assert store.load(chain[:k], dev_ids[:k])
+        # Host-resident hits are loaded; an HBM-only entry (inserted by a
+        # request whose save could not get host blocks) names a device block
+        # the caller still owns: a hit with nothing to move.
+        on_host = (pkg.BlockStatus.HOST, pkg.BlockStatus.HOST_AND_HBM)
+        load_h = [h for h, b in found if b.status in on_host]
+        load_d = [dev_ids[i] for i, (_, b) in enumerate(found) if b.status in on_host]
+        in_hbm = [h for h, b in found if b.status not in on_host]
+        if in_hbm:
+            store.release(in_hbm)
+            device_hits += len(in_hbm)
+        if load_h and not store.load(load_h, load_d):
+            raise RuntimeError(f"store load of {len(load_h)} blocks failed: {store.last_error()}")
         n_save = 0
         if rest:
             sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
             if store.insert(rest, sl, on_host=False):
                 if store.save(rest):
                     n_save = len(rest)
-                else:  # a block past the prefix is still cached (a hole)
+                else:  # no host blocks to spare (everything else pinned)
                     store.release(rest)
                     skipped += len(rest)
             else:
                 skipped += len(rest)
-        poll_all(k, n_save)
+        poll_all(len(load_h), n_save)
         t_run += time.perf_counter() - t0
-        loaded += k
+        loaded += len(load_h)
         saved += n_save
         hits += k
         asked += nb
@@ -527,7 +537,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
            "host_tier_blocks": host_blocks, "host_tier_memory": args.zipf_host_alloc,
            "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
            "batches": args.zipf_batches, "blocks_saved": saved, "blocks_loaded": loaded,
-           "blocks_skipped": skipped,
+           "blocks_skipped": skipped, "device_hits": device_hits,
            "hit_rate": round(hits / max(asked, 1), 4),
            "gbps": round(moved / t_run / 1e9, 2),
            "blocks_per_s": round((saved + loaded) / t_run, 1)}

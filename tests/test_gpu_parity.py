@@ -585,19 +585,24 @@ def test_zero_copy_needs_pinned_host(kvx, cuda):
 
 
 def test_auto_mode_picks_by_host_fragmentation(kvx, cuda):
-    """Auto mode stages copies whose host ids form long runs and moves
-    fragmented ones with the zero-copy kernel; both are bit-exact."""
+    """Auto mode stages copies whose host runs average at least 4 MiB per
+    storage and moves shorter ones with the zero-copy kernel; both are
+    bit-exact."""
     rng = np.random.default_rng(31)
-    host, dev = dev_pools(rng, cuda, 2, 1, 256, 4096)
+    bb = 65536
+    host, dev = dev_pools(rng, cuda, 2, 1, 256, bb)
     mgr = make_mgr(kvx, dev, 256)
     ids = rng.choice(256, size=64, replace=False).tolist()
-    mgr.d2h(ids, list(range(64))).Await()
+    mgr.d2h(ids, list(range(64))).Await()  # one 4 MiB run per storage
     assert mgr.engine_stats()["staged_copies"] == 1
-    hids = (64 + rng.choice(192, size=64, replace=False)).tolist()  # clear of 0..63
-    mgr.d2h(ids, hids).Await()
+    mgr.d2h(ids[:32], list(range(64, 96))).Await()  # one 2 MiB run
     assert mgr.engine_stats()["zero_copy_copies"] == 1
+    hids = (96 + rng.choice(160, size=64, replace=False)).tolist()  # clear of 0..95
+    mgr.d2h(ids, hids).Await()
+    assert mgr.engine_stats()["zero_copy_copies"] == 2
     for l in range(2):
-        hv = mgr.host_view(l).reshape(256, 4096)
+        hv = mgr.host_view(l).reshape(256, bb)
+        assert np.array_equal(hv[64:96], host[l][0][ids[:32]])
         assert np.array_equal(hv[:64], host[l][0][ids])
         assert np.array_equal(hv[hids], host[l][0][ids])
     mgr.close()

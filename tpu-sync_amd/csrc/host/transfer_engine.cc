@@ -530,13 +530,13 @@ StatusOr<CopyFuture> TransferEngine::Copy(
   if (opts_.mode == TransferMode::kAuto && host_ok) {
     // The staged path costs one hipMemcpyAsync per (storage, host run) and
     // lets SDMA carry H2D next to a D2H in flight; the zero-copy kernel costs
-    // the same for any host layout. Fragmented host ids (short runs) go
-    // zero-copy.
+    // the same for any host layout. Short host runs go zero-copy.
     int64_t runs = 0;
     for (size_t i = 0; i < chost.size(); ++i) {
       if (i == 0 || chost[i] != chost[i - 1] + 1) ++runs;
     }
-    zero_copy = static_cast<int64_t>(chost.size()) < opts_.auto_staged_min_run * runs;
+    zero_copy = static_cast<int64_t>(chost.size()) * max_block <
+                opts_.auto_staged_min_run_bytes * runs;
   }
   if (zero_copy) {
     if (!host_ok) {

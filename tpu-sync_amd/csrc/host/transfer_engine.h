@@ -62,9 +62,10 @@ struct ByteExtent {
 //            mirror image for reload), pipelined chunk by chunk;
 //   kZeroCopy: one kernel moves every block between the pool and the pinned
 //            host mirror directly (GPU loads/stores over PCIe), no staging;
-//   kAuto: staged when the host ids form long runs (average at least
-//          auto_staged_min_run blocks) or the host memory is not mapped for
-//          the GPU; zero-copy for fragmented host ids.
+//   kAuto: staged when the host ids form long runs (average run of a
+//          storage at least auto_staged_min_run_bytes); zero-copy otherwise.
+//          Host memory the GPU cannot map always goes staged (through the
+//          pageable lanes).
 // Copies whose runs are all at least direct_min_bytes use one
 // hipMemcpyAsync per (storage, run) in every mode.
 enum class TransferMode : int { kAuto = 0, kStaged = 1, kZeroCopy = 2 };
@@ -86,8 +87,13 @@ struct EngineOptions {
   // time (measured on MI355X: 16 writers / 64 readers).
   int64_t zero_copy_d2h_workgroups = 16;
   int64_t zero_copy_h2d_workgroups = 64;
-  // kAuto stages a copy whose host runs average at least this many blocks.
-  int64_t auto_staged_min_run = 32;
+  // kAuto stages a copy whose host runs average at least this many bytes
+  // per storage. Measured on MI355X (Llama-3-8B KV, 64 storages): alone in
+  // its direction the zero-copy kernel is as fast or faster at every run
+  // length; with an offload and a reload in flight together, staging (SDMA
+  // for H2D) wins from 4 MiB runs (83 against 79 GB/s; 16 MiB: 93 against
+  // 82) and loses at 2 MiB and below (71 against 73; 1 MiB: 51 against 64).
+  int64_t auto_staged_min_run_bytes = 4ll << 20;
   // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
   // bounce buffers that this many host threads fill and drain, one lane per
   // direction with its own streams and staging ring (0: leave such copies to

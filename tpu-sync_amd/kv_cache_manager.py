@@ -52,8 +52,9 @@ class RaidenFuture:
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
-        if h and _capi._lib is not None:
-            _capi._lib.kvx_future_release(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and lib is not None:
+            lib.kvx_future_release(h)
 
 
 def _stream_ptr(stream) -> int:
@@ -147,8 +148,9 @@ class LogicalBlockManager:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h and getattr(self, "_owned", False) and _capi._lib is not None:
-            _capi._lib.kvx_block_manager_destroy(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and getattr(self, "_owned", False) and lib is not None:
+            lib.kvx_block_manager_destroy(h)
             self._h = None
 
 
@@ -802,8 +804,9 @@ class KVCacheManager:
 
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
-        if h and _capi._lib is not None:
-            _capi._lib.kvx_manager_destroy(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and lib is not None:
+            lib.kvx_manager_destroy(h)
 
     def __del__(self):
         self.close()

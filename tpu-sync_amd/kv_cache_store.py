@@ -365,8 +365,9 @@ class KVCacheStore:
 
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
-        if h and _capi._lib is not None:
-            _capi._lib.kvx_store_destroy(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and lib is not None:
+            lib.kvx_store_destroy(h)
 
     def __del__(self):
         self.close()
@@ -465,8 +466,9 @@ class LRUCache:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h and _capi._lib is not None:
-            _capi._lib.kvx_lru_destroy(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and lib is not None:
+            lib.kvx_lru_destroy(h)
             self._h = None
 
 
@@ -552,8 +554,9 @@ class KVCacheMetadataShmRegion:
 
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
-        if h and _capi._lib is not None:
-            _capi._lib.kvx_metadata_shm_release(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and lib is not None:
+            lib.kvx_metadata_shm_release(h)
 
     def __del__(self):
         self.close()

@@ -265,8 +265,9 @@ class WeightSynchronizer:
 
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
-        if h and _capi._lib is not None:
-            _capi._lib.kvx_weight_sync_destroy(h)
+        lib = _capi._lib if _capi is not None else None  # None at interpreter exit
+        if h and lib is not None:
+            lib.kvx_weight_sync_destroy(h)
 
     def __del__(self):
         self.close()
