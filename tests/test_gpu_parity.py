@@ -606,3 +606,28 @@ def test_auto_mode_picks_by_host_fragmentation(kvx, cuda):
         assert np.array_equal(hv[:64], host[l][0][ids])
         assert np.array_equal(hv[hids], host[l][0][ids])
     mgr.close()
+
+
+@pytest.mark.parametrize("host_alloc", ["pinned", "malloc"])
+def test_empty_and_zero_size_copies_move_nothing(kvx, cuda, host_alloc):
+    """Zero-size runs, empty id lists and empty entry lists are no-ops that
+    return completed futures, on every path (pinned and pageable mirrors)."""
+    rng = np.random.default_rng(21)
+    host, dev = dev_pools(rng, cuda, 2, 1, 16, 4096)
+    mgr = make_mgr(kvx, dev, 16, host_alloc=host_alloc)
+    before = [d[0].clone() for d in dev]
+    for f in (mgr.d2h([3], [4], [0]), mgr.h2d([4], [3], [0]),
+              mgr.d2h([1, 2], [5, 6], [0, 0])):
+        f.Await()
+        assert f.IsReady()
+    stg = torch.empty(0, dtype=torch.uint8, device=cuda)
+    mgr.gather([], stg).Await()
+    mgr.scatter([], stg).Await()
+    mgr.d2h_pool_blocks(0, []).Await()
+    mgr.h2d_pool_blocks(1, []).Await()
+    kvx.copy_strided([], device=0).Await()
+    mgr.wait_for_pending_work()
+    for l in range(2):
+        assert not mgr.host_view(l).any()
+        assert torch.equal(dev[l][0], before[l])
+    mgr.close()
