@@ -450,17 +450,18 @@ def test_futures_and_stream_order(kvx, cuda):
     mgr.close()
 
 
-def test_concurrent_disjoint_blocks(kvx, cuda):
+@pytest.mark.parametrize("host_alloc", ["pinned", "malloc"])
+def test_concurrent_disjoint_blocks(kvx, cuda, host_alloc):
     """tpu_sync/frameworks/jax/kv_cache_manager_test.py:520-594: one thread
     loops H2D/D2H of blocks 0:4 while another moves 4:8 once; both ranges
-    keep their values."""
+    keep their values (malloc: both threads share the bounce lanes)."""
     shape = (8, 128 * 8 * 8 * 128 * 4 // 8)
     init = np.zeros(shape, np.float32)
     init[0:4] = 1.0
     init[4:8] = 2.0
     raw = init.view(np.uint8).reshape(8, -1)
     pools = [torch.from_numpy(raw.copy()).to(cuda) for _ in range(2)]
-    mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=8)
+    mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=8, host_alloc=host_alloc)
     mgr.d2h().Await()
     stop = threading.Event()
     errors = []
