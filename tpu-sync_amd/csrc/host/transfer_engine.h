@@ -185,7 +185,8 @@ class TransferEngine {
   // block size form one piece of the kernel (see block_copy.h).
   int device() const { return opts_.device; }
   EngineStats stats() const;
-  // Blocks until everything enqueued on the engine's streams has finished.
+  // Blocks until both pageable lanes have drained and everything enqueued on
+  // the engine's streams has finished.
   Status Synchronize();
   // Sums the profiled launches of gather (or scatter) kernels recorded so
   // far; waits for them to finish. `reset` drops the samples.
@@ -245,7 +246,8 @@ class TransferEngine {
                                   const std::vector<int64_t>& chost,
                                   hipStream_t dep);
   // The staged pipeline on `lane`; *done receives the completion event, or
-  // nullptr when the copy is complete on return (D2H through bounce buffers).
+  // nullptr for a D2H through bounce buffers, which completes when its last
+  // bounce slot drains (the lane then fulfils its future).
   Status StagedOnLane(const LaneView& lane, Direction dir,
                       const std::vector<StorageView>& storages,
                       const std::vector<int64_t>& cdev, const std::vector<int64_t>& chost,
@@ -263,8 +265,9 @@ class TransferEngine {
     std::vector<HostSegment> segs;
     std::function<Status(uint64_t)> kernel;
   };
-  // Runs `chunks` through the lane's staging ring (and bounce buffers); D2H
-  // through bounce buffers has every byte in host memory on return.
+  // Runs `chunks` through the lane's staging ring (and bounce buffers). A D2H
+  // through bounce buffers returns with its last slots still owed to host
+  // memory; they drain when their slot comes round again or the lane idles.
   Status PipelineChunks(const LaneView& lane, Direction dir, const std::vector<ChunkWork>& chunks,
                         int64_t* memcpys);
   // Pool extents through a pageable lane (*done as StagedOnLane).
