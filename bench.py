@@ -595,6 +595,11 @@ def main():
                                   transfer_mode=mode)
 
     mgr = make_mgr(args.mode)
+    nodes = [d for d in os.listdir("/sys/devices/system/node") if d.startswith("node")] \
+        if os.path.isdir("/sys/devices/system/node") else []
+    host_info = {"gpu_numa_node": int(pkg._capi.load().kvx_gpu_numa_node(0)),
+                 "mirror_numa_node": mgr.assigned_numa_node,
+                 "numa_nodes": len(nodes), "cpus": os.cpu_count()}
     log(f"manager ready (mode {args.mode})")
     rng = np.random.default_rng(0)
     slots = [list(range(k * n, (k + 1) * n)) for k in range(4)]
@@ -752,6 +757,7 @@ def main():
         "hbm_copy_same_bytes_gbps": round(hbm_copy_gbps, 1),
         "gather_frac_of_measured_copy": round(iso["gather"]["achieved"] / hbm_copy_gbps, 4),
         "cpu_baseline": cpu,
+        "host": host_info,
         **extras,
         "configs": configs,
     }
