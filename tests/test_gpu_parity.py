@@ -1,8 +1,10 @@
 """GPU parity: the HIP path (libkvx through its C-ABI) against the oracle on
-the same seeded inputs, bit-exact. Covers the direct and the staged
-(gather/scatter kernel + pipelined DMA) paths, every vector width of the
-kernel, layer/shard/slot restrictions, the reference's e2e known answers,
-device gather/scatter, bad ids, and a full-size Llama-3-8B pool round trip.
+the same seeded inputs, bit-exact. Covers the direct, staged (gather/scatter
+kernel + pipelined DMA), zero-copy, bounce-lane (pageable mirrors) and
+runtime-pageable paths, every vector width of the kernel and its tail,
+layer/shard/slot restrictions, the reference's e2e known answers, device
+gather/scatter, bad ids, empty copies, threads, the auto-mode choice and a
+full-size Llama-3-8B pool round trip.
 """
 import os
 import threading
