@@ -78,6 +78,9 @@ def parse_args():
                    help="host tier memory: pinned (hipHostMalloc) or a /dev/shm segment")
     p.add_argument("--zipf-docs", type=int, default=8,
                    help="documents whose hash-chain prefixes the churn requests")
+    p.add_argument("--zipf-inflight", type=int, default=1,
+                   help="requests whose copies may be in flight at once (1: each "
+                        "request's load and save finish before the next is issued)")
     p.add_argument("--rocpd-summary", metavar="DB",
                    help="print per-kernel (name, grid) duration statistics of a "
                         "rocprofv3 results database and exit")
@@ -458,7 +461,9 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     blocks log-uniform). Lookup returns the cached prefix, which is loaded
     into device blocks; the rest is inserted and saved (evicting LRU entries
     once the host tier is full). Load (H2D) and save (D2H) of a request are
-    issued together and polled together."""
+    issued together; up to --zipf-inflight requests have copies in flight
+    (the next request is looked up and issued while the previous one's
+    copies run), as in a server with several requests in progress."""
     L, P, bb = 80, 12000, 32768
     host_blocks = args.zipf_host_blocks
     S = 2 * L
@@ -483,43 +488,53 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     w = 1.0 / np.arange(1, docs + 1) ** 1.1
     cdf = np.cumsum(w) / w.sum()
 
-    def poll_all(want_load, want_save):
-        got_l = got_s = 0
-        while got_l < want_load or got_s < want_save:
-            if got_l < want_load:
+    done_l = done_s = 0
+    loading = set()  # hashes whose load has not been polled done
+
+    def poll_until(want_load, want_save):
+        nonlocal done_l, done_s
+        while done_l < want_load or done_s < want_save:
+            if done_l < want_load:
                 done, failed = store.poll_load_status()[:2]
                 if failed:
                     raise RuntimeError(f"store load failed: {len(failed)} blocks")
-                got_l += len(done)
-            if got_s < want_save:
+                done_l += len(done)
+                loading.difference_update(done)
+            if done_s < want_save:
                 done, failed = store.poll_save_status()[:2]
                 if failed:
                     raise RuntimeError(f"store save failed: {len(failed)} blocks")
-                got_s += len(done)
+                done_s += len(done)
 
-    moved = saved = loaded = hits = asked = skipped = device_hits = 0
-    t_run = 0.0
+    saved = loaded = hits = asked = skipped = device_hits = 0
+    inflight = max(1, args.zipf_inflight)
+    window = []  # (loads, saves) of the requests possibly still in flight
+    t0 = time.perf_counter()
     for step in range(args.zipf_batches):
         doc = int(np.searchsorted(cdf, rng.random()))
         nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
         chain = [b"d%03d:%05d" % (doc, i) for i in range(nb)]
         dev_ids = rng.permutation(P)[:nb].tolist()
-        t0 = time.perf_counter()
         found = store.lookup(chain, pin_found=True)
         k = len(found)
         rest = chain[k:]
         # Host-resident hits are loaded; an HBM-only entry (inserted by a
-        # request whose save could not get host blocks) names a device block
-        # the caller still owns: a hit with nothing to move.
+        # request whose save could not get host blocks, or whose save is
+        # still in flight) names a device block the caller owns: a hit with
+        # nothing to move.
+        # A block another request in flight is loading arrives with that
+        # load: also a hit with nothing to move.
         on_host = (pkg.BlockStatus.HOST, pkg.BlockStatus.HOST_AND_HBM)
-        load_h = [h for h, b in found if b.status in on_host]
-        load_d = [dev_ids[i] for i, (_, b) in enumerate(found) if b.status in on_host]
-        in_hbm = [h for h, b in found if b.status not in on_host]
+        to_load = [b.status in on_host and h not in loading for h, b in found]
+        load_h = [h for (h, _), t in zip(found, to_load) if t]
+        load_d = [dev_ids[i] for i, t in enumerate(to_load) if t]
+        in_hbm = [h for (h, _), t in zip(found, to_load) if not t]
         if in_hbm:
             store.release(in_hbm)
             device_hits += len(in_hbm)
         if load_h and not store.load(load_h, load_d):
             raise RuntimeError(f"store load of {len(load_h)} blocks failed: {store.last_error()}")
+        loading.update(load_h)
         n_save = 0
         if rest:
             sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
@@ -529,21 +544,28 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
                 else:  # no host blocks to spare (everything else pinned)
                     store.release(rest)
                     skipped += len(rest)
-            else:
+            else:  # another request in flight inserted some of them
                 skipped += len(rest)
-        poll_all(len(load_h), n_save)
-        t_run += time.perf_counter() - t0
         loaded += len(load_h)
         saved += n_save
         hits += k
         asked += nb
+        window.append((len(load_h), n_save))
+        # Keep at most `inflight` requests in flight: wait until every copy
+        # but those of the newest inflight - 1 requests has landed.
+        keep = window[len(window) - (inflight - 1):] if inflight > 1 else []
+        poll_until(loaded - sum(x[0] for x in keep), saved - sum(x[1] for x in keep))
+        window = keep
+    poll_until(loaded, saved)
+    t_run = time.perf_counter() - t0
     moved = (saved + loaded) * S * bb
     out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
                        "churn through the KV store: requests are prefixes (64-2048 blocks) of "
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
            "host_tier_blocks": host_blocks, "host_tier_memory": args.zipf_host_alloc,
            "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
-           "batches": args.zipf_batches, "blocks_saved": saved, "blocks_loaded": loaded,
+           "batches": args.zipf_batches, "requests_in_flight": inflight,
+           "blocks_saved": saved, "blocks_loaded": loaded,
            "blocks_skipped": skipped, "device_hits": device_hits,
            "hit_rate": round(hits / max(asked, 1), 4),
            "gbps": round(moved / t_run / 1e9, 2),
