@@ -54,15 +54,16 @@ extern "C" {
 #define KVX_HOST_PINNED 1 /* hipHostMalloc page-locked, zeroed */
 #define KVX_HOST_SHM 2    /* /dev/shm segment, survives the process */
 
-/* Transfer modes for copies whose runs are short (runs of at least
- * direct_min_bytes always use one hipMemcpyAsync per run):
+/* Transfer modes for copies whose runs are short (with a pinned mirror,
+ * runs of at least direct_min_bytes always use one hipMemcpyAsync per run):
  *   KVX_MODE_STAGED: gather kernel -> device staging ring -> hipMemcpyAsync
  *     (and H2D -> scatter for reload), pipelined chunk by chunk;
  *   KVX_MODE_ZERO_COPY: one kernel moves the blocks between the pool and the
  *     pinned host mirror directly over PCIe (needs KVX_HOST_PINNED);
- *   KVX_MODE_AUTO: staged when the host ids of a copy form long runs (an
- *     average of 32 blocks or more) or the mirror is not pinned, zero-copy
- *     for fragmented host ids. */
+ *   KVX_MODE_AUTO: staged when a copy's host runs average at least 4 MiB per
+ *     storage, zero-copy below that.
+ * A pageable mirror (KVX_HOST_MALLOC, KVX_HOST_SHM) is always staged, through
+ * the pinned bounce lanes (see host_copy_threads). */
 #define KVX_MODE_AUTO 0
 #define KVX_MODE_STAGED 1
 #define KVX_MODE_ZERO_COPY 2
