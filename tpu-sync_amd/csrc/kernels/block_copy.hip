@@ -212,10 +212,14 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
 // The common launch (one piece of large blocks, no second paged side, one
 // block per workgroup) without the piece selection: the workgroup reads the
 // block id and the storage base with two independent scalar loads and starts
-// its vector loads after one wait. With kInterleave (a scatter over whole
-// storages) consecutive workgroups take the same block index of consecutive
-// storages, so the writes in flight at any moment spread over every storage
-// instead of crowding one: 3 points of HBM bandwidth on random destinations.
+// its vector loads after one wait. Over whole storages the workgroup order
+// is chosen by measurement (random ids, 64 storages of 512 MiB):
+//   kAllStorages (scatter): consecutive workgroups take the same block index
+//     of consecutive storages, so the writes in flight spread over every
+//     storage instead of crowding one (+1 to +3 points of HBM bandwidth);
+//   kStoragePairs (gather): the same block index of storages 2q and 2q + 1,
+//     then the next index (+1.5 points against storage-major order; wider
+//     groups measured slower).
 struct FastParams {
   uint64_t storages;
   uint64_t staging;
@@ -227,16 +231,23 @@ struct FastParams {
   uint32_t f0;
   uint32_t n;
   uint32_t elems;
-  uint32_t wstorages;  // kInterleave: storages in the launch (f0 = w0 * n)
+  uint32_t wstorages;  // whole-storage orders: storages in the launch (f0 = w0 * n)
 };
 
-template <typename V, bool kGather, int kUnroll, bool kInterleave>
+enum FastOrder : int { kStorageMajor = 0, kStoragePairs = 1, kAllStorages = 2 };
+
+template <typename V, bool kGather, int kUnroll, int kOrder>
 __global__ __launch_bounds__(kThreads) void block_copy_fast_kernel(FastParams P) {
   const uint32_t g = blockIdx.x;
   uint32_t w, i;
-  if (kInterleave) {
+  if (kOrder == kAllStorages) {
     i = g / P.wstorages;
     w = P.f0 / P.n + (g - i * P.wstorages);
+  } else if (kOrder == kStoragePairs) {
+    const uint32_t q = g / (2 * P.n);
+    const uint32_t r = g - q * 2 * P.n;
+    i = r >> 1;
+    w = P.f0 / P.n + 2 * q + (r & 1);
   } else {
     const uint32_t f = P.f0 + g;
     w = f / P.n;
@@ -330,7 +341,7 @@ bool BuildParams(const CopyLaunch& l, int vec_bytes, KParams* P,
 
 // The fast kernel's parameters when the launch qualifies (one whole-block
 // piece, bpw 1, no second paged side).
-bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, bool* interleave) {
+bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, int* order) {
   const KPiece& p = K.p[0];
   if (K.npieces != 1 || !p.whole || p.bpw != 1 || p.others != 0) return false;
   *F = FastParams{};
@@ -344,25 +355,36 @@ bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, bool* interle
   F->f0 = p.f0;
   F->n = K.n;
   F->elems = p.elems;
-  *interleave = dir == CopyDir::kScatter && p.f0 % K.n == 0 && p.nblocks % K.n == 0 &&
-                p.nblocks / K.n >= 2;
-  F->wstorages = *interleave ? p.nblocks / K.n : 0;
+  const bool whole_storages = p.f0 % K.n == 0 && p.nblocks % K.n == 0;
+  const uint32_t W = p.nblocks / K.n;
+  *order = kStorageMajor;
+  if (whole_storages && W >= 2) {
+    if (dir == CopyDir::kScatter) {
+      *order = kAllStorages;
+    } else if (W % 2 == 0) {
+      *order = kStoragePairs;
+    }
+  }
+  F->wstorages = W;
   return true;
 }
 
 template <typename V, int kUnroll>
 hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, hipStream_t stream) {
   FastParams F;
-  bool interleave = false;
-  if (BuildFastParams(P, dir, &F, &interleave)) {
-    if (dir == CopyDir::kGather) {
-      hipLaunchKernelGGL((block_copy_fast_kernel<V, true, kUnroll, false>), dim3(grid),
+  int order = kStorageMajor;
+  if (BuildFastParams(P, dir, &F, &order)) {
+    if (dir == CopyDir::kGather && order == kStoragePairs) {
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, true, kUnroll, kStoragePairs>), dim3(grid),
                          dim3(kThreads), 0, stream, F);
-    } else if (interleave) {
-      hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, true>), dim3(grid),
+    } else if (dir == CopyDir::kGather) {
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, true, kUnroll, kStorageMajor>), dim3(grid),
+                         dim3(kThreads), 0, stream, F);
+    } else if (order == kAllStorages) {
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, kAllStorages>), dim3(grid),
                          dim3(kThreads), 0, stream, F);
     } else {
-      hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, false>), dim3(grid),
+      hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, kStorageMajor>), dim3(grid),
                          dim3(kThreads), 0, stream, F);
     }
     return hipGetLastError();
