@@ -272,6 +272,14 @@ int kvx_future_is_ready(kvx_future* f);
 int kvx_future_poll_error(kvx_future* f);
 int kvx_future_await(kvx_future* f);
 int kvx_future_wait_on_stream(kvx_future* f, void* stream);
+/* PjRtCopyFuture::OnReady (tpu_sync/core/raw_transfer_core.h:491-530): calls
+ * cb(user, code) once the copy is done, with its final status code (the
+ * message of a failure is not available to the callback). A done copy calls
+ * cb before this returns; otherwise one library thread shared by all
+ * futures calls it, so cb must not block for long. The future may be
+ * released before cb runs. */
+typedef void (*kvx_ready_fn)(void* user, int32_t code);
+int kvx_future_on_ready(kvx_future* f, kvx_ready_fn cb, void* user);
 void kvx_future_release(kvx_future* f);
 
 /*

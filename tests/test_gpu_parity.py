@@ -634,3 +634,48 @@ def test_empty_and_zero_size_copies_move_nothing(kvx, cuda, host_alloc):
         assert not mgr.host_view(l).any()
         assert torch.equal(dev[l][0], before[l])
     mgr.close()
+
+
+def test_on_ready_callbacks(kvx, cuda):
+    """PjRtCopyFuture::OnReady (raw_transfer_core.h:491-530): each callback
+    runs once, after its copy's bytes landed, with the final status code; on
+    a done future before on_ready returns; a failed (queued, invalid) copy
+    reports its code."""
+    rng = np.random.default_rng(23)
+    host, dev = dev_pools(rng, cuda, 4, 1, 64, 65536)
+    mgr = make_mgr(kvx, dev, 64)
+    got = {}
+    done = threading.Event()
+
+    def record(k):
+        def cb(code):
+            # The copy's bytes are in the host mirror when the callback runs.
+            ok = np.array_equal(mgr.host_view(0).reshape(64, 65536)[k], host[0][0][k])
+            got[k] = (code, ok)
+            if len(got) == 16:
+                done.set()
+        return cb
+
+    for k in range(16):
+        mgr.d2h([k], [k], [1]).on_ready(record(k))
+    assert done.wait(60)
+    assert all(v == (0, True) for v in got.values()), got
+    f = mgr.d2h([20], [20], [1])
+    f.Await()
+    sync_codes = []
+    f.on_ready(sync_codes.append)  # already done: called before returning
+    assert sync_codes == [0]
+    mgr.close()
+    qm = make_mgr(kvx, dev, 64, dispatch="queued")
+    codes = []
+    fired = threading.Event()
+    bad = qm.d2h([70], [0], [1])  # device range error, reported through the future
+
+    def on_bad(code):
+        codes.append(code)
+        fired.set()
+
+    bad.on_ready(on_bad)
+    assert fired.wait(60)
+    assert codes == [3]
+    qm.close()

@@ -198,6 +198,9 @@ class PushItemC(ctypes.Structure):
     _fields_ = [(k, ctypes.c_int64) for k in ("layer", "shard", "k", "staging_offset", "size")]
 
 
+# kvx_ready_fn(user, code)
+READY_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32)
+
 # kvx_transfer_fn(user, d2h, src, dst, n) -> status
 TRANSFER_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                ctypes.POINTER(ctypes.c_int64),
@@ -249,6 +252,7 @@ PROTOTYPES = {
     "kvx_future_poll_error": (_int, [_vp]),
     "kvx_future_await": (_int, [_vp]),
     "kvx_future_wait_on_stream": (_int, [_vp, _vp]),
+    "kvx_future_on_ready": (_int, [_vp, ctypes.c_void_p, _vp]),
     "kvx_future_release": (None, [_vp]),
     "kvx_block_manager_create": (_int, [_i32, ctypes.POINTER(_vp)]),
     "kvx_block_manager_destroy": (None, [_vp]),

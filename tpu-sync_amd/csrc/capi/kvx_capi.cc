@@ -504,6 +504,11 @@ int kvx_future_wait_on_stream(kvx_future* f, void* stream) {
   if (f == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null future");
   return Done(f->f.WaitOnStream(static_cast<hipStream_t>(stream)));
 }
+int kvx_future_on_ready(kvx_future* f, kvx_ready_fn cb, void* user) {
+  if (f == nullptr || cb == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null future or callback");
+  f->f.OnReady([cb, user](kvx::Status st) { cb(user, static_cast<int32_t>(st.code())); });
+  return KVX_OK;
+}
 void kvx_future_release(kvx_future* f) { delete f; }
 
 int kvx_block_manager_create(int32_t num_blocks, kvx_block_manager** out) {

@@ -1,10 +1,60 @@
 #include "copy_future.h"
 
+#include <chrono>
+#include <list>
 #include <thread>
 
 #include "hip_util.h"
 
 namespace kvx {
+
+// One process-wide thread runs every OnReady callback whose copy was not yet
+// done at registration: it polls the pending copies (never blocking on one
+// while another may finish first) and calls each callback, outside its lock,
+// once its copy is done. A callback that blocks delays the ones after it.
+class ReadyPoller {
+ public:
+  static ReadyPoller& Get() {
+    // Never destroyed: callbacks may still be pending at process exit.
+    static ReadyPoller* p = new ReadyPoller();
+    return *p;
+  }
+  void Add(std::shared_ptr<CopyFuture::State> s, std::function<void(Status)> cb) {
+    {
+      std::lock_guard<std::mutex> l(mu_);
+      items_.push_back(Item{std::move(s), std::move(cb)});
+    }
+    cv_.notify_one();
+  }
+
+ private:
+  struct Item {
+    std::shared_ptr<CopyFuture::State> state;
+    std::function<void(Status)> cb;
+  };
+  ReadyPoller() {
+    std::thread([this] { Loop(); }).detach();
+  }
+  void Loop() {
+    while (true) {
+      std::list<Item> ready;
+      {
+        std::unique_lock<std::mutex> l(mu_);
+        cv_.wait(l, [this] { return !items_.empty(); });
+        for (auto it = items_.begin(); it != items_.end();) {
+          auto next = std::next(it);
+          if (CopyFuture::StateReady(*it->state)) ready.splice(ready.end(), items_, it);
+          it = next;
+        }
+      }
+      for (Item& r : ready) r.cb(CopyFuture::StateAwait(*r.state));
+      if (ready.empty()) std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+  }
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::list<Item> items_;
+};
 
 CopyFuture::State::~State() {
   for (hipEvent_t e : events) {
@@ -148,8 +198,7 @@ void CopyFuture::OnReady(std::function<void(Status)> cb) const {
     cb(Await());
     return;
   }
-  std::shared_ptr<State> s = state_;
-  std::thread([s, cb = std::move(cb)]() { cb(StateAwait(*s)); }).detach();
+  ReadyPoller::Get().Add(state_, std::move(cb));
 }
 
 }  // namespace kvx

@@ -61,6 +61,7 @@ class CopyFuture {
     bool done = false;
     ~State();
   };
+  friend class ReadyPoller;
   static void WaitIssued(const State& s);
   static bool StateReady(const State& s);
   static Status StatePoll(const State& s);

@@ -18,6 +18,9 @@ from typing import Any, List, Optional, Sequence, Tuple
 from . import _capi
 
 
+_pending_callbacks = {}  # OnReady trampolines the library has not called yet
+
+
 class RaidenFuture:
     """Async completion of one copy (tpu_sync/core/raiden_future.h:25-36)."""
 
@@ -45,10 +48,28 @@ class RaidenFuture:
         _capi.check(_capi.load().kvx_future_wait_on_stream(
             self._h, ctypes.c_void_p(_stream_ptr(stream))), self._where)
 
+    def OnReady(self, fn) -> None:
+        """Calls fn(code) once the copy is done (code 0 on success, else the
+        absl status code), from a library thread unless it is already done;
+        raiden_future.h / PjRtCopyFuture::OnReady."""
+        key = object()
+
+        def tramp(_user, code):
+            _pending_callbacks.pop(key, None)
+            fn(int(code))
+
+        cb = _capi.READY_FN(tramp)
+        _pending_callbacks[key] = cb  # alive until the library calls it
+        rc = _capi.load().kvx_future_on_ready(self._h, cb, None)
+        if rc != 0:
+            _pending_callbacks.pop(key, None)
+            _capi.check(rc, self._where)
+
     # Pythonic aliases.
     await_ = Await
     is_ready = IsReady
     poll_error = PollError
+    on_ready = OnReady
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
