@@ -34,8 +34,8 @@ HBM_PEAK_GBPS = 8000.0
 # 0.500, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
 # (kernel, algorithmic bytes per launch).
 MEASURED_TRAFFIC = {
-    ("gather", 2 * 512 * 64 * 32768): int((524521.7 / 0.50002 + 1048580.2 / 1.0) * 1024),
-    ("scatter", 2 * 512 * 64 * 32768): int((524342.2 / 0.50002 + 1048595.0 / 1.0) * 1024),
+    ("gather", 2 * 512 * 64 * 32768): int((524447.9 / 0.50002 + 1048579.1 / 1.0) * 1024),
+    ("scatter", 2 * 512 * 64 * 32768): int((524340.4 / 0.50002 + 1048594.9 / 1.0) * 1024),
 }
 
 WORKLOADS = {
