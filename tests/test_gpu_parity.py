@@ -189,17 +189,22 @@ def test_duplicate_destinations_last_wins(kvx, cuda, mode):
 def test_reference_known_answers_dtypes(kvx, cuda, golden):
     """The reference's e2e cases (shift copy, partial chunks, auto-allocate,
     whole-layer copy) at their block shape (128, 8, 8, 128) for fp8, bf16,
-    fp32 and int32 byte widths, on both copy paths."""
+    fp32 and int32 byte widths, on every copy path."""
     elems = 128 * 8 * 8 * 128
     for itemsize, dtype in [(1, "fp8"), (2, "bf16"), (4, "fp32"), (4, "int32")]:
-        for path in ("direct", "staged", "zero_copy"):
+        for path in ("direct", "staged", "zero_copy", "bounce", "big_blocks"):
             for case in golden["transfer_cases"]:
                 L, P, H = case["layers"], case["blocks"], case["host_blocks"]
                 rng = np.random.default_rng(101)
                 host, dev = dev_pools(rng, cuda, L, 1, P, elems * itemsize)
-                mgr = make_mgr(kvx, dev, H, **(PATHS[path] if path != "staged" else
-                                               dict(direct_min_bytes=1 << 40,
-                                                    transfer_mode="staged")))
+                kw = {"staged": dict(direct_min_bytes=1 << 40, transfer_mode="staged"),
+                      # pageable mirror: block copies and whole-layer copies
+                      # through the bounce lanes
+                      "bounce": dict(direct_min_bytes=1 << 40, host_alloc="malloc"),
+                      # blocks larger than a staging chunk: one DMA per run
+                      "big_blocks": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16,
+                                         transfer_mode="staged")}.get(path, None)
+                mgr = make_mgr(kvx, dev, H, **(kw if kw is not None else PATHS[path]))
                 print(f"{dtype} {path} {case['source']}", flush=True)
                 for op in case["ops"]:
                     if op["op"] == "d2h_auto_allocate":

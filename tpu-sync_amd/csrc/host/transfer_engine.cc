@@ -521,7 +521,9 @@ StatusOr<CopyFuture> TransferEngine::Copy(
     KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
     return CopyPageable(dir, storages, cdev, chost, {}, dep);
   }
-  if (min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) {
+  if ((min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) ||
+      max_block > opts_.staging_chunk_bytes) {
+    // Long runs, or blocks that do not fit a staging chunk: one DMA per run.
     return CopyDirect(dir, storages, src, dst, sizes, dep);
   }
   std::vector<int64_t> cdev, chost;
@@ -582,6 +584,28 @@ StatusOr<CopyFuture> TransferEngine::CopyDirect(
 StatusOr<CopyFuture> TransferEngine::CopyFull(
     Direction dir, const std::vector<StorageView>& storages,
     const std::vector<int64_t>& bytes, hipStream_t dep) {
+  bool host_ok = true;
+  for (const StorageView& s : storages) host_ok = host_ok && s.host_kernel_access;
+  if (!host_ok && opts_.host_copy_threads > 0) {
+    // Pageable host memory: each storage's leading bytes as one extent
+    // through a bounce lane, one lane copy per distinct length.
+    std::vector<CopyFuture> parts;
+    std::vector<bool> taken(storages.size(), false);
+    for (size_t w = 0; w < storages.size(); ++w) {
+      if (taken[w] || bytes[w] == 0) continue;
+      std::vector<StorageView> group;
+      for (size_t v = w; v < storages.size(); ++v) {
+        if (!taken[v] && bytes[v] == bytes[w]) {
+          group.push_back(storages[v]);
+          taken[v] = true;
+        }
+      }
+      KVX_ASSIGN_OR_RETURN(CopyFuture f,
+                           CopyPageable(dir, group, {}, {}, {ByteExtent{0, bytes[w]}}, dep));
+      parts.push_back(f);
+    }
+    return CopyFuture::Join(parts);
+  }
   std::lock_guard<std::mutex> l(mu_);
   DeviceGuard g(opts_.device);
   hipStream_t cs = dir == Direction::kD2H ? d2h_stream_ : h2d_stream_;

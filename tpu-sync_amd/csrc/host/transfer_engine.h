@@ -153,7 +153,8 @@ class TransferEngine {
                             hipStream_t dep);
 
   // Whole-buffer copy of `bytes` per storage (the reference's empty-spec
-  // full-layer copy).
+  // full-layer copy): one hipMemcpyAsync per storage, or through a bounce
+  // lane for pageable host memory.
   StatusOr<CopyFuture> CopyFull(Direction dir,
                                 const std::vector<StorageView>& storages,
                                 const std::vector<int64_t>& bytes,
