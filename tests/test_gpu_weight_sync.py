@@ -63,16 +63,19 @@ def _tensors(rng, cuda, sizes, dtype=torch.bfloat16):
     return out
 
 
-@pytest.mark.parametrize("chunk", [0, 4096, 70_000])
-def test_weight_sync_round_trip_matches_oracle(kvx, cuda, chunk):
+@pytest.mark.parametrize("chunk,host_alloc", [(0, "pinned"), (4096, "pinned"),
+                                              (70_000, "pinned"), (70_000, "malloc")])
+def test_weight_sync_round_trip_matches_oracle(kvx, cuda, chunk, host_alloc):
     """Tensors of awkward sizes (odd, sub-16-byte, multi-chunk); the host
     image must equal the oracle's pack at every tensor's offset, and h2d
-    restores the device tensors after they are overwritten."""
+    restores the device tensors after they are overwritten (pinned or
+    pageable host image)."""
     rng = np.random.default_rng(8)
     sizes = [1, 7, 16, 250, 4096, 12345, 65536, 100_003, 3, 2048]
     ts = _tensors(rng, cuda, sizes)
     originals = [u8(t).copy() for t in ts]
-    ws = kvx.WeightSynchronizer([[t] for t in ts], chunk_bytes=chunk, staging_chunks=2)
+    ws = kvx.WeightSynchronizer([[t] for t in ts], chunk_bytes=chunk, staging_chunks=2,
+                                host_alloc=host_alloc)
     want, offs = W.pack(originals)
     assert ws.total_bytes == want.size
     ws.d2h().Await()
