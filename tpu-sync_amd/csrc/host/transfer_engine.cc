@@ -227,6 +227,21 @@ struct TransferEngine::PageableLane {
   Ring ring;
   ArgRing args;
   std::unique_ptr<Bounce> bounce;
+
+  // Releases whatever was created (also after a failed set-up). The worker
+  // has been joined; the owner's device is current.
+  ~PageableLane() {
+    for (hipStream_t s : {ks, cs}) {
+      if (s != nullptr) (void)hipStreamSynchronize(s);
+    }
+    for (uint64_t b : ring.bufs) (void)hipFree(reinterpret_cast<void*>(b));
+    for (hipEvent_t e : ring.ready) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ring.free) (void)hipEventDestroy(e);
+    bounce.reset();
+    for (hipStream_t s : {ks, cs}) {
+      if (s != nullptr) (void)hipStreamDestroy(s);
+    }
+  }
 };
 
 TransferEngine::TransferEngine(const EngineOptions& opts) : opts_(opts) {}
@@ -285,18 +300,7 @@ TransferEngine::~TransferEngine() {
     lane->worker.join();
   }
   DeviceGuard g(opts_.device);
-  for (std::unique_ptr<PageableLane>& lane : lanes_) {
-    if (!lane) continue;
-    (void)hipStreamSynchronize(lane->ks);
-    (void)hipStreamSynchronize(lane->cs);
-    for (uint64_t b : lane->ring.bufs) (void)hipFree(reinterpret_cast<void*>(b));
-    for (hipEvent_t e : lane->ring.ready) (void)hipEventDestroy(e);
-    for (hipEvent_t e : lane->ring.free) (void)hipEventDestroy(e);
-    lane->bounce.reset();
-    (void)hipStreamDestroy(lane->ks);
-    (void)hipStreamDestroy(lane->cs);
-    lane.reset();
-  }
+  for (std::unique_ptr<PageableLane>& lane : lanes_) lane.reset();
   for (hipStream_t s :
        {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
     if (s != nullptr) (void)hipStreamSynchronize(s);
