@@ -47,13 +47,15 @@ def u8(a):
     return np.ascontiguousarray(a).view(np.uint8).reshape(-1)
 
 
-@pytest.mark.parametrize("mode", ["staged", "zero_copy"])
+@pytest.mark.parametrize("mode", ["staged", "zero_copy", "bounce"])
 def test_fp8_payload_and_scales_round_trip_match_oracle(kvx, oracle, cuda, mode):
+    """bounce: a pageable (malloc) mirror; payload and scales of a chunk still
+    move in one launch, through the bounce lane."""
     rng = np.random.default_rng(40)
     layers, blocks, host_blocks = 4, 96, 64
     kv_np, sc_np, kv, sc, bb = build(rng, cuda, layers, blocks)
-    mgr = kvx.KVCacheManager(kv, host_blocks_to_allocate=host_blocks, scale_tables=sc,
-                             transfer_mode=mode)
+    kw = dict(host_alloc="malloc") if mode == "bounce" else dict(transfer_mode=mode)
+    mgr = kvx.KVCacheManager(kv, host_blocks_to_allocate=host_blocks, scale_tables=sc, **kw)
     assert mgr.num_kv_layers == 2 * layers and mgr.num_layers == 3 * layers
     assert mgr.block_bytes(0) == bb and mgr.block_bytes(2 * layers) == 32
     dev = [u8(a).copy() for a in kv_np + sc_np]
