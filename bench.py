@@ -144,11 +144,18 @@ def timed_events(torch, fn, reps, stream):
 
 
 def pcie_peaks(torch, dev, nbytes=1 << 30, reps=5):
-    """Large pinned hipMemcpyAsync per direction, and both at once."""
+    """Large pinned hipMemcpyAsync per direction, and both at once, on random
+    bytes like the workload's."""
     h = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
     h2 = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
-    d = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    d2 = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    d = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev,
+                      generator=gen).view(torch.uint8)
+    d2 = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev,
+                       generator=gen).view(torch.uint8)
+    h.copy_(d)
+    h2.copy_(d2)
+    torch.cuda.synchronize()
     s1 = torch.cuda.Stream(dev)
     s2 = torch.cuda.Stream(dev)
     t_d2h = timed_events(torch, lambda: h.copy_(d, non_blocking=True), reps, s1)
