@@ -16,18 +16,11 @@ ArgRing::~ArgRing() {
     (void)hipEventSynchronize(s.done);
     (void)hipEventDestroy(s.done);
   }
-  if (upload_ != nullptr) {
-    (void)hipStreamSynchronize(upload_);
-    (void)hipStreamDestroy(upload_);
-  }
   if (host_ != nullptr) (void)hipHostFree(host_);
   if (dev_ != 0) (void)hipFree(reinterpret_cast<void*>(dev_));
 }
 
-Status ArgRing::Init(int64_t bytes) {
-  KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&upload_, hipStreamNonBlocking));
-  return Grow(bytes);
-}
+Status ArgRing::Init(int64_t bytes) { return Grow(bytes); }
 
 Status ArgRing::Grow(int64_t bytes) {
   for (Slice& s : inflight_) {
@@ -78,19 +71,9 @@ StatusOr<int64_t> ArgRing::Alloc(int64_t bytes) {
 }
 
 Status ArgRing::Upload(int64_t off, int64_t bytes, hipStream_t stream) {
-  if (upload_ == nullptr) {
-    KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(dev_ + off), host_ + off,
-                                           bytes, hipMemcpyHostToDevice, stream));
-    return OkStatus();
-  }
   KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(dev_ + off), host_ + off,
-                                         bytes, hipMemcpyHostToDevice, upload_));
-  hipEvent_t e = nullptr;
-  KVX_HIP_RETURN_IF_ERROR(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-  Status st = HipStatus(hipEventRecord(e, upload_), "hipEventRecord(upload)");
-  if (st.ok()) st = HipStatus(hipStreamWaitEvent(stream, e, 0), "hipStreamWaitEvent(upload)");
-  (void)hipEventDestroy(e);
-  return st;
+                                         bytes, hipMemcpyHostToDevice, stream));
+  return OkStatus();
 }
 
 Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {

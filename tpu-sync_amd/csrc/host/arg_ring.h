@@ -1,8 +1,9 @@
 // Pinned-host + device ring for kernel argument tables.
 //
 // A launch writes its table into the pinned half, uploads it with one
-// hipMemcpyAsync on the ring's copy stream (the launching stream waits for
-// it) and records an event after the launch; a region is handed out again only once the event that last read it
+// hipMemcpyAsync on the launching stream (no stream of its own, which would
+// take a share of the process's hardware queues) and records an event after
+// the launch; a region is handed out again only once the event that last read it
 // has completed (the host waits only when the ring wraps onto unfinished
 // work). Not thread-safe: the owner serialises calls.
 #ifndef KVX_HOST_ARG_RING_H_
@@ -32,8 +33,7 @@ class ArgRing {
   StatusOr<int64_t> Alloc(int64_t bytes);
   uint8_t* host(int64_t off) const { return host_ + off; }
   uint64_t dev(int64_t off) const { return dev_ + static_cast<uint64_t>(off); }
-  // Uploads [off, off + bytes) on the ring's own copy stream and makes
-  // `stream` wait for it, so the upload overlaps work already on `stream`.
+  // Uploads [off, off + bytes) on `stream`, ahead of the launch that reads it.
   Status Upload(int64_t off, int64_t bytes, hipStream_t stream);
   // Marks [off, off + bytes) in use until the work now enqueued on `stream`
   // finishes.
@@ -48,7 +48,6 @@ class ArgRing {
   Status Grow(int64_t bytes);
   uint8_t* host_ = nullptr;
   uint64_t dev_ = 0;
-  hipStream_t upload_ = nullptr;  // on the device current at Init
   int64_t size_ = 0;
   int64_t head_ = 0;
   std::deque<Slice> inflight_;

@@ -260,14 +260,8 @@ StatusOr<std::unique_ptr<TransferEngine>> TransferEngine::Create(
 Status TransferEngine::Init() {
   DeviceGuard g(opts_.device);
   if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
-  KVX_HIP_RETURN_IF_ERROR(
-      hipStreamCreateWithFlags(&gather_stream_, hipStreamNonBlocking));
-  KVX_HIP_RETURN_IF_ERROR(
-      hipStreamCreateWithFlags(&d2h_stream_, hipStreamNonBlocking));
-  KVX_HIP_RETURN_IF_ERROR(
-      hipStreamCreateWithFlags(&h2d_stream_, hipStreamNonBlocking));
-  KVX_HIP_RETURN_IF_ERROR(
-      hipStreamCreateWithFlags(&scatter_stream_, hipStreamNonBlocking));
+  KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueues(
+      {&gather_stream_, &d2h_stream_, &h2d_stream_, &scatter_stream_}));
   return GrowArgRing(opts_.arg_ring_bytes);
 }
 
@@ -1208,8 +1202,7 @@ StatusOr<TransferEngine::PageableLane*> TransferEngine::Lane(Direction dir) {
   if (slot) return slot.get();
   DeviceGuard g(opts_.device);
   auto lane = std::make_unique<PageableLane>();
-  KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&lane->ks, hipStreamNonBlocking));
-  KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(&lane->cs, hipStreamNonBlocking));
+  KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueues({&lane->ks, &lane->cs}));
   KVX_RETURN_IF_ERROR(lane->args.Init(1 << 20));
   // The thread that issues the lane's copies takes part in every host copy.
   lane->bounce = std::make_unique<Bounce>(opts_.host_copy_threads - 1);
