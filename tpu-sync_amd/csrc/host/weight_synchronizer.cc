@@ -67,9 +67,8 @@ Status WeightSynchronizer::Init() {
     default:
       return UnimplementedError("weight sync host memory must be pinned or malloc");
   }
-  for (hipStream_t* s : {&ks_, &d2h_, &h2d_}) {
-    KVX_HIP_RETURN_IF_ERROR(hipStreamCreateWithFlags(s, hipStreamNonBlocking));
-  }
+  // Pack kernels and the two DMA directions on different hardware queues.
+  KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueues({&ks_, &d2h_, &h2d_}));
   const int64_t chunk = std::min<int64_t>(cfg_.chunk_bytes, std::max<int64_t>(total_, 1));
   cfg_.chunk_bytes = chunk;
   for (int k = 0; k < cfg_.staging_chunks; ++k) {
