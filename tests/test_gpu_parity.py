@@ -684,3 +684,28 @@ def test_on_ready_callbacks(kvx, cuda):
     assert fired.wait(60)
     assert codes == [3]
     qm.close()
+
+
+@pytest.mark.parametrize("layers", [3, 4])
+def test_gather_scatter_every_block_of_the_pool(kvx, cuda, layers):
+    """Maximum size for a pool: all P block ids, permuted, gathered into one
+    staging buffer (storage pairs when the storage count is even, storage-
+    major when odd) and scattered back under the inverse permutation into a
+    zeroed pool: the pool must come back byte for byte."""
+    rng = np.random.default_rng(24 + layers)
+    P, bb = 512, 16384
+    host, dev = dev_pools(rng, cuda, layers, 1, P, bb)
+    mgr = make_mgr(kvx, dev, 4)
+    perm = rng.permutation(P)
+    stg = torch.empty(layers * P * bb, dtype=torch.uint8, device=cuda)
+    mgr.gather(perm.tolist(), stg).Await()
+    got = dev_np(stg).reshape(layers, P, bb)
+    for l in range(layers):
+        assert np.array_equal(got[l], host[l][0][perm]), l
+    fresh = [[torch.zeros(P, bb, dtype=torch.uint8, device=cuda)] for _ in range(layers)]
+    mgr2 = make_mgr(kvx, fresh, 4)
+    mgr2.scatter(perm.tolist(), stg).Await()
+    for l in range(layers):
+        assert np.array_equal(dev_np(fresh[l][0]), host[l][0]), l
+    mgr.close()
+    mgr2.close()
