@@ -189,6 +189,25 @@ int kvx_manager_scatter(kvx_manager* m, const int64_t* ids, int64_t n,
                         int64_t layer_idx, int64_t shard_idx, void* stream,
                         kvx_future** out);
 
+/*
+ * kvx_manager_gather with no allocation. No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under stream capture,
+ * serving loops or harnesses that forbid hipMalloc). Same ids, staging
+ * layout, restrictions, checks and bytes as kvx_manager_gather, enqueued on
+ * `stream` with no future (order later work after it on that stream). The id
+ * and storage-base tables go to a fixed per-GPU device array of
+ * (KVX_NO_ALLOC_MAX_IDS + 32 + KVX_NO_ALLOC_MAX_STORAGES) x 8 bytes
+ * (160.25 KiB) instead of the library's argument ring; larger calls are
+ * rejected with KVX_INVALID_ARGUMENT. The host ids are consumed before the
+ * call returns. Every call on one GPU shares that array: calls that overlap
+ * on one GPU (different streams or unordered threads) race.
+ */
+#define KVX_NO_ALLOC_MAX_IDS 16384
+#define KVX_NO_ALLOC_MAX_STORAGES 4096
+int kvx_manager_gather_no_alloc(kvx_manager* m, const int64_t* ids, int64_t n,
+                                uint64_t staging, int64_t staging_bytes, int32_t order,
+                                int64_t layer_idx, int64_t shard_idx, void* stream);
+
 /* Staging slots: kv_cache_manager_base.cc:1421-1466. */
 int kvx_manager_configure_host_staging_slots(kvx_manager* m, int64_t num_slots,
                                              int64_t max_major_per_slot);

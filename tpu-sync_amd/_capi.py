@@ -228,6 +228,8 @@ PROTOTYPES = {
                                   ctypes.POINTER(_vp)]),
     "kvx_manager_scatter": (_int, [_vp, _i64p, _i64, _u64, _i64, _i32, _i64, _i64, _vp,
                                    ctypes.POINTER(_vp)]),
+    "kvx_manager_gather_no_alloc": (_int, [_vp, _i64p, _i64, _u64, _i64, _i32, _i64, _i64,
+                                           _vp]),
     "kvx_manager_configure_host_staging_slots": (_int, [_vp, _i64, _i64]),
     "kvx_manager_host_span": (_int, [_vp, _i64, _i64, _i64, _i64, _u64p, _i64p, _i64p]),
     "kvx_manager_block_host_ptr": (_int, [_vp, _i64, _i64, _i32, _u64p]),

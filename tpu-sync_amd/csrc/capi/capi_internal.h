@@ -34,6 +34,12 @@ struct kvx_strings {
   std::vector<std::string> items;
 };
 
+namespace kvx {
+// Looks up this device's address of the no-alloc gather's scratch array
+// (kvx_no_alloc.hip) once per device; the device must be current.
+Status InitNoAllocScratch(int device);
+}  // namespace kvx
+
 namespace kvx_capi {
 
 int Fail(const kvx::Status& s);

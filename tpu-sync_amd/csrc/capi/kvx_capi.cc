@@ -8,6 +8,7 @@
 #include <string>
 #include <vector>
 
+#include "../host/hip_util.h"
 #include "../host/kv_cache_store.h"
 #include "../host/numa.h"
 #include "../kernels/block_copy.h"
@@ -158,8 +159,17 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
     c.engine.zero_copy_d2h_workgroups = cfg->zero_copy_workgroups;
     c.engine.zero_copy_h2d_workgroups = cfg->zero_copy_workgroups;
   }
+  const bool device_backed = cfg->device_ptrs != nullptr;
+  const int device = c.device;
   auto r = kvx::KVCacheManager::Create(std::move(c));
   if (!r.ok()) return Fail(r.status());
+  if (device_backed) {
+    // Set-up of kvx_manager_gather_no_alloc on this device.
+    kvx::DeviceGuard dg(device);
+    kvx::Status st = dg.ok() ? kvx::InitNoAllocScratch(device)
+                             : kvx::InternalError("hipSetDevice failed");
+    if (!st.ok()) return Fail(st);
+  }
   auto* m = new kvx_manager;
   m->impl = std::move(r).value();
   m->lbm_view.lbm = m->impl->host_block_manager();

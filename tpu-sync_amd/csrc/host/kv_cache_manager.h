@@ -263,6 +263,18 @@ class KVCacheManager {
   int64_t major_dim() const { return major_dim_; }
   int64_t host_blocks() const { return host_blocks_; }
   bool device_backed() const { return engine_ != nullptr; }
+  // Device base address and bytes of one (layer, shard) storage, with no
+  // allocation (false for a bad index or a CPU-only manager).
+  bool DeviceStorage(size_t layer, size_t shard, uint64_t* dev, int64_t* dev_bytes) const {
+    if (!device_backed() || layer >= static_cast<size_t>(num_layers_) ||
+        shard >= static_cast<size_t>(num_shards_)) {
+      return false;
+    }
+    const StorageInfo& si = storages_[layer * num_shards_ + shard];
+    *dev = si.dev;
+    *dev_bytes = si.dev_bytes;
+    return true;
+  }
   // True when the shared-memory host tier attached to a surviving segment.
   bool shm_warm() const { return shm_warm_; }
   int device() const { return cfg_.device; }
