@@ -53,6 +53,10 @@ extern "C" {
 #define KVX_HOST_MALLOC 0 /* posix_memalign, zeroed */
 #define KVX_HOST_PINNED 1 /* hipHostMalloc page-locked, zeroed */
 #define KVX_HOST_SHM 2    /* /dev/shm segment, survives the process */
+/* The reference's choice (CreateHostMemoryAllocator,
+ * tpu_sync/core/utils.h:48-91): KVX_HOST_SHM when shm_key or RAIDEN_SHM_KEY is
+ * non-empty, else KVX_HOST_PINNED. */
+#define KVX_HOST_AUTO 3
 
 /* Transfer modes for copies whose runs are short (with a pinned mirror,
  * runs of at least direct_min_bytes always use one hipMemcpyAsync per run):
@@ -103,9 +107,13 @@ typedef struct kvx_manager_config {
   int64_t staging_chunk_bytes;  /* device staging chunk, 0 = 64 MiB */
   int64_t staging_chunks;       /* chunks per direction, 0 = 4 */
   int64_t direct_min_bytes;     /* min run bytes for a copy without staging, 0 = 4 MiB */
-  const char* shm_key;          /* KVX_HOST_SHM: segment key */
-  const char* shm_server_name;  /* KVX_HOST_SHM: optional server name */
-  const char* model_uid;        /* KVX_HOST_SHM: schema check on warm boot */
+  /* Shared-memory tier naming; NULL (or "" for shm_key) takes the reference's
+   * environment defaults (tpu_sync/core/utils.h:48-91,
+   * tpu_sync/core/host_memory_allocator.cc:267-271). */
+  const char* shm_key;          /* segment key; default RAIDEN_SHM_KEY */
+  const char* shm_server_name;  /* segment suffix; default RAIDEN_SHM_SERVER_NAME */
+  const char* model_uid;        /* schema check on warm boot; default
+                                   RAIDEN_SHM_MODEL_UID, else "default_model" */
   int32_t profile_kernels;      /* 1: time every kernel launch with HIP events */
   int32_t transfer_mode;        /* KVX_MODE_*: how short runs cross PCIe */
   int64_t zero_copy_workgroups; /* workgroup cap of a zero-copy launch in both
@@ -336,6 +344,10 @@ int32_t kvx_block_manager_num_locked(kvx_block_manager* b);
 int kvx_manager_register_with_controller(kvx_manager* m, const char* address);
 /* 1 when the shared-memory host tier attached to a surviving segment. */
 int32_t kvx_manager_shm_warm(const kvx_manager* m);
+/* The host memory kind the manager's mirror uses (KVX_HOST_MALLOC, _PINNED or
+ * _SHM), after KVX_HOST_AUTO was resolved as CreateHostMemoryAllocator does
+ * (tpu_sync/core/utils.h:48-91). */
+int32_t kvx_manager_host_alloc(const kvx_manager* m);
 
 /* ---------------------------------------------------------------------------
  * Host tier: KV store (local flows), LRU index and metadata table.
@@ -382,8 +394,11 @@ typedef struct kvx_store_config {
   int64_t shard_size_bytes;
   const char* store_server_ip;  /* required, not a wildcard */
   int32_t raiden_controller_port; /* 0: pick an unused in-process address */
-  const char* metadata_shm_key; /* crash-persistent table; NULL or "": none */
-  const char* model_uid;        /* NULL: "default_model" */
+  /* Crash-persistent metadata table: NULL takes the reference's default
+   * "<RAIDEN_SHM_KEY>_metadata[_<RAIDEN_SHM_SERVER_NAME>]" (none when
+   * RAIDEN_SHM_KEY is unset; kv_cache_store_wrapper.cc:46-58), "" means none. */
+  const char* metadata_shm_key;
+  const char* model_uid;        /* NULL: RAIDEN_SHM_MODEL_UID, else "default_model" */
   int32_t no_auto_recover;      /* 1: do not recover from a surviving table
                                    at creation (call ..._recover_... later) */
   int64_t host_blocks;          /* controller host blocks; 0 = capacity */

@@ -1,10 +1,15 @@
 /* A plain C11 client of the C-ABI (include/kvx.h), built and run by
  * tests/test_c_client.py on the CPU: a host-only manager's block accessors
  * and pool table, copy specs, the block allocator and the wire framing, with
- * the reference's known answers. Exits non-zero at the first mismatch. */
+ * the reference's known answers, and the RAIDEN_SHM_* environment defaults
+ * applied inside the library (a manager and a store that name no segment).
+ * Exits non-zero at the first mismatch. */
+#define _POSIX_C_SOURCE 200809L /* setenv, getpid, unlink */
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include "kvx.h"
 
@@ -88,6 +93,62 @@ int main(void) {
   EXPECT(kvx_block_manager_allocate(b, 3, 1, got) == KVX_OK);
   EXPECT(got[0] == 0 && got[1] == 1 && got[2] == 2);
   kvx_block_manager_destroy(b);
+
+  /* RAIDEN_SHM_*: a manager asking for the reference's default allocator
+   * (KVX_HOST_AUTO) and naming no segment gets the shm tier under
+   * RAIDEN_SHM_KEY, warm on its second creation; a store naming no metadata
+   * table gets "<key>_metadata". */
+  char key[64], path[96], meta[96];
+  snprintf(key, sizeof(key), "kvx_c_env_%d", (int)getpid());
+  snprintf(path, sizeof(path), "/dev/shm/%s", key);
+  snprintf(meta, sizeof(meta), "/dev/shm/%s_metadata", key);
+  EXPECT(setenv("RAIDEN_SHM_KEY", key, 1) == 0);
+  EXPECT(setenv("RAIDEN_SHM_MODEL_UID", "c_client_model", 1) == 0);
+  kvx_manager_config ec;
+  memset(&ec, 0, sizeof(ec));
+  ec.host_alloc = KVX_HOST_AUTO;
+  ec.num_layers = 2;
+  ec.num_shards = 1;
+  ec.slice_byte_size = 128;
+  ec.host_blocks = 4;
+  kvx_manager* e1 = NULL;
+  EXPECT(kvx_manager_create(&ec, &e1) == KVX_OK);
+  EXPECT(kvx_manager_host_alloc(e1) == KVX_HOST_SHM);
+  EXPECT(kvx_manager_shm_warm(e1) == 0);
+  EXPECT(access(path, F_OK) == 0);
+  EXPECT(kvx_manager_write_block(e1, 1, 3, 0, payload, sizeof(payload)) == KVX_OK);
+  kvx_manager_destroy(e1);
+  kvx_manager* e2 = NULL;
+  EXPECT(kvx_manager_create(&ec, &e2) == KVX_OK);
+  EXPECT(kvx_manager_shm_warm(e2) == 1);
+  EXPECT(kvx_manager_read_block(e2, 1, 3, 0, back, sizeof(back)) == KVX_OK);
+  EXPECT(memcmp(back, payload, sizeof(back)) == 0);
+  kvx_manager_destroy(e2);
+  /* Another schema uid: the segment is reformatted (cold). */
+  EXPECT(setenv("RAIDEN_SHM_MODEL_UID", "other_model", 1) == 0);
+  kvx_manager* e3 = NULL;
+  EXPECT(kvx_manager_create(&ec, &e3) == KVX_OK);
+  EXPECT(kvx_manager_shm_warm(e3) == 0);
+  kvx_manager_destroy(e3);
+
+  kvx_store_config sc;
+  memset(&sc, 0, sizeof(sc));
+  sc.capacity = 4;
+  sc.job_name = "job";
+  sc.job_replica_id = "0";
+  sc.data_name = "cache";
+  sc.num_shards = 1;
+  sc.store_server_ip = "127.0.0.1";
+  kvx_store* st = NULL;
+  EXPECT(kvx_store_create(&sc, &st) == KVX_OK);
+  EXPECT(access(meta, F_OK) == 0);
+  kvx_store_destroy(st);
+  unlink(path);
+  unlink(meta);
+  EXPECT(unsetenv("RAIDEN_SHM_KEY") == 0);
+  /* shm without a key anywhere is refused. */
+  ec.host_alloc = KVX_HOST_SHM;
+  EXPECT(kvx_manager_create(&ec, &e1) == KVX_INVALID_ARGUMENT);
   puts("c client ok");
   return 0;
 }

@@ -1,0 +1,92 @@
+"""The Python boundary checks every tensor it hands to a kernel before any
+library call: a tensor off the HIP device, on another device than the
+manager, non-contiguous or expanded, or spanning more bytes than its storage
+is rejected with ValueError; a column split also needs a contiguous 2-D
+weight and outputs of the weight's dtype. Tensors that claim to be on a
+device are CPU tensors behind a wrapper: the checks run on the host only."""
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from fake_device import FakeDeviceTensor  # noqa: E402
+
+
+
+class ShortStorage(FakeDeviceTensor):
+    def untyped_storage(self):
+        class S:
+            def nbytes(self):
+                return 8
+        return S()
+
+
+def test_device_buffer_accepts_a_contiguous_device_tensor(kvx):
+    t = torch.empty(16, dtype=torch.float32)[4:]
+    ptr, nbytes = kvx._capi.device_buffer(FakeDeviceTensor(t), "x", 0)
+    assert ptr == t.data_ptr() and nbytes == 48
+
+
+@pytest.mark.parametrize("make,msg", [
+    (lambda: torch.empty(4), "HIP device"),
+    (lambda: FakeDeviceTensor(torch.empty(4), index=1), "device 1"),
+    (lambda: FakeDeviceTensor(torch.empty(1).expand(4096)), "contiguous"),
+    (lambda: FakeDeviceTensor(torch.empty(8, 8).t()), "contiguous"),
+    (lambda: ShortStorage(torch.empty(64, dtype=torch.uint8)), "storage holds 8"),
+])
+def test_device_buffer_rejects(kvx, make, msg):
+    with pytest.raises(ValueError, match=msg):
+        kvx._capi.device_buffer(make(), "x", 0)
+
+
+def test_manager_rejects_host_and_mixed_device_pools(kvx):
+    with pytest.raises(ValueError, match="HIP device"):
+        kvx.KVCacheManager([torch.zeros(8, 64)], host_blocks_to_allocate=2)
+    pools = [FakeDeviceTensor(torch.zeros(8, 64)), FakeDeviceTensor(torch.zeros(8, 64), 1)]
+    with pytest.raises(ValueError, match="device 1"):
+        kvx.KVCacheManager(pools, host_blocks_to_allocate=2)
+
+
+def test_gather_and_scatter_reject_host_staging(kvx):
+    mgr = kvx.KVCacheManager.create_host_only_for_testing(
+        num_layers=2, slice_byte_size=64, host_blocks=4)
+    for fn in (mgr.gather, mgr.scatter):
+        with pytest.raises(ValueError, match="HIP device"):
+            fn([0, 1], torch.empty(256, dtype=torch.uint8), stream=0)
+        with pytest.raises(ValueError, match="contiguous"):
+            fn([0], FakeDeviceTensor(torch.empty(1, dtype=torch.uint8).expand(256)), stream=0)
+    mgr.close()
+
+
+def test_column_split_entries_checks_weight_and_outputs(kvx):
+    ws = kvx.weight_synchronizer
+    w = torch.zeros(4, 8, dtype=torch.bfloat16)
+    outs = [FakeDeviceTensor(torch.zeros(4, 4, dtype=torch.bfloat16)) for _ in range(2)]
+    with pytest.raises(ValueError, match="HIP device"):
+        ws.column_split_entries(w, outs)
+    with pytest.raises(ValueError, match="contiguous"):
+        ws.column_split_entries(FakeDeviceTensor(torch.zeros(8, 4, dtype=torch.bfloat16).t()),
+                                outs)
+    with pytest.raises(ValueError, match="dtype"):
+        ws.column_split_entries(FakeDeviceTensor(w),
+                                [FakeDeviceTensor(torch.zeros(4, 4, dtype=torch.float32))] * 2)
+    with pytest.raises(ValueError, match="device 1"):
+        ws.column_split_entries(FakeDeviceTensor(w),
+                                [outs[0], FakeDeviceTensor(torch.zeros(4, 4, dtype=torch.bfloat16), 1)])
+    with pytest.raises(ValueError, match="2-D"):
+        ws.column_split_entries(FakeDeviceTensor(torch.zeros(8, dtype=torch.bfloat16)), outs)
+    entries = ws.column_split_entries(FakeDeviceTensor(w), outs)
+    assert [e.as_tuple() for e in entries] == [
+        (w.data_ptr(), outs[0].data_ptr(), 8, 4, 16, 8),
+        (w.data_ptr() + 8, outs[1].data_ptr(), 8, 4, 16, 8)]
+
+
+def test_weight_synchronizer_rejects_host_tensors_and_staging(kvx):
+    with pytest.raises(ValueError, match="HIP device"):
+        kvx.WeightSynchronizer([[torch.zeros(16)]])
+    ws = kvx.WeightSynchronizer.__new__(kvx.WeightSynchronizer)
+    ws._device = 0
+    for fn in (ws.pack, ws.unpack):
+        with pytest.raises(ValueError, match="HIP device"):
+            fn(torch.empty(64, dtype=torch.uint8), stream=0)
+        with pytest.raises(ValueError, match="device 1"):
+            fn(FakeDeviceTensor(torch.empty(64, dtype=torch.uint8), 1), stream=0)

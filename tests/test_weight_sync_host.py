@@ -4,6 +4,7 @@ shard-slice math against known answers, and the product's entry builders
 import numpy as np
 import pytest
 
+from fake_device import FakeDeviceTensor
 from oracle import weight_sync as W
 
 
@@ -27,6 +28,22 @@ def test_nd_shard_slices_known_answers():
         W.nd_shard_slices((4,), (1, 1))
 
 
+def test_nd_shard_slices_reference_goldens(kvx):
+    """The reference's own goldens (nd_slice_math_test.py:70-100), for the
+    oracle and the product."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "nd_slice_cases.json")
+    with open(path) as f:
+        cases = json.load(f)["cases"]
+    assert len(cases) == 2
+    for c in cases:
+        want = [[tuple(d) for d in shard] for shard in c["bounds"]]
+        shape, mesh = tuple(c["global_shape"]), tuple(c["mesh_shape"])
+        assert [[tuple(d) for d in s] for s in W.nd_shard_slices(shape, mesh)] == want
+        assert [[tuple(d) for d in s] for s in kvx.compute_nd_shard_slices(shape, mesh)] == want
+
+
 def test_product_shard_slices_match_oracle(kvx):
     rng = np.random.default_rng(0)
     for _ in range(200):
@@ -45,7 +62,8 @@ def test_column_split_entries_equal_numpy_slicing(kvx):
         w = torch.from_numpy(rng.integers(-30000, 30000, (rows, cols), dtype=np.int16))
         bounds = W.nd_shard_slices((rows, cols), (1, k))
         outs = [torch.zeros(rows, b[1][1] - b[1][0], dtype=torch.int16) for b in bounds]
-        entries = {e.dst: e for e in kvx.column_split_entries(w, outs)}
+        entries = {e.dst: e for e in kvx.column_split_entries(
+            FakeDeviceTensor(w), [FakeDeviceTensor(o) for o in outs])}
         # Execute the entries with the oracle on the host bytes: every output
         # must equal the numpy column slice (empty chunks have no entry).
         src = w.numpy().view(np.uint8).reshape(-1)

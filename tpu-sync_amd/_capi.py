@@ -19,7 +19,7 @@ STATUS_NAMES = {
     14: "UNAVAILABLE", 15: "DATA_LOSS",
 }
 
-HOST_MALLOC, HOST_PINNED, HOST_SHM = 0, 1, 2
+HOST_MALLOC, HOST_PINNED, HOST_SHM, HOST_AUTO = 0, 1, 2, 3
 MODES = {"auto": 0, "staged": 1, "zero_copy": 2}
 LAYER_MAJOR, BLOCK_MAJOR = 0, 1
 
@@ -273,6 +273,7 @@ PROTOTYPES = {
     "kvx_gather_blocks": (_int, [_u64, _i64, _i64, _i64, _u64, _i64, _u64, _i32, _u64, _vp]),
     "kvx_scatter_blocks": (_int, [_u64, _i64, _i64, _i64, _u64, _i64, _u64, _i32, _u64, _vp]),
     "kvx_manager_register_with_controller": (_int, [_vp, ctypes.c_char_p]),
+    "kvx_manager_host_alloc": (_i32, [_vp]),
     "kvx_manager_shm_warm": (_i32, [_vp]),
     # host tier
     "kvx_strings_count": (_i64, [_vp]),
@@ -441,6 +442,26 @@ def load():
 
 def last_error():
     return load().kvx_last_error().decode(errors="replace")
+
+
+def device_buffer(t, what, device=None):
+    """(data_ptr, nbytes) of a tensor handed to a kernel, checked before any
+    launch. A tensor that is not on a HIP device, is on another device than
+    ``device``, is not contiguous (an expanded or strided view), or claims
+    more bytes than its storage holds past its offset raises ValueError:
+    the kernels address numel * element_size bytes from data_ptr."""
+    if not getattr(t, "is_cuda", False):
+        raise ValueError(f"{what} must be a tensor on a HIP device, got {getattr(t, 'device', t)}")
+    index = t.device.index if t.device.index is not None else 0
+    if device is not None and index != device:
+        raise ValueError(f"{what} is on device {index}, expected device {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    nbytes = t.numel() * t.element_size()
+    held = t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()
+    if nbytes > held:
+        raise ValueError(f"{what} spans {nbytes} bytes but its storage holds {held}")
+    return t.data_ptr(), nbytes
 
 
 def check(code, where=""):

@@ -11,6 +11,7 @@
 #include "../host/hip_util.h"
 #include "../host/kv_cache_store.h"
 #include "../host/numa.h"
+#include "../host/raiden_env.h"
 #include "../kernels/block_copy.h"
 #include "capi_internal.h"
 
@@ -104,13 +105,25 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   c.major_dim = cfg->major_dim;
   c.slice_byte_size = cfg->slice_byte_size;
   c.host_blocks = cfg->host_blocks;
-  if (cfg->host_alloc < 0 || cfg->host_alloc > 2) {
+  if (cfg->host_alloc < KVX_HOST_MALLOC || cfg->host_alloc > KVX_HOST_AUTO) {
     return Fail(KVX_INVALID_ARGUMENT, "unknown host_alloc kind");
   }
-  c.host_alloc = static_cast<kvx::HostAllocKind>(cfg->host_alloc);
-  if (cfg->shm_key) c.shm_key = cfg->shm_key;
-  if (cfg->shm_server_name) c.shm_server_name = cfg->shm_server_name;
-  if (cfg->model_uid) c.model_uid = cfg->model_uid;
+  // The reference picks the shared-memory allocator, its key and schema uid
+  // from RAIDEN_SHM_* (tpu_sync/core/utils.h:48-91); fields left NULL here
+  // take those defaults.
+  const std::string key = cfg->shm_key != nullptr ? cfg->shm_key : "";
+  int32_t kind = cfg->host_alloc;
+  if (kind == KVX_HOST_AUTO) {
+    kind = !key.empty() || !kvx::ShmKeyFromEnv().empty() ? KVX_HOST_SHM : KVX_HOST_PINNED;
+  }
+  c.host_alloc = static_cast<kvx::HostAllocKind>(kind);
+  if (kind == KVX_HOST_SHM) {
+    c.shm_key = !key.empty() ? key : kvx::ShmKeyFromEnv();
+    c.shm_server_name = cfg->shm_server_name != nullptr ? std::string(cfg->shm_server_name)
+                                                        : kvx::ShmServerNameFromEnv();
+    c.model_uid = cfg->model_uid != nullptr ? std::string(cfg->model_uid)
+                                            : kvx::ShmModelUidFromEnv();
+  }
   if (cfg->staging_chunk_bytes > 0) c.engine.staging_chunk_bytes = cfg->staging_chunk_bytes;
   if (cfg->staging_chunks > 0) c.engine.staging_chunks = static_cast<int>(cfg->staging_chunks);
   if (cfg->direct_min_bytes > 0) c.engine.direct_min_bytes = cfg->direct_min_bytes;
@@ -118,7 +131,7 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   if (cfg->transfer_mode < KVX_MODE_AUTO || cfg->transfer_mode > KVX_MODE_ZERO_COPY) {
     return Fail(KVX_INVALID_ARGUMENT, "unknown transfer_mode");
   }
-  if (cfg->transfer_mode == KVX_MODE_ZERO_COPY && cfg->host_alloc != KVX_HOST_PINNED) {
+  if (cfg->transfer_mode == KVX_MODE_ZERO_COPY && kind != KVX_HOST_PINNED) {
     return Fail(KVX_INVALID_ARGUMENT, "zero-copy transfers need KVX_HOST_PINNED host memory");
   }
   c.engine.mode = static_cast<kvx::TransferMode>(cfg->transfer_mode);
@@ -193,6 +206,10 @@ int kvx_manager_register_with_controller(kvx_manager* m, const char* address) {
 
 int32_t kvx_manager_shm_warm(const kvx_manager* m) {
   return m != nullptr && m->impl->shm_warm() ? 1 : 0;
+}
+
+int32_t kvx_manager_host_alloc(const kvx_manager* m) {
+  return m == nullptr ? -1 : static_cast<int32_t>(m->impl->host_alloc());
 }
 
 int32_t kvx_manager_numa_node(const kvx_manager* m) {
@@ -620,7 +637,9 @@ static int RawCopy(bool gather, uint64_t storage_table, int64_t num_storages,
   if (order != KVX_LAYER_MAJOR && order != KVX_BLOCK_MAJOR) {
     return Fail(KVX_INVALID_ARGUMENT, "unknown staging order");
   }
-  if (num_storages * n > UINT32_MAX || n > INT32_MAX) {
+  // Bounds first, then the product as a division: no signed overflow.
+  if (n > INT32_MAX || num_storages > static_cast<int64_t>(UINT32_MAX) ||
+      static_cast<uint64_t>(num_storages) > UINT32_MAX / static_cast<uint64_t>(n)) {
     return Fail(KVX_INVALID_ARGUMENT, "too many blocks for one launch");
   }
   kvx::CopyLaunch l;

@@ -8,6 +8,7 @@
 #include "../host/kv_cache_metadata.h"
 #include "../host/kv_cache_store.h"
 #include "../host/lru_cache.h"
+#include "../host/raiden_env.h"
 #include "capi_internal.h"
 
 struct kvx_store {
@@ -144,8 +145,13 @@ int kvx_store_create(const kvx_store_config* cfg, kvx_store** out) {
   o.shard_size_bytes = cfg->shard_size_bytes;
   o.store_server_ip = Str(cfg->store_server_ip);
   o.raiden_controller_port = cfg->raiden_controller_port;
-  o.metadata_shm_key = Str(cfg->metadata_shm_key);
-  if (cfg->model_uid != nullptr) o.model_uid = cfg->model_uid;
+  // NULL fields take the reference's RAIDEN_SHM_* defaults
+  // (tpu_sync/kv_cache/kv_cache_store_wrapper.cc:46-58, 116-123); an empty
+  // metadata key disables the table.
+  o.metadata_shm_key = cfg->metadata_shm_key != nullptr ? std::string(cfg->metadata_shm_key)
+                                                        : kvx::MetadataShmKeyFromEnv();
+  o.model_uid = cfg->model_uid != nullptr ? std::string(cfg->model_uid)
+                                          : kvx::ShmModelUidFromEnv();
   o.recover_at_create = cfg->no_auto_recover == 0;
   if (cfg->host_blocks < 0) return Fail(KVX_INVALID_ARGUMENT, "host_blocks must be non-negative");
   o.host_blocks = static_cast<size_t>(cfg->host_blocks);

@@ -100,6 +100,8 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
   const int64_t tbytes = static_cast<int64_t>(table.size() * sizeof(StridedEntryDev));
   const int64_t bytes = tbytes + static_cast<int64_t>(grid) * 4;
   KVX_ASSIGN_OR_RETURN(int64_t off, ring.Alloc(bytes));
+  ArgSliceGuard keep([&ring, off, bytes, stream] { return ring.Commit(off, bytes, stream); },
+                     stream);
   std::memcpy(ring.host(off), table.data(), static_cast<size_t>(tbytes));
   uint32_t* map = reinterpret_cast<uint32_t*>(ring.host(off) + tbytes);
   for (size_t e = 0; e < table.size(); ++e) {
@@ -110,7 +112,7 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
   KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
       reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
       static_cast<uint32_t>(table.size()), grid, vec, stream, max_workgroups));
-  return ring.Commit(off, bytes, stream);
+  return keep.Commit();
 }
 
 }  // namespace kvx

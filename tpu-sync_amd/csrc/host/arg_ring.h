@@ -13,6 +13,7 @@
 
 #include <cstdint>
 #include <deque>
+#include <functional>
 #include <vector>
 
 #include "../kernels/strided_copy.h"
@@ -51,6 +52,35 @@ class ArgRing {
   int64_t size_ = 0;
   int64_t head_ = 0;
   std::deque<Slice> inflight_;
+};
+
+// Keeps an argument-table slice reserved on every return path. A slice whose
+// upload has been queued may be read by that upload and by the launches
+// after it, so it must be committed (its completion event recorded on the
+// launching stream) even when a later step fails: Commit() does it on the
+// success path, the destructor on an early return. If recording the event
+// fails, the stream is drained instead, so nothing in flight can still read
+// the slice when the ring hands it out again.
+class ArgSliceGuard {
+ public:
+  ArgSliceGuard(std::function<Status()> commit, hipStream_t stream)
+      : commit_(std::move(commit)), stream_(stream) {}
+  ~ArgSliceGuard() {
+    if (!done_) (void)Commit();
+  }
+  ArgSliceGuard(const ArgSliceGuard&) = delete;
+  ArgSliceGuard& operator=(const ArgSliceGuard&) = delete;
+  Status Commit() {
+    done_ = true;
+    Status st = commit_();
+    if (!st.ok()) (void)hipStreamSynchronize(stream_);
+    return st;
+  }
+
+ private:
+  std::function<Status()> commit_;
+  hipStream_t stream_;
+  bool done_ = false;
 };
 
 // Uploads the table and tile map of `copies` through `ring` and launches the

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstdlib>
 #include <initializer_list>
 #include <string>
 #include <vector>
@@ -45,7 +46,17 @@ class DeviceGuard {
   bool restore_ = false;
 };
 
-// Creates non-blocking streams that land on distinct hardware queues.
+// Hardware queues per process the HIP runtime uses: GPU_MAX_HW_QUEUES, or
+// its default of 4.
+inline int HwQueuesPerProcess() {
+  const char* v = std::getenv("GPU_MAX_HW_QUEUES");
+  const int n = v != nullptr ? std::atoi(v) : 0;
+  return n >= 1 && n <= 64 ? n : 4;
+}
+
+// Creates non-blocking streams meant to land on distinct hardware queues
+// (best effort: the placement rests on the runtime's observed policy, not on
+// a documented guarantee).
 //
 // The HIP runtime backs a process's streams with at most GPU_MAX_HW_QUEUES
 // hardware queues (4 by default): the first streams get new queues, later
@@ -54,11 +65,13 @@ class DeviceGuard {
 // when the pool fills between them, and streams on one queue run in order:
 // an offload's DMA and a reload's DMA on one queue serialize (measured:
 // offload+reload of Llama-3-8B batches at 54 instead of 96 GB/s when one
-// stream existed before the engine's). Four short-lived spacer streams
-// created first fill the pool and even out the counts, so the streams
-// created next each join a different queue.
+// stream existed before the engine's). One short-lived spacer stream per
+// hardware queue, created first, fills the pool and evens out counts that
+// differ by at most one, so the streams created next each join a different
+// queue. Counts that differ by more (many streams created elsewhere on one
+// queue) can still put two of them on one queue.
 inline Status CreateStreamsOnDistinctQueues(std::initializer_list<hipStream_t*> out) {
-  std::vector<hipStream_t> spacers(4, nullptr);
+  std::vector<hipStream_t> spacers(static_cast<size_t>(HwQueuesPerProcess()), nullptr);
   Status st = OkStatus();
   for (hipStream_t& s : spacers) {
     if (st.ok()) st = HipStatus(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "spacer stream");

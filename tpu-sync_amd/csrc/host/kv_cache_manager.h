@@ -277,6 +277,7 @@ class KVCacheManager {
   }
   // True when the shared-memory host tier attached to a surviving segment.
   bool shm_warm() const { return shm_warm_; }
+  HostAllocKind host_alloc() const { return cfg_.host_alloc; }
   int device() const { return cfg_.device; }
   // The NUMA node host mirrors were placed on (the reference's
   // assigned_numa_node), or -1.

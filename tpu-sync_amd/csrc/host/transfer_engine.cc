@@ -781,6 +781,8 @@ StatusOr<CopyFuture> TransferEngine::CopyZeroCopy(
     arg_bytes += 2 * tb;
   }
   KVX_ASSIGN_OR_RETURN(int64_t aoff, ArgAlloc(arg_bytes));
+  ArgSliceGuard keep([this, aoff, arg_bytes, ks] { return ArgCommit(aoff, aoff + arg_bytes, ks); },
+                     ks);
   const int64_t ids2_off = AlignUp(n * 8, kArgAlign);
   std::memcpy(arg_host_ + aoff, cdev.data(), n * 8);
   std::memcpy(arg_host_ + aoff + ids2_off, chost.data(), n * 8);
@@ -822,7 +824,7 @@ StatusOr<CopyFuture> TransferEngine::CopyZeroCopy(
     const int vec = LaunchVectorBytes(cl, acc);
     KVX_RETURN_IF_ERROR(LaunchCopy(cl, d2h, vec, ks));
   }
-  KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, ks));
+  KVX_RETURN_IF_ERROR(keep.Commit());
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, ks));
   ++stats_.zero_copy_copies;
@@ -986,6 +988,12 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
     arg_host = arg_host_ + aoff;
     arg_dev = arg_dev_ + aoff;
   }
+  ArgSliceGuard keep(
+      [this, &lane, aoff, arg_bytes, ks] {
+        return lane.args != nullptr ? lane.args->Commit(aoff, arg_bytes, ks)
+                                    : ArgCommit(aoff, aoff + arg_bytes, ks);
+      },
+      ks);
   std::memcpy(arg_host, cdev.data(), n * 8);
   uint64_t align_acc = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
@@ -1103,14 +1111,13 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
   KVX_RETURN_IF_ERROR(PipelineChunks(lane, dir, chunks, &memcpys));
 
   const int64_t nchunks = static_cast<int64_t>(chunks.size());
+  KVX_RETURN_IF_ERROR(keep.Commit());
   if (lane.args != nullptr) {
-    KVX_RETURN_IF_ERROR(lane.args->Commit(aoff, arg_bytes, ks));
     std::lock_guard<std::mutex> l(mu_);
     stats_.memcpy_calls += memcpys;
     stats_.chunks += nchunks;
     stats_.kernel_launches += launches;
   } else {
-    KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, ks));
     stats_.memcpy_calls += memcpys;
     stats_.chunks += nchunks;
   }
@@ -1344,6 +1351,9 @@ StatusOr<CopyFuture> TransferEngine::DeviceCopy(
     arg_bytes += AlignUp(static_cast<int64_t>(groups[gi].members.size()) * 8, kArgAlign);
   }
   KVX_ASSIGN_OR_RETURN(int64_t aoff, ArgAlloc(arg_bytes));
+  ArgSliceGuard keep(
+      [this, aoff, arg_bytes, stream] { return ArgCommit(aoff, aoff + arg_bytes, stream); },
+      stream);
   std::memcpy(arg_host_ + aoff, ids.data(), n * 8);
   uint64_t acc = staging;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
@@ -1380,7 +1390,7 @@ StatusOr<CopyFuture> TransferEngine::DeviceCopy(
     const int vec = LaunchVectorBytes(cl, acc);
     KVX_RETURN_IF_ERROR(LaunchCopy(cl, gather, vec, stream));
   }
-  KVX_RETURN_IF_ERROR(ArgCommit(aoff, aoff + arg_bytes, stream));
+  KVX_RETURN_IF_ERROR(keep.Commit());
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
   return CopyFuture::FromEvents({done}, {});

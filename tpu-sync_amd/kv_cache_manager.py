@@ -86,20 +86,6 @@ def _stream_ptr(stream) -> int:
     return int(getattr(stream, "cuda_stream", stream))
 
 
-def _host_tier_from_env(host_alloc, shm_key, shm_server_name, model_uid):
-    """Host memory kind and shm naming, defaulting from RAIDEN_SHM_* like the
-    reference (tpu_sync/core/utils.h:48-91)."""
-    import os
-    env_key = os.environ.get("RAIDEN_SHM_KEY", "")
-    if host_alloc is None:
-        host_alloc = "shm" if (shm_key or env_key) else "pinned"
-    if host_alloc == "shm":
-        shm_key = shm_key or env_key
-        model_uid = model_uid or os.environ.get("RAIDEN_SHM_MODEL_UID") or "default_model"
-        shm_server_name = shm_server_name or os.environ.get("RAIDEN_SHM_SERVER_NAME") or None
-    return host_alloc, shm_key, shm_server_name, model_uid
-
-
 def _flatten_caches(kv_caches) -> Tuple[List[List[Any]], int]:
     layers = []
     for entry in kv_caches:
@@ -185,11 +171,11 @@ class KVCacheManager:
       host_blocks_to_allocate: host mirror blocks per (layer, shard).
       max_blocks / num_slots: alternatively, a staging-slot layout; the host
         mirror then holds max_blocks * num_slots blocks.
-      host_alloc: "pinned" (hipHostMalloc), "malloc" or "shm". Default:
-        "shm" when RAIDEN_SHM_KEY is set (segment key; model uid from
-        RAIDEN_SHM_MODEL_UID, server name from RAIDEN_SHM_SERVER_NAME, as the
-        reference's CreateHostMemoryAllocator reads them,
-        tpu_sync/core/utils.h:48-91), else "pinned".
+      host_alloc: "pinned" (hipHostMalloc), "malloc" or "shm". Default (None):
+        the library chooses "shm" when shm_key or RAIDEN_SHM_KEY is set, else
+        "pinned"; shm names left None take RAIDEN_SHM_KEY, RAIDEN_SHM_MODEL_UID
+        and RAIDEN_SHM_SERVER_NAME, as the reference's CreateHostMemoryAllocator
+        reads them (tpu_sync/core/utils.h:48-91).
       raiden_controller_address: joins the KVCacheStore whose controller
         has this address (in this process) as its transfer worker.
       scale_tables: per-layer side tables with the same major dimension (for
@@ -242,19 +228,23 @@ class KVCacheManager:
         layers, num_shards = _flatten_caches(kv_caches)
         ptrs, sizes = [], []
         major_dim = 0
-        device = 0
+        device = None
         for shards in layers:
             for t in shards:
-                if not t.is_contiguous():
+                if getattr(t, "is_cuda", False) and not t.is_contiguous():
                     raise RuntimeError("kv cache tensors must be contiguous")
-                ptrs.append(t.data_ptr())
-                sizes.append(t.numel() * t.element_size())
-                device = t.device.index or 0
+                if device is None and getattr(t, "is_cuda", False):
+                    device = t.device.index or 0
+                ptr, nbytes = _capi.device_buffer(t, "kv cache tensor", device)
+                ptrs.append(ptr)
+                sizes.append(nbytes)
+        device = device or 0
+        self._device = device
         if layers:
             major_dim = int(layers[0][0].shape[0])
         self._tensors = layers  # borrowed device buffers stay alive
-        host_alloc, shm_key, shm_server_name, model_uid = _host_tier_from_env(
-            host_alloc, shm_key, shm_server_name, model_uid)
+        # host_alloc None: the library picks shm when shm_key or RAIDEN_SHM_KEY
+        # is set, else pinned; unset shm names take RAIDEN_SHM_* there.
         self._init(device, len(layers), num_shards, ptrs, sizes, major_dim, 0,
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
@@ -287,6 +277,13 @@ class KVCacheManager:
         return int(_capi.load().kvx_manager_numa_node(self._h))
 
     @property
+    def host_alloc(self) -> str:
+        """The host mirror's memory kind: "malloc", "pinned" or "shm"."""
+        kind = _capi.load().kvx_manager_host_alloc(self._h)
+        return {_capi.HOST_MALLOC: "malloc", _capi.HOST_PINNED: "pinned",
+                _capi.HOST_SHM: "shm"}[kind]
+
+    @property
     def shm_warm(self) -> bool:
         """True when the shared-memory host tier attached to a surviving segment."""
         return bool(_capi.load().kvx_manager_shm_warm(self._h))
@@ -298,7 +295,7 @@ class KVCacheManager:
               numa="auto", dispatch="env", host_copy_threads=0):
         lib = _capi.load()
         kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
-                 "shm": _capi.HOST_SHM}
+                 "shm": _capi.HOST_SHM, None: _capi.HOST_AUTO}
         cfg = _capi.ManagerConfig()
         cfg.device = device
         cfg.host_alloc = kinds[host_alloc]
@@ -347,8 +344,7 @@ class KVCacheManager:
         shared-memory segment named by shm_key or RAIDEN_SHM_KEY)."""
         obj = cls.__new__(cls)
         obj._tensors = []
-        host_alloc, shm_key, shm_server_name, model_uid = _host_tier_from_env(
-            host_alloc, shm_key, shm_server_name, model_uid)
+        obj._device = None  # no device: gather/scatter fail in the library
         obj._init(0, num_layers, num_shards, [], [], 0, slice_byte_size, host_blocks,
                   host_alloc, 0, 0, 0, shm_key, shm_server_name, model_uid)
         obj.node_id = node_id
@@ -419,13 +415,13 @@ class KVCacheManager:
 
     def _device_copy(self, fn, where, block_ids, staging, order, layer_idx, shard_idx,
                      stream):
+        ptr, nbytes = _capi.device_buffer(staging, "staging", self._device)
         ids, n = _capi.i64_array(block_ids)
-        nbytes = staging.numel() * staging.element_size()
         out = ctypes.c_void_p()
         if stream is None:
             import torch
             stream = torch.cuda.current_stream(staging.device)
-        _capi.check(fn(self._h, ids, n, staging.data_ptr(), nbytes, order,
+        _capi.check(fn(self._h, ids, n, ptr, nbytes, order,
                        -1 if layer_idx is None else layer_idx,
                        -1 if shard_idx is None else shard_idx,
                        ctypes.c_void_p(_stream_ptr(stream)), ctypes.byref(out)), where)

@@ -17,7 +17,6 @@ its index from a surviving table at construction
 """
 import ctypes
 import enum
-import os
 from typing import List, Optional, Sequence, Tuple
 
 from . import _capi
@@ -139,17 +138,6 @@ def _take_slices(handle) -> List[Tuple[bytes, RaidenBlockId]]:
     return out
 
 
-def _metadata_key_from_env() -> str:
-    key = os.environ.get("RAIDEN_SHM_KEY", "")
-    if not key:
-        return ""
-    key += "_metadata"
-    server = os.environ.get("RAIDEN_SHM_SERVER_NAME", "")
-    if server:
-        key += "_" + server
-    return key
-
-
 class KVCacheStore:
     """Host-tier KV store with the reference's pin contract.
 
@@ -163,8 +151,9 @@ class KVCacheStore:
         reference validates them (num_shards >= 1, ip non-empty and not a
         wildcard).
       raiden_controller_port: 0 picks an unused in-process address.
-      metadata_shm_key / model_uid: crash-persistent table; default from
-        RAIDEN_SHM_KEY / RAIDEN_SHM_MODEL_UID ("" disables it).
+      metadata_shm_key / model_uid: crash-persistent table; None takes the
+        library's defaults from RAIDEN_SHM_KEY (+ "_metadata", + "_" +
+        RAIDEN_SHM_SERVER_NAME) and RAIDEN_SHM_MODEL_UID; "" disables it.
       recover_at_create: rebuild the index from a surviving table now.
       host_blocks: host blocks of the controller's allocator (default:
         capacity, as the reference sizes it).
@@ -182,15 +171,13 @@ class KVCacheStore:
                              "one node only")
         del expected_worker_count, kv_pool_group
         rid = raiden_id if raiden_id is not None else RaidenId()
-        if metadata_shm_key is None:
-            metadata_shm_key = _metadata_key_from_env()
-        if model_uid is None:
-            model_uid = os.environ.get("RAIDEN_SHM_MODEL_UID") or "default_model"
         cfg = _capi.StoreConfig()
         cfg.capacity = int(capacity)
+        # None passes NULL: the library applies the RAIDEN_SHM_* defaults.
         self._strs = [rid.job_name.encode(), rid.job_replica_id.encode(),
                       rid.data_name.encode(), store_server_ip.encode(),
-                      metadata_shm_key.encode(), model_uid.encode()]
+                      None if metadata_shm_key is None else metadata_shm_key.encode(),
+                      None if model_uid is None else model_uid.encode()]
         (cfg.job_name, cfg.job_replica_id, cfg.data_name, cfg.store_server_ip,
          cfg.metadata_shm_key, cfg.model_uid) = self._strs
         cfg.data_replica_idx = rid.data_replica_idx

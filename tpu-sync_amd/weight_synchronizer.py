@@ -66,6 +66,10 @@ def column_split_entries(weight, outputs: Sequence[Any]) -> List[StridedEntry]:
     """Entries copying column chunk j of a row-major 2-D ``weight`` [R, C]
     into contiguous ``outputs[j]`` ([R, C_j]); chunk bounds from
     compute_nd_shard_slices((R, C), (1, k))."""
+    if weight.dim() != 2:
+        raise ValueError("column_split_entries needs a 2-D weight")
+    wptr, _ = _capi.device_buffer(weight, "weight")
+    device = weight.device.index or 0
     rows, cols = int(weight.shape[0]), int(weight.shape[1])
     item = weight.element_size()
     k = len(outputs)
@@ -76,9 +80,12 @@ def column_split_entries(weight, outputs: Sequence[Any]) -> List[StridedEntry]:
         out = outputs[j]
         if tuple(out.shape) != (rows, c1 - c0) or not out.is_contiguous():
             raise ValueError(f"output {j} must be a contiguous [{rows}, {c1 - c0}] tensor")
+        if out.dtype != weight.dtype:
+            raise ValueError(f"output {j} has dtype {out.dtype}, the weight {weight.dtype}")
+        optr, _ = _capi.device_buffer(out, f"output {j}", device)
         if c1 == c0 or rows == 0:
             continue  # an empty chunk moves nothing
-        entries.append(StridedEntry(weight.data_ptr() + c0 * item, out.data_ptr(),
+        entries.append(StridedEntry(wptr + c0 * item, optr,
                                     (c1 - c0) * item, rows, cols * item, (c1 - c0) * item))
     return entries
 
@@ -127,14 +134,17 @@ class WeightSynchronizer:
         num_shards = len(layers[0]) if layers else 1
         if any(len(s) != num_shards for s in layers):
             raise RuntimeError("Number of shards mismatch across layers")
-        ptrs, sizes, device = [], [], 0
+        ptrs, sizes, device = [], [], None
         for shards in layers:
             for t in shards:
-                if not t.is_contiguous():
+                if getattr(t, "is_cuda", False) and not t.is_contiguous():
                     raise RuntimeError("weight tensors must be contiguous")
-                ptrs.append(t.data_ptr())
-                sizes.append(t.numel() * t.element_size())
-                device = t.device.index or 0
+                if device is None and getattr(t, "is_cuda", False):
+                    device = t.device.index or 0
+                ptr, nbytes = _capi.device_buffer(t, "weight tensor", device)
+                ptrs.append(ptr)
+                sizes.append(nbytes)
+        device = device or 0
         self._tensors = layers
         self._device = device
         cfg = _capi.WeightSyncConfig()
@@ -182,20 +192,20 @@ class WeightSynchronizer:
     def pack(self, staging, stream=None) -> RaidenFuture:
         """Packs every weight into a device tensor of total_bytes bytes laid
         out by the offset table (one kernel launch)."""
+        ptr, nbytes = _capi.device_buffer(staging, "staging", self._device)
         if stream is None:
             import torch
             stream = torch.cuda.current_stream(staging.device)
         return self._fut(_capi.load().kvx_weight_sync_pack, "WeightSynchronizer pack",
-                         staging.data_ptr(), staging.numel() * staging.element_size(),
-                         stream=stream, keep=(self, staging))
+                         ptr, nbytes, stream=stream, keep=(self, staging))
 
     def unpack(self, staging, stream=None) -> RaidenFuture:
+        ptr, nbytes = _capi.device_buffer(staging, "staging", self._device)
         if stream is None:
             import torch
             stream = torch.cuda.current_stream(staging.device)
         return self._fut(_capi.load().kvx_weight_sync_unpack, "WeightSynchronizer unpack",
-                         staging.data_ptr(), staging.numel() * staging.element_size(),
-                         stream=stream, keep=(self, staging))
+                         ptr, nbytes, stream=stream, keep=(self, staging))
 
     def host_buffer_info(self, layer_idx: int = 0, shard_idx: int = 0) -> Tuple[int, int, int]:
         """(host address, bytes, offset in the packed image) of one weight."""
