@@ -7,10 +7,12 @@ blocks, bf16, a pool of 16384 blocks (32 GiB of HBM). One step offloads a
 batch of 512 random blocks into a pinned host slot and reloads the previous
 batch from the other host slot into 512 random free blocks; the two run at
 the same time in the two PCIe directions. value = KV payload bytes
-offloaded + reloaded per second. The headline mode (auto) moves short runs
-with one zero-copy kernel (pool <-> pinned host over PCIe); the staged mode
-(gather kernel + hipMemcpyAsync through a device staging ring, and H2D +
-scatter) is measured in the same run.
+offloaded + reloaded per second. The headline mode (auto) picks per copy:
+a batch's host runs here average 16 MiB per storage, so it stages (gather
+kernel + hipMemcpyAsync through a device staging ring, and H2D + scatter);
+headline_path reports the copies it issued. The staged and zero-copy modes
+(one kernel between pool and pinned host over PCIe) are measured in the same
+run.
 
 Printed as one JSON line, with the gather kernel's HBM roofline (HIP events
 on the kernel's stream over the timed region), measured pinned PCIe peaks
@@ -68,15 +70,18 @@ def parse_args():
     p.add_argument("--configs", default="fp8,weights,pools,zipf",
                    help="comma list of extra workloads to measure after the headline "
                         "(fp8, weights, pools, zipf; empty for none)")
-    p.add_argument("--zipf-host-blocks", type=int, default=2048,
-                   help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks")
-    p.add_argument("--zipf-batches", type=int, default=24)
+    p.add_argument("--zipf-host-blocks", type=int, default=0,
+                   help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks (0: "
+                        "the configured 256 GB budget, capped by free /dev/shm, available "
+                        "RAM and a 160 GiB process budget)")
+    p.add_argument("--zipf-batches", type=int, default=150)
     p.add_argument("--pools-host-alloc", default="pinned", choices=["pinned", "malloc"],
                    help="host mirror of the sparse-pool config (malloc: pageable, through "
                         "the bounce lanes)")
-    p.add_argument("--zipf-host-alloc", default="pinned", choices=["pinned", "shm"],
-                   help="host tier memory: pinned (hipHostMalloc) or a /dev/shm segment")
-    p.add_argument("--zipf-docs", type=int, default=8,
+    p.add_argument("--zipf-host-alloc", default="shm", choices=["pinned", "shm"],
+                   help="host tier memory: a /dev/shm segment (the reference's shared-"
+                        "memory tier) or pinned (hipHostMalloc)")
+    p.add_argument("--zipf-docs", type=int, default=64,
                    help="documents whose hash-chain prefixes the churn requests")
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
@@ -182,13 +187,33 @@ def pcie_peaks(torch, dev, nbytes=1 << 30, reps=5):
     return out
 
 
-def cpu_baseline(oracle, S, bb, n, min_seconds):
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(oracle, S, bb, n, pool_blocks, min_seconds):
     """The reference's host block pack/unpack (oracle restatement of
     ReadBlockBytes/WriteBlockBytes per block per storage) on host pools of
-    the workload's block shape, single-threaded and on every allowed core."""
-    pool_blocks = 1024
+    the workload's shape (the full pool when the host has room for it, else
+    1024 blocks per storage), single-threaded and on every allowed core."""
+    try:
+        with open("/proc/meminfo") as f:
+            kb = {ln.split(":")[0]: int(ln.split()[1]) for ln in f if ln.strip()}
+        avail = kb["MemAvailable"] * 1024
+    except (OSError, KeyError, ValueError):
+        avail = 0
+    if S * pool_blocks * bb * 3 > avail:
+        pool_blocks = 1024
     rng = np.random.default_rng(7)
-    pools = [rng.integers(0, 256, pool_blocks * bb, dtype=np.uint8) for _ in range(S)]
+    # Every page is written once (the values do not matter to a byte copy).
+    pools = [np.full(pool_blocks * bb, k & 0xFF, np.uint8) for k in range(S)]
     staging = np.empty(S * n * bb, np.uint8)
     try:
         ncores = len(os.sched_getaffinity(0))
@@ -207,18 +232,24 @@ def cpu_baseline(oracle, S, bb, n, min_seconds):
             t_total += time.perf_counter() - t0
             assert rc == 0 and rc2 == 0
             iters += 1
-        legs[threads] = (2 * iters * S * n * bb / t_total / 1e9, iters)
+        legs[threads] = (2 * iters * S * n * bb / t_total / 1e9, iters,
+                         2 * iters * n / t_total)
         log(f"cpu baseline threads={threads}: {legs[threads][0]:.2f} GB/s ({iters} iters)")
     best = legs[ncores]
+    del pools, staging
     return {
         "value": round(best[0], 3),
         "unit": "GB/s",
         "cores": ncores,
         "kind": "port",
+        "blocks_per_s": round(best[2], 1),
+        "cpu_model": cpu_model(),
         "single_thread_gbps": round(legs[1][0], 3),
+        "single_thread_blocks_per_s": round(legs[1][2], 1),
         "sample": (f"{S} storages x {pool_blocks}-block host pools x {bb} B blocks; "
                    f"per iteration extract {n} random ids into a contiguous buffer and "
-                   f"insert it at {n} other ids; {best[1]} iterations"),
+                   f"insert it at {n} other ids (a block = all {S} storages, "
+                   f"{S * bb} B); {best[1]} iterations on {ncores} threads"),
     }
 
 
@@ -460,23 +491,57 @@ def bench_pools(torch, pkg, dev, args, rng):
     return out
 
 
+def zipf_host_blocks(args, block_bytes):
+    """Host tier of the churn in blocks, and what set it: the configuration's
+    256 GB budget, capped by free /dev/shm (for the shm tier), available RAM
+    and a 160 GiB process budget (the pool's pinned staging, the bounce lanes
+    and the interpreter need the rest of the host memory a process may use)."""
+    if args.zipf_host_blocks > 0:
+        return args.zipf_host_blocks, "--zipf-host-blocks"
+    if args.zipf_host_alloc == "pinned":
+        # Page-locked allocations much beyond this were refused (out of memory).
+        return 2048, "pinned tier: 10 GiB"
+    limits = {"configured 256 GB budget": 256e9, "160 GiB process budget": float(160 << 30)}
+    st = os.statvfs("/dev/shm")
+    limits["80% of free /dev/shm"] = 0.8 * st.f_bavail * st.f_frsize
+    try:
+        with open("/proc/meminfo") as f:
+            kb = {ln.split(":")[0]: int(ln.split()[1]) for ln in f if ln.strip()}
+        limits["60% of MemAvailable"] = 0.6 * kb["MemAvailable"] * 1024
+    except (OSError, KeyError, ValueError):
+        pass
+    name, lim = min(limits.items(), key=lambda kv: kv[1])
+    return int(lim // block_bytes), name
+
+
+def percentiles_ms(xs):
+    if not xs:
+        return None
+    a = np.sort(np.asarray(xs)) * 1e3
+    return {"count": len(xs), "p50": round(float(np.percentile(a, 50)), 2),
+            "p99": round(float(np.percentile(a, 99)), 2), "max": round(float(a[-1]), 2)}
+
+
 def bench_zipf_store(torch, pkg, dev, args, rng):
     """Llama-3-70B-shaped KV (80 layers, K and V: 160 storages of 12000 x 32
-    KiB blocks, 58.6 GiB) with a host tier of pinned blocks behind the
-    KVCacheStore; prefix-cache churn: each request is a prefix of one of
-    --zipf-docs documents' block-hash chains (document drawn Zipf(1.1), length 64-2048
-    blocks log-uniform). Lookup returns the cached prefix, which is loaded
-    into device blocks; the rest is inserted and saved (evicting LRU entries
-    once the host tier is full). Load (H2D) and save (D2H) of a request are
-    issued together; up to --zipf-inflight requests have copies in flight
-    (the next request is looked up and issued while the previous one's
-    copies run), as in a server with several requests in progress."""
+    KiB blocks, 58.6 GiB) with a host LRU tier (default: a /dev/shm segment of
+    the configured 256 GB budget, or as much of it as the machine allows)
+    behind the KVCacheStore; prefix-cache churn: each request is a prefix of
+    one of --zipf-docs documents' block-hash chains (document drawn Zipf(1.1),
+    length 64-2048 blocks log-uniform). Lookup returns the cached prefix,
+    which is loaded into device blocks; the rest is inserted and saved
+    (evicting LRU entries once the host tier is full). Load (H2D) and save
+    (D2H) of a request are issued together; up to --zipf-inflight requests
+    have copies in flight (the next request is looked up and issued while the
+    previous one's copies run), as in a server with several requests in
+    progress. With one request in flight, each request's latency (lookup to
+    both copies polled done) is recorded."""
     L, P, bb = 80, 12000, 32768
-    host_blocks = args.zipf_host_blocks
     S = 2 * L
+    host_blocks, tier_limit = zipf_host_blocks(args, S * bb)
     log(f"zipf: allocating {S} x {P} x {bb} B pool ({S * P * bb / 2**30:.1f} GiB), "
         f"{host_blocks} host blocks ({host_blocks * S * bb / 2**30:.1f} GiB "
-        f"{args.zipf_host_alloc})")
+        f"{args.zipf_host_alloc}, limit: {tier_limit})")
     pools = [torch.empty(P, bb, dtype=torch.uint8, device=dev) for _ in range(S)]
     for p in pools:
         p.random_(0, 256)
@@ -485,11 +550,14 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     tier = {}
     if args.zipf_host_alloc == "shm":
         tier = {"host_alloc": "shm", "shm_key": f"kvx_bench_{os.getpid()}"}
+    t_tier = time.perf_counter()
     mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=host_blocks,
                              staging_chunk_bytes=args.chunk_mib << 20,
                              staging_chunks=args.chunks,
                              raiden_controller_address=store.raiden_controller_address,
                              **tier)
+    t_tier = time.perf_counter() - t_tier
+    log(f"zipf: host tier ready in {t_tier:.1f} s")
     rid = store.raiden_id
     docs = args.zipf_docs
     w = 1.0 / np.arange(1, docs + 1) ** 1.1
@@ -513,11 +581,13 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
                     raise RuntimeError(f"store save failed: {len(failed)} blocks")
                 done_s += len(done)
 
-    saved = loaded = hits = asked = skipped = device_hits = 0
+    saved = loaded = hits = asked = skipped = device_hits = replaced = 0
     inflight = max(1, args.zipf_inflight)
     window = []  # (loads, saves) of the requests possibly still in flight
+    latency = []  # (blocks, seconds) per request, one request in flight
     t0 = time.perf_counter()
     for step in range(args.zipf_batches):
+        t_req = time.perf_counter()
         doc = int(np.searchsorted(cdf, rng.random()))
         nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
         chain = [b"d%03d:%05d" % (doc, i) for i in range(nb)]
@@ -544,11 +614,15 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
         loading.update(load_h)
         n_save = 0
         if rest:
+            # Chain blocks past the cached prefix that are still on the host
+            # (their prefix was evicted first) cannot be reached through a
+            # prefix lookup any more; the request's fresh copies replace them.
+            replaced += store.evict(rest)
             sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
             if store.insert(rest, sl, on_host=False):
                 if store.save(rest):
                     n_save = len(rest)
-                else:  # no host blocks to spare (everything else pinned)
+                else:  # no host blocks to spare, or a block pinned by another request
                     store.release(rest)
                     skipped += len(rest)
             else:  # another request in flight inserted some of them
@@ -563,6 +637,8 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
         keep = window[len(window) - (inflight - 1):] if inflight > 1 else []
         poll_until(loaded - sum(x[0] for x in keep), saved - sum(x[1] for x in keep))
         window = keep
+        if inflight == 1:
+            latency.append((nb, time.perf_counter() - t_req))
     poll_until(loaded, saved)
     t_run = time.perf_counter() - t0
     moved = (saved + loaded) * S * bb
@@ -571,12 +647,19 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
            "host_tier_blocks": host_blocks, "host_tier_memory": args.zipf_host_alloc,
            "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
+           "host_tier_limit": tier_limit, "host_tier_setup_s": round(t_tier, 1),
            "batches": args.zipf_batches, "requests_in_flight": inflight,
            "blocks_saved": saved, "blocks_loaded": loaded,
            "blocks_skipped": skipped, "device_hits": device_hits,
+           "stale_suffix_blocks_replaced": replaced,
+           "blocks_evicted_lru": max(0, saved - replaced - store.size()),
            "hit_rate": round(hits / max(asked, 1), 4),
            "gbps": round(moved / t_run / 1e9, 2),
-           "blocks_per_s": round((saved + loaded) / t_run, 1)}
+           "blocks_per_s": round((saved + loaded) / t_run, 1),
+           "latency_ms": ({"all_requests": percentiles_ms([t for _, t in latency]),
+                           "requests_64_to_127_blocks": percentiles_ms(
+                               [t for nb, t in latency if nb < 128])}
+                          if latency else None)}
     log(f"zipf: {out}")
     mgr.close()
     store.close()
@@ -644,6 +727,11 @@ def main():
     stats = mgr.engine_stats()
     log(f"offload+reload: {value:.2f} GB/s, {elapsed / args.steps * 1e3:.2f} ms/step "
         f"({stats})")
+    # What the headline copies actually did (the auto mode decides per copy).
+    kinds = {"staged": stats["staged_copies"], "zero_copy": stats["zero_copy_copies"],
+             "direct": stats["direct_copies"]}
+    headline_path = {"mode": args.mode, **{f"{k}_copies": v for k, v in kinds.items()},
+                     "path": "+".join(k for k, v in kinds.items() if v) or "none"}
     kg = mgr.kernel_times(True, reset=True)
     ks = mgr.kernel_times(False, reset=True)
 
@@ -709,7 +797,7 @@ def main():
         half = n * S * bb
         reps = max(3, args.sub_steps // 2)
         modes = {}
-        for mode in ("zero_copy", "staged"):
+        for mode in [args.mode] + [x for x in ("zero_copy", "staged") if x != args.mode]:
             m = mgr if mode == args.mode else make_mgr(mode)
             t_off, t_rel = one_direction(m, batch, slots, reps)
             el_steps = args.steps if m is mgr else args.sub_steps
@@ -723,16 +811,17 @@ def main():
                 m.close()
         log("measuring pinned PCIe peaks")
         peaks = pcie_peaks(torch, dev)
-        head_mode = "zero_copy" if args.mode == "auto" else args.mode
         for mode, r in modes.items():
             r["offload_frac_of_pcie_d2h"] = round(r["offload_gbps"] / peaks["pcie_d2h_gbps"], 4)
             r["reload_frac_of_pcie_h2d"] = round(r["reload_gbps"] / peaks["pcie_h2d_gbps"], 4)
             r["duplex_frac_of_pcie_bidir"] = round(r["duplex_gbps"] / peaks["pcie_bidir_gbps"], 4)
+        # Per direction: the headline manager itself (its mode), one copy at a
+        # time; the path it took is in headline_path.
         extras = {
-            "offload_gbps": modes[head_mode]["offload_gbps"],
-            "reload_gbps": modes[head_mode]["reload_gbps"],
-            "offload_frac_of_pcie_d2h": modes[head_mode]["offload_frac_of_pcie_d2h"],
-            "reload_frac_of_pcie_h2d": modes[head_mode]["reload_frac_of_pcie_h2d"],
+            "offload_gbps": modes[args.mode]["offload_gbps"],
+            "reload_gbps": modes[args.mode]["reload_gbps"],
+            "offload_frac_of_pcie_d2h": modes[args.mode]["offload_frac_of_pcie_d2h"],
+            "reload_frac_of_pcie_h2d": modes[args.mode]["reload_frac_of_pcie_h2d"],
             "duplex_frac_of_pcie_bidir": round(value / peaks["pcie_bidir_gbps"], 4),
             **{k: round(v, 2) for k, v in peaks.items()},
             "modes": modes,
@@ -756,7 +845,7 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         log("CPU baseline (oracle host pack/unpack)")
-        cpu = cpu_baseline(__graft_entry__.load_oracle(), S, bb, n, args.cpu_seconds)
+        cpu = cpu_baseline(__graft_entry__.load_oracle(), S, bb, n, P, args.cpu_seconds)
 
     out = {
         "metric": "KV offload/reload GB/s (HBM gather + PCIe) and % of roofline, 1 GPU",
@@ -779,6 +868,7 @@ def main():
             "transfer_mode": args.mode, "staging_chunk_mib": args.chunk_mib,
         },
         "blocks_per_s": round(args.steps * 2 * n / elapsed, 1),
+        "headline_path": headline_path,
         "roofline": iso["gather"],
         "scatter_roofline": iso["scatter"],
         "loop_gather": loop_gather,
