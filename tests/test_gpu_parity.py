@@ -310,6 +310,50 @@ def test_raw_kernel_bad_id_flag(kvx, cuda):
                                  stream) == 3
 
 
+@pytest.mark.parametrize("bb", [16, 48, 36, 3, 1024])
+@pytest.mark.parametrize("id_list", [[-1, 25, 4, 99, 11], [-5, 30, 21]])
+def test_raw_small_blocks_bad_first_or_all(kvx, cuda, bb, id_list):
+    """Small-block path (many blocks per workgroup): a workgroup whose first
+    blocks have bad ids, and one whose blocks all have bad ids, move exactly
+    the good blocks and flag the bad ones."""
+    rng = np.random.default_rng(bb + len(id_list))
+    W, P = 4, 21
+    n = len(id_list)
+    pools = [torch.from_numpy(rng.integers(0, 256, (P, bb), dtype=np.uint8)).to(cuda)
+             for _ in range(W)]
+    table = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64, device=cuda)
+    ids = torch.tensor(id_list, dtype=torch.int64, device=cuda)
+    stg = torch.full((W, n, bb), 0x5C, dtype=torch.uint8, device=cuda)
+    err = torch.zeros(1, dtype=torch.int32, device=cuda)
+    lib = kvx._capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.kvx_gather_blocks(table.data_ptr(), W, bb, P, ids.data_ptr(), n,
+                                 stg.data_ptr(), 0, err.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    got = stg.cpu().numpy()
+    for w in range(W):
+        ref = pools[w].cpu().numpy()
+        for i, b in enumerate(id_list):
+            if 0 <= b < P:
+                assert np.array_equal(got[w, i], ref[b])
+            else:
+                assert (got[w, i] == 0x5C).all()
+    zero = [torch.zeros(P, bb, dtype=torch.uint8, device=cuda) for _ in range(W)]
+    table2 = torch.tensor([p.data_ptr() for p in zero], dtype=torch.int64, device=cuda)
+    err.zero_()
+    assert lib.kvx_scatter_blocks(table2.data_ptr(), W, bb, P, ids.data_ptr(), n,
+                                  stg.data_ptr(), 0, err.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    good = [b for b in id_list if 0 <= b < P]
+    for w in range(W):
+        z = zero[w].cpu().numpy()
+        want = np.zeros_like(z)
+        want[good] = pools[w].cpu().numpy()[good]
+        assert np.array_equal(z, want)
+
+
 def bf16_normal(rng, shape):
     """float32 N(0,1) rounded to bf16 (nearest even) on the bit pattern."""
     x = rng.standard_normal(shape, dtype=np.float32).view(np.uint32)
