@@ -9,7 +9,9 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkvx.so")
+# KVX_LIBRARY names another build of the same library (the sanitizer builds of
+# the Makefile's asan / tsan targets); by default the in-tree libkvx.so.
+LIB_PATH = os.environ.get("KVX_LIBRARY") or os.path.join(_HERE, "libkvx.so")
 
 STATUS_NAMES = {
     0: "OK", 1: "CANCELLED", 2: "UNKNOWN", 3: "INVALID_ARGUMENT",
