@@ -74,14 +74,14 @@ def parse_args():
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks (0: "
                         "the configured 256 GB budget, capped by free /dev/shm, available "
                         "RAM and a 160 GiB process budget)")
-    p.add_argument("--zipf-batches", type=int, default=150)
+    p.add_argument("--zipf-batches", type=int, default=240)
     p.add_argument("--pools-host-alloc", default="pinned", choices=["pinned", "malloc"],
                    help="host mirror of the sparse-pool config (malloc: pageable, through "
                         "the bounce lanes)")
     p.add_argument("--zipf-host-alloc", default="shm", choices=["pinned", "shm"],
                    help="host tier memory: a /dev/shm segment (the reference's shared-"
                         "memory tier) or pinned (hipHostMalloc)")
-    p.add_argument("--zipf-docs", type=int, default=64,
+    p.add_argument("--zipf-docs", type=int, default=160,
                    help="documents whose hash-chain prefixes the churn requests")
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
@@ -124,6 +124,24 @@ def rocpd_summary(db_path):
             short = short if len(short) <= 60 else short[:57] + "..."
             print(f"{short:<60} {grid or 0:>9} {counter:>11} {cnt:>6} {avg:>13.1f} "
                   f"{mn:>13.1f} {mx:>13.1f}")
+    # Streams and the hardware queues their kernels ran on (memory copies that
+    # run on SDMA engines have no compute queue).
+    q = ("select stream_id, queue_id, name, count(*) from kernels "
+         "group by stream_id, queue_id, name order by stream_id, count(*) desc")
+    rows = list(cur.execute(q))
+    if rows:
+        print(f"\n{'stream':>6} {'queue':>5} {'launches':>8}  kernel")
+        for sid, qid, name, cnt in rows:
+            short = (name.replace("void ", "").replace("(anonymous namespace)::", "")
+                     .replace("unsigned int __vector(4)", "u32x4"))
+            if ">(" in short:
+                short = short[:short.index(">(") + 1]
+            print(f"{sid:>6} {qid if qid is not None else '-':>5} {cnt:>8}  {short[:70]}")
+        q = ("select stream_id, name, count(*), sum(size) from memory_copies "
+             "group by stream_id, name order by stream_id")
+        print(f"\n{'stream':>6} {'copies':>8} {'GB':>9}  direction (SDMA or blit)")
+        for sid, name, cnt, size in cur.execute(q):
+            print(f"{sid:>6} {cnt:>8} {size / 1e9:>9.3f}  {name}")
     q = ("select name, count(*), sum(size), avg(end - start), sum(end - start) "
          "from memory_copies group by name")
     rows = list(cur.execute(q))
@@ -522,7 +540,7 @@ def percentiles_ms(xs):
             "p99": round(float(np.percentile(a, 99)), 2), "max": round(float(a[-1]), 2)}
 
 
-def bench_zipf_store(torch, pkg, dev, args, rng):
+def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     """Llama-3-70B-shaped KV (80 layers, K and V: 160 storages of 12000 x 32
     KiB blocks, 58.6 GiB) with a host LRU tier (default: a /dev/shm segment of
     the configured 256 GB budget, or as much of it as the machine allows)
@@ -585,6 +603,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
     inflight = max(1, args.zipf_inflight)
     window = []  # (loads, saves) of the requests possibly still in flight
     latency = []  # (blocks, seconds) per request, one request in flight
+    per_request = []  # (blocks loaded, blocks saved) per request
     t0 = time.perf_counter()
     for step in range(args.zipf_batches):
         t_req = time.perf_counter()
@@ -639,9 +658,21 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
         window = keep
         if inflight == 1:
             latency.append((nb, time.perf_counter() - t_req))
+        per_request.append((len(load_h), n_save))
     poll_until(loaded, saved)
     t_run = time.perf_counter() - t0
     moved = (saved + loaded) * S * bb
+    # PCIe bound of this request stream: a request's load (H2D) and save (D2H)
+    # run at once, each at most at its direction's measured pinned peak, and
+    # requests follow one another, so the stream needs at least
+    # sum(max(load bytes / H2D peak, save bytes / D2H peak)).
+    pcie_bound = None
+    if peaks and inflight == 1:
+        t_min = sum(max(l * S * bb / (peaks["pcie_h2d_gbps"] * 1e9),
+                        sv * S * bb / (peaks["pcie_d2h_gbps"] * 1e9))
+                    for l, sv in per_request)
+        if t_min > 0:
+            pcie_bound = moved / t_min / 1e9
     out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
                        "churn through the KV store: requests are prefixes (64-2048 blocks) of "
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
@@ -655,6 +686,9 @@ def bench_zipf_store(torch, pkg, dev, args, rng):
            "blocks_evicted_lru": max(0, saved - replaced - store.size()),
            "hit_rate": round(hits / max(asked, 1), 4),
            "gbps": round(moved / t_run / 1e9, 2),
+           "pcie_bound_gbps": round(pcie_bound, 2) if pcie_bound else None,
+           "frac_of_pcie_bound": round(moved / t_run / 1e9 / pcie_bound, 4)
+                                 if pcie_bound else None,
            "blocks_per_s": round((saved + loaded) / t_run, 1),
            "latency_ms": ({"all_requests": percentiles_ms([t for _, t in latency]),
                            "requests_64_to_127_blocks": percentiles_ms(
@@ -793,6 +827,7 @@ def main():
     mgr.kernel_times(False, reset=True)
 
     extras = {}
+    measured_peaks = None
     if not args.no_extras:
         half = n * S * bb
         reps = max(3, args.sub_steps // 2)
@@ -811,6 +846,7 @@ def main():
                 m.close()
         log("measuring pinned PCIe peaks")
         peaks = pcie_peaks(torch, dev)
+        measured_peaks = peaks
         for mode, r in modes.items():
             r["offload_frac_of_pcie_d2h"] = round(r["offload_gbps"] / peaks["pcie_d2h_gbps"], 4)
             r["reload_frac_of_pcie_h2d"] = round(r["reload_gbps"] / peaks["pcie_h2d_gbps"], 4)
@@ -840,7 +876,8 @@ def main():
     if "pools" in wanted:
         configs["sparse_pool_copies"] = bench_pools(torch, pkg, dev, args, rng)
     if "zipf" in wanted:
-        configs["llama3_70b_zipf_churn"] = bench_zipf_store(torch, pkg, dev, args, rng)
+        configs["llama3_70b_zipf_churn"] = bench_zipf_store(torch, pkg, dev, args, rng,
+                                                            peaks=measured_peaks)
 
     cpu = None
     if args.cpu_seconds > 0:
