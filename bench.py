@@ -83,6 +83,10 @@ def parse_args():
                         "memory tier) or pinned (hipHostMalloc)")
     p.add_argument("--zipf-docs", type=int, default=160,
                    help="documents whose hash-chain prefixes the churn requests")
+    p.add_argument("--zipf-chunk-mib", type=int, default=0,
+                   help="staging chunk of the churn's manager (0: --chunk-mib)")
+    p.add_argument("--zipf-host-threads", type=int, default=0,
+                   help="host copy threads of the churn's bounce lanes (0: the library's 8)")
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
                         "request's load and save finish before the next is issued)")
@@ -570,8 +574,9 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
         tier = {"host_alloc": "shm", "shm_key": f"kvx_bench_{os.getpid()}"}
     t_tier = time.perf_counter()
     mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=host_blocks,
-                             staging_chunk_bytes=args.chunk_mib << 20,
+                             staging_chunk_bytes=(args.zipf_chunk_mib or args.chunk_mib) << 20,
                              staging_chunks=args.chunks,
+                             host_copy_threads=args.zipf_host_threads,
                              raiden_controller_address=store.raiden_controller_address,
                              **tier)
     t_tier = time.perf_counter() - t_tier
@@ -680,6 +685,8 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
            "host_tier_gib": round(host_blocks * S * bb / 2**30, 1),
            "host_tier_limit": tier_limit, "host_tier_setup_s": round(t_tier, 1),
            "batches": args.zipf_batches, "requests_in_flight": inflight,
+           "staging_chunk_mib": args.zipf_chunk_mib or args.chunk_mib,
+           "host_copy_threads": args.zipf_host_threads or 8,
            "blocks_saved": saved, "blocks_loaded": loaded,
            "blocks_skipped": skipped, "device_hits": device_hits,
            "stale_suffix_blocks_replaced": replaced,
