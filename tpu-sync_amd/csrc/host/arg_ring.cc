@@ -89,7 +89,8 @@ Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {
 }
 
 Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
-                                hipStream_t stream, uint32_t max_workgroups) {
+                                hipStream_t stream, uint32_t max_workgroups,
+                                hipEvent_t kernel_start) {
   if (copies.empty()) return OkStatus();
   const int vec = StridedVectorBytes(copies);
   std::vector<StridedEntryDev> table;
@@ -109,6 +110,7 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
     for (uint32_t t = table[e].tile_begin; t < end; ++t) map[t] = static_cast<uint32_t>(e);
   }
   KVX_RETURN_IF_ERROR(ring.Upload(off, bytes, stream));
+  if (kernel_start != nullptr) KVX_HIP_RETURN_IF_ERROR(hipEventRecord(kernel_start, stream));
   KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
       reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
       static_cast<uint32_t>(table.size()), grid, vec, stream, max_workgroups));

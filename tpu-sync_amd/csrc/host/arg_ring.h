@@ -85,9 +85,12 @@ class ArgSliceGuard {
 
 // Uploads the table and tile map of `copies` through `ring` and launches the
 // strided-copy kernel on `stream` (at most max_workgroups workgroups when
-// > 0); the ring region stays reserved until the launch ends.
+// > 0); the ring region stays reserved until the launch ends. A non-null
+// `kernel_start` is recorded on `stream` after the upload, right before the
+// launch (to time the kernel alone).
 Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
-                                hipStream_t stream, uint32_t max_workgroups = 0);
+                                hipStream_t stream, uint32_t max_workgroups = 0,
+                                hipEvent_t kernel_start = nullptr);
 
 }  // namespace kvx
 

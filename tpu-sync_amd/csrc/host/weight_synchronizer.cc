@@ -144,9 +144,10 @@ Status WeightSynchronizer::Launch(const std::vector<StridedCopy>& copies, bool p
   if (cfg_.profile_kernels) {
     KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.start));
     KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.stop));
-    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.start, stream));
   }
-  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(args_, copies, stream));
+  // The start event goes on the stream after the table upload, so a sample
+  // times the kernel alone.
+  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(args_, copies, stream, 0, s.start));
   if (cfg_.profile_kernels) {
     KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.stop, stream));
     for (const StridedCopy& c : copies) s.bytes += c.size * (c.count > 0 ? c.count : 1);
