@@ -196,21 +196,8 @@ def test_cpu_manager_auto_allocate_needs_device(kvx):
     m.close()
 
 
-def test_network_surface_fails_loudly(kvx):
-    """The reference manager's network transport accessors and calls
-    (tpu_sync/api/torch/kv_cache_manager.py:162-213, 334-448) exist with the
-    same names; they raise, or report that nothing runs."""
+def test_node_id_kept(kvx):
     m = kvx.KVCacheManager.create_host_only_for_testing(num_layers=1, slice_byte_size=64,
                                                         host_blocks=4, node_id=5)
     assert m.node_id == 5
-    assert m.listener_port is None and m.is_listener_active is False
-    assert m.poll_stats() == ([], [], [])
-    for name in ("local_port", "local_control_port", "transfer_address", "listener_address",
-                 "raiden_worker_port"):
-        with pytest.raises(NotImplementedError, match="network block transport"):
-            getattr(m, name)
-    with pytest.raises(NotImplementedError):
-        m.start_read("r", 1, [0], [0])
-    with pytest.raises(NotImplementedError):
-        m.register_recv(1, "r", 3)
     m.close()

@@ -484,72 +484,6 @@ class KVCacheManager:
             return np.zeros(0, np.uint8)
         return np.ctypeslib.as_array((ctypes.c_uint8 * size).from_address(ptr))
 
-    # -- network transport (not part of this build) ------------------------
-    # The reference's manager also runs a TCP block transport, a control
-    # listener and a gRPC worker (tpu_sync/api/torch/kv_cache_manager.py:
-    # 162-213, 334-448). This package moves blocks on one node only: the
-    # endpoint accessors and network transfer calls fail loudly, and the
-    # listener / transfer status report that nothing runs.
-    def _no_network(self, what):
-        raise NotImplementedError(
-            f"KVCacheManager.{what}: the network block transport is not part of this "
-            "MI355X build (single node: use d2h/h2d, gather/scatter, stage_for_push, "
-            "prepare_load/issue_h2d and the transport framing in tpu_sync_amd.transport)")
-
-    @property
-    def raiden_worker_port(self) -> int:
-        self._no_network("raiden_worker_port")
-
-    @property
-    def local_control_port(self) -> int:
-        self._no_network("local_control_port")
-
-    @property
-    def local_port(self) -> int:
-        self._no_network("local_port")
-
-    @property
-    def transfer_address(self) -> str:
-        self._no_network("transfer_address")
-
-    @property
-    def listener_address(self) -> str:
-        self._no_network("listener_address")
-
-    @property
-    def listener_port(self) -> Optional[int]:
-        return None
-
-    @property
-    def is_listener_active(self) -> bool:
-        return False
-
-    def get_local_endpoints(self) -> List[dict]:
-        self._no_network("get_local_endpoints")
-
-    def register_active_plan(self, uuid: int, request: Any, is_sender: bool) -> None:
-        self._no_network("register_active_plan")
-
-    def unregister_active_plan(self, uuid: int) -> None:
-        self._no_network("unregister_active_plan")
-
-    def push_registered_plan(self, uuid: int, peer: str, *args, **kwargs) -> Any:
-        self._no_network("push_registered_plan")
-
-    def register_recv(self, uuid: int, req_id: str, expected_block_count: int) -> None:
-        self._no_network("register_recv")
-
-    def register_read(self, req_id: str, uuid: int, block_ids: List[int]) -> bool:
-        self._no_network("register_read")
-
-    def start_read(self, req_id: str, uuid: int, *args, **kwargs) -> None:
-        self._no_network("start_read")
-
-    def poll_stats(self) -> Tuple[List[str], List[str], List[str]]:
-        """(done sending, done receiving, failed receiving) request ids of
-        network transfers: always empty here."""
-        return [], [], []
-
     # -- staging-slot pool --------------------------------------------------
     def initialize_slot_pool(self, num_slots: int) -> None:
         _capi.check(_capi.load().kvx_manager_initialize_slot_pool(self._h, num_slots),

@@ -16,7 +16,7 @@ device: ``copy_strided(entries)`` runs any list of
 and ``column_split_entries`` builds the entries of a column split whose
 bounds follow ``compute_nd_shard_slices`` (tpu_sync/kv_cache/
 nd_slice_math.py:23-70: equal tiles, remainder to the last shard).
-Networked pushes (push_weights, listeners) are out of scope.
+Networked pushes and their listener are not part of this package.
 """
 import ctypes
 import itertools
@@ -255,23 +255,6 @@ class WeightSynchronizer:
         _capi.check(_capi.load().kvx_weight_sync_kernel_times(
             self._h, int(pack), int(reset), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(b)))
         return {"launches": n.value, "total_ms": ms.value, "bytes": b.value}
-
-    def push_weights(self, peers: List[str]) -> None:
-        raise NotImplementedError("networked weight pushes are not part of this build")
-
-    # The reference's listener accessors (tpu_sync/api/torch/weight_synchronizer.py:
-    # 95-108): Optional ports, None when no listener runs -- none does here.
-    @property
-    def local_port(self) -> Optional[int]:
-        return None
-
-    @property
-    def listener_port(self) -> Optional[int]:
-        return None
-
-    @property
-    def is_listener_active(self) -> bool:
-        return False
 
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
