@@ -10,6 +10,7 @@
 #include "../kernels/block_copy.h"
 #include "../kernels/strided_copy.h"
 #include "hip_util.h"
+#include "stream_copy.h"
 
 namespace kvx {
 namespace {
@@ -124,7 +125,7 @@ struct TransferEngine::Bounce {
     return first;
   }
 
-  // A fixed pool of threads running parallel memcpy batches.
+  // A fixed pool of threads running parallel host copy batches.
   explicit Bounce(int threads) {
     for (int t = 0; t < threads; ++t) workers.emplace_back([this] { Work(); });
   }
@@ -165,12 +166,27 @@ struct TransferEngine::Bounce {
 
  private:
   void Drain(std::vector<Segment>* p) {
+    const size_t n = p->size();
+    // Many small pieces (random blocks of a pageable tier: each crosses
+    // several 4 KiB pages) are taken four at a time, so a thread knows its
+    // next piece and prefetches it while it copies the current one; few
+    // pieces are taken one at a time to keep every thread busy.
+    const size_t take = n >= 64 * (workers.size() + 1) ? 4 : 1;
     size_t finished = 0;
-    for (size_t i = next.fetch_add(1); i < p->size(); i = next.fetch_add(1)) {
-      const Segment& s = (*p)[i];
-      std::memcpy(s.dst, s.src, s.bytes);
-      ++finished;
+    for (size_t i = next.fetch_add(take); i < n; i = next.fetch_add(take)) {
+      const size_t e = std::min(n, i + take);
+      if (take > 1) PrefetchSource((*p)[i].src, (*p)[i].bytes);
+      for (size_t j = i; j < e; ++j) {
+        if (j + 1 < e) PrefetchSource((*p)[j + 1].src, (*p)[j + 1].bytes);
+        // Streaming stores: the DMA engines read and write the same host
+        // memory meanwhile, and the bytes are not read again by this CPU.
+        StreamCopy((*p)[j].dst, (*p)[j].src, (*p)[j].bytes);
+        ++finished;
+      }
     }
+    // Completion is published under `mu` below; the DMA that reads these
+    // bytes (or the caller that reads the pageable side) comes after it.
+    StreamFence();
     if (finished > 0) {
       std::lock_guard<std::mutex> l(mu);
       left -= finished;
