@@ -274,10 +274,17 @@ int kvx_manager_block_chunks(kvx_manager* m, int64_t block_array_idx, int64_t sh
 int64_t kvx_manager_allocated_host_bytes(const kvx_manager* m);
 /* Blocks until every copy the manager issued has finished. */
 int kvx_manager_wait_for_pending_work(kvx_manager* m);
-/* Counters of what the transfer engine issued: out[0..6] = direct copies,
- * staged copies, hipMemcpyAsync calls, kernel launches, staging chunks,
- * zero-copy copies, pool-extent kernel copies. */
+/* Counters of what the transfer engine issued: out[0..7] = direct copies,
+ * staged copies, DMA calls, kernel launches, staging chunks, zero-copy
+ * copies, pool-extent kernel copies, copies through the pageable lanes. */
 int kvx_manager_engine_stats(kvx_manager* m, int64_t* out8);
+/* SDMA engines of the pageable lanes' DMAs (no reference counterpart: the
+ * reference's host tiers are registered memory, DMA'd directly): the
+ * device-to-host engine bit << 16 | the host-to-device engine bit
+ * (hsa_amd_sdma_engine_id_t), chosen when the first lane starts. 0 while no
+ * lane has run, or when the lanes use hipMemcpyAsync (KVX_LANE_DMA=hip, or
+ * no engine available); -1 for a null or CPU-only manager. */
+int32_t kvx_manager_lane_dma_engines(kvx_manager* m);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the
  * gather (gather = 1) or scatter (gather = 0) kernels so far. Waits for the

@@ -103,6 +103,10 @@ PATHS = {
     # slots are drained and refilled inside one copy; 3 host threads.
     "bounce": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                    host_alloc="malloc", host_copy_threads=3),
+    # The same with the lanes' DMAs through hipMemcpyAsync (KVX_LANE_DMA=hip)
+    # instead of fixed SDMA engines.
+    "bounce_hip": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                       host_alloc="malloc", host_copy_threads=3),
     # Pageable mirror left to the runtime's per-run hipMemcpyAsync.
     "pageable": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                      host_alloc="malloc", host_copy_threads=-1),
@@ -110,9 +114,12 @@ PATHS = {
 MODES = ["staged", "zero_copy"]
 
 
-@pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "pageable"])
+@pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "bounce_hip",
+                                  "pageable"])
 @pytest.mark.parametrize("bb", [32768, 61424, 12992, 1024, 48, 36, 3])
-def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
+def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
+    if path == "bounce_hip":
+        monkeypatch.setenv("KVX_LANE_DMA", "hip")
     rng = np.random.default_rng(bb * 7 + len(path))
     layers, shards, blocks, hb = 3, 2, 40, 30
     host, dev = dev_pools(rng, cuda, layers, shards, blocks, bb)
@@ -133,14 +140,20 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, path, bb):
         assert mir.transfer(d2h, src, dst, sizes, layer, shard) == 0
         mir.check(mgr, dev)
     stats = mgr.engine_stats()
-    if path in ("staged", "bounce", "pageable"):
+    if path in ("staged", "bounce", "bounce_hip", "pageable"):
         assert stats["direct_copies"] == 0 and stats["staged_copies"] == 12
         assert stats["chunks"] > 12 or bb < 1024
-        assert stats["bounce_copies"] == (12 if path == "bounce" else 0)
+        assert stats["bounce_copies"] == (12 if path.startswith("bounce") else 0)
     elif path == "zero_copy":
         assert stats["zero_copy_copies"] == 12 and stats["memcpy_calls"] == 0
     else:
         assert stats["staged_copies"] == 0 and stats["zero_copy_copies"] == 0
+    # The lanes' DMAs: one SDMA engine bit per direction, or hipMemcpyAsync.
+    if path == "bounce":
+        engines = mgr.lane_dma_engines
+        assert engines is not None and all(e and e & (e - 1) == 0 for e in engines), engines
+    elif path == "bounce_hip":
+        assert mgr.lane_dma_engines is None
     mgr.close()
 
 

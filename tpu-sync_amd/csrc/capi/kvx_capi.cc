@@ -499,6 +499,10 @@ int kvx_manager_engine_stats(kvx_manager* m, int64_t* out8) {
   out8[7] = s.bounce_copies;
   return KVX_OK;
 }
+int32_t kvx_manager_lane_dma_engines(kvx_manager* m) {
+  if (m == nullptr || m->impl->engine() == nullptr) return -1;
+  return static_cast<int32_t>(m->impl->engine()->LaneDmaEngines());
+}
 
 int kvx_manager_kernel_times(kvx_manager* m, int32_t gather, int32_t reset,
                              int64_t* out_launches, double* out_total_ms,

@@ -92,17 +92,31 @@ struct TransferEngine::Bounce {
   };
   std::vector<uint8_t*> bufs;
   std::vector<hipEvent_t> dma_done;  // last DMA into (D2H) or out of (H2D) bufs[k]
+  // With fixed SDMA engines (sdma != null) the DMAs are ROCr copies and
+  // dma_sig[k] stands in for dma_done[k].
+  const SdmaEngines* sdma = nullptr;
+  std::vector<hsa_signal_t> dma_sig;
   std::vector<bool> used;
   std::vector<std::vector<Segment>> owed;  // D2H: host copies still due from bufs[k]
   std::vector<std::vector<CopyFuture>> waiters;  // D2H: copies complete once bufs[k] drains
   std::deque<size_t> order;                // D2H: slots with copies owed, oldest first
+
+  Status WaitDma(size_t k) {
+    if (sdma != nullptr) return SdmaEngines::Wait(dma_sig[k]);
+    return HipStatus(hipEventSynchronize(dma_done[k]), "bounce buffer DMA");
+  }
+  // Waits for every DMA still in flight (SDMA copies are on no stream, so a
+  // stream synchronisation does not cover them).
+  void WaitAllDma() {
+    for (size_t k = 0; k < dma_sig.size(); ++k) (void)SdmaEngines::Wait(dma_sig[k]);
+  }
 
   // D2H: waits for the oldest slot's DMA, moves its bytes into place and
   // completes the copies waiting on it.
   Status DrainOldest() {
     const size_t k = order.front();
     order.pop_front();
-    Status st = HipStatus(hipEventSynchronize(dma_done[k]), "bounce buffer DMA");
+    Status st = WaitDma(k);
     if (st.ok()) Copy(owed[k]);
     owed[k].clear();
     used[k] = false;
@@ -136,6 +150,8 @@ struct TransferEngine::Bounce {
     }
     cv.notify_all();
     for (std::thread& t : workers) t.join();
+    WaitAllDma();
+    for (hsa_signal_t s : dma_sig) SdmaEngines::DestroySignal(s);
     for (uint8_t* b : bufs) (void)hipHostFree(b);
     for (hipEvent_t e : dma_done) (void)hipEventDestroy(e);
   }
@@ -250,6 +266,7 @@ struct TransferEngine::PageableLane {
     for (hipStream_t s : {ks, cs}) {
       if (s != nullptr) (void)hipStreamSynchronize(s);
     }
+    if (bounce) bounce->WaitAllDma();  // before the staging buffers go
     for (uint64_t b : ring.bufs) (void)hipFree(reinterpret_cast<void*>(b));
     for (hipEvent_t e : ring.ready) (void)hipEventDestroy(e);
     for (hipEvent_t e : ring.free) (void)hipEventDestroy(e);
@@ -334,6 +351,12 @@ TransferEngine::~TransferEngine() {
        {gather_stream_, d2h_stream_, h2d_stream_, scatter_stream_}) {
     if (s != nullptr) (void)hipStreamDestroy(s);
   }
+}
+
+uint32_t TransferEngine::LaneDmaEngines() {
+  std::lock_guard<std::mutex> l(lanes_mu_);
+  if (!sdma_ || (!lanes_[0] && !lanes_[1])) return 0;
+  return (sdma_->engine(/*d2h=*/true) << 16) | sdma_->engine(/*d2h=*/false);
 }
 
 EngineStats TransferEngine::stats() const {
@@ -865,8 +888,93 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
   return CopyFuture::FromEvents({done}, {});
 }
 
+Status TransferEngine::PipelineBounceSdma(const LaneView& lane, Direction dir,
+                                          const std::vector<ChunkWork>& chunks,
+                                          int64_t* memcpys) {
+  const bool d2h = dir == Direction::kD2H;
+  Ring& ring = *lane.ring;
+  Bounce* b = lane.bounce;
+  const SdmaEngines& dma = *b->sdma;
+  // The host orders each DMA against the lane's kernels, since a ROCr copy
+  // waits on no stream: a D2H chunk's DMA starts once its gather has run; an
+  // H2D chunk's scatter is launched once its DMA has landed, one chunk
+  // later, so the next chunk's host fill and DMA overlap that wait.
+  auto segments = [&](const ChunkWork& ch, uint8_t* bb, std::vector<Bounce::Segment>* out) {
+    for (const HostSegment& s : ch.segs) {
+      const size_t bytes = static_cast<size_t>(s.bytes);
+      if (d2h) {
+        out->push_back(Bounce::Segment{s.host, bb + s.off, bytes});
+      } else {
+        out->push_back(Bounce::Segment{bb + s.off, s.host, bytes});
+      }
+    }
+  };
+  if (d2h) {
+    for (const ChunkWork& ch : chunks) {
+      const size_t k = ring.next;
+      ring.next = (ring.next + 1) % ring.bufs.size();
+      const uint64_t buf = ring.bufs[k];
+      // Staging slot k is free once bounce slot k has drained: its last DMA
+      // read the staging buffer.
+      while (b->used[k]) KVX_RETURN_IF_ERROR(b->DrainOldest());
+      KVX_RETURN_IF_ERROR(ch.kernel(buf));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.ready[k], lane.ks));
+      KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(ring.ready[k]));
+      KVX_RETURN_IF_ERROR(dma.Start(/*d2h=*/true, b->bufs[k], reinterpret_cast<void*>(buf),
+                                    static_cast<size_t>(ch.bytes), b->dma_sig[k]));
+      ++*memcpys;
+      segments(ch, b->bufs[k], &b->owed[k]);
+      b->used[k] = true;
+      b->order.push_back(k);
+      ring.used[k] = true;
+    }
+    return OkStatus();
+  }
+  // H2D. On an error return no DMA of this call may still be in flight: the
+  // next call refills the bounce buffers.
+  struct DrainOnError {
+    Bounce* b;
+    bool armed = true;
+    ~DrainOnError() {
+      if (armed) b->WaitAllDma();
+    }
+  } guard{b};
+  const ChunkWork* prev = nullptr;
+  size_t prev_k = 0;
+  auto scatter = [&](const ChunkWork& ch, size_t j) -> Status {
+    KVX_RETURN_IF_ERROR(b->WaitDma(j));
+    KVX_RETURN_IF_ERROR(ch.kernel(ring.bufs[j]));
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[j], lane.ks));
+    return OkStatus();
+  };
+  for (const ChunkWork& ch : chunks) {
+    const size_t k = ring.next;
+    ring.next = (ring.next + 1) % ring.bufs.size();
+    // The slot's last scatter has read the staging buffer (its DMA landed
+    // before that scatter was launched).
+    if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(ring.free[k]));
+    std::vector<Bounce::Segment> segs;
+    segments(ch, b->bufs[k], &segs);
+    b->Copy(segs);
+    KVX_RETURN_IF_ERROR(dma.Start(/*d2h=*/false, reinterpret_cast<void*>(ring.bufs[k]),
+                                  b->bufs[k], static_cast<size_t>(ch.bytes), b->dma_sig[k]));
+    ++*memcpys;
+    b->used[k] = true;
+    ring.used[k] = true;
+    if (prev != nullptr) KVX_RETURN_IF_ERROR(scatter(*prev, prev_k));
+    prev = &ch;
+    prev_k = k;
+  }
+  if (prev != nullptr) KVX_RETURN_IF_ERROR(scatter(*prev, prev_k));
+  guard.armed = false;
+  return OkStatus();
+}
+
 Status TransferEngine::PipelineChunks(const LaneView& lane, Direction dir,
                                       const std::vector<ChunkWork>& chunks, int64_t* memcpys) {
+  if (lane.bounce != nullptr && lane.bounce->sdma != nullptr) {
+    return PipelineBounceSdma(lane, dir, chunks, memcpys);
+  }
   const bool d2h = dir == Direction::kD2H;
   hipStream_t ks = lane.ks;
   hipStream_t cs = lane.cs;
@@ -1246,6 +1354,23 @@ StatusOr<TransferEngine::PageableLane*> TransferEngine::Lane(Direction dir) {
     lane->bounce->used.push_back(false);
     lane->bounce->owed.emplace_back();
     lane->bounce->waiters.emplace_back();
+  }
+  if (!sdma_tried_) {
+    // Fixed SDMA engines for the lanes' DMAs unless KVX_LANE_DMA=hip, or
+    // ROCr cannot provide them (then hipMemcpyAsync).
+    sdma_tried_ = true;
+    const char* mode = std::getenv("KVX_LANE_DMA");
+    if (mode == nullptr || std::string(mode) != "hip") {
+      StatusOr<std::unique_ptr<SdmaEngines>> e = SdmaEngines::Create(opts_.device);
+      if (e.ok()) sdma_ = std::move(e.value());
+    }
+  }
+  if (sdma_) {
+    for (int k = 0; k < opts_.staging_chunks; ++k) {
+      KVX_ASSIGN_OR_RETURN(hsa_signal_t s, SdmaEngines::NewSignal());
+      lane->bounce->dma_sig.push_back(s);
+    }
+    lane->bounce->sdma = sdma_.get();
   }
   PageableLane* raw = lane.get();
   lane->worker = std::thread([this, raw] { LaneLoop(raw); });

@@ -29,6 +29,7 @@
 
 #include "arg_ring.h"
 #include "copy_future.h"
+#include "sdma_engines.h"
 #include "status.h"
 
 namespace kvx {
@@ -186,6 +187,10 @@ class TransferEngine {
   // block size form one piece of the kernel (see block_copy.h).
   int device() const { return opts_.device; }
   EngineStats stats() const;
+  // SDMA engine bits of the pageable lanes' DMAs, (device-to-host << 16) |
+  // host-to-device; 0 while no lane exists or when the lanes use
+  // hipMemcpyAsync.
+  uint32_t LaneDmaEngines();
   // Blocks until both pageable lanes have drained and everything enqueued on
   // the engine's streams has finished.
   Status Synchronize();
@@ -271,6 +276,9 @@ class TransferEngine {
   // memory; they drain when their slot comes round again or the lane idles.
   Status PipelineChunks(const LaneView& lane, Direction dir, const std::vector<ChunkWork>& chunks,
                         int64_t* memcpys);
+  // PipelineChunks of a bounce lane whose DMAs run on fixed SDMA engines.
+  Status PipelineBounceSdma(const LaneView& lane, Direction dir,
+                            const std::vector<ChunkWork>& chunks, int64_t* memcpys);
   // Pool extents through a pageable lane (*done as StagedOnLane).
   Status ExtentsOnLane(const LaneView& lane, Direction dir,
                        const std::vector<StorageView>& storages,
@@ -326,6 +334,10 @@ class TransferEngine {
   std::unique_ptr<ArgRing> extent_args_;  // strided tables of CopyExtents
   std::mutex lanes_mu_;
   std::unique_ptr<PageableLane> lanes_[2];  // by Direction
+  // Engines of the lanes' DMAs (null: hipMemcpyAsync), chosen with the
+  // first lane; destroyed after the lanes.
+  std::unique_ptr<SdmaEngines> sdma_;
+  bool sdma_tried_ = false;
   EngineStats stats_;
 };
 

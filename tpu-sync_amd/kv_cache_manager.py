@@ -747,6 +747,16 @@ class KVCacheManager:
                 "chunks", "zero_copy_copies", "extent_kernel_copies", "bounce_copies")
         return dict(zip(keys, list(out)))
 
+    @property
+    def lane_dma_engines(self) -> Optional[Tuple[int, int]]:
+        """SDMA engine bits (device-to-host, host-to-device) of the pageable
+        lanes' DMAs; None while no lane has run or when they use
+        hipMemcpyAsync."""
+        v = int(_capi.load().kvx_manager_lane_dma_engines(self._h))
+        if v < 0:
+            raise RuntimeError("lane_dma_engines: manager has no transfer engine")
+        return (v >> 16, v & 0xFFFF) if v else None
+
     def kernel_times(self, gather: bool = True, reset: bool = False) -> dict:
         """Profiled launches of the gather (or scatter) kernel: count, total ms
         (HIP events on the kernel's stream) and algorithmic HBM bytes."""
