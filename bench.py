@@ -83,8 +83,9 @@ def parse_args():
                         "memory tier) or pinned (hipHostMalloc)")
     p.add_argument("--zipf-docs", type=int, default=160,
                    help="documents whose hash-chain prefixes the churn requests")
-    p.add_argument("--zipf-chunk-mib", type=int, default=0,
-                   help="staging chunk of the churn's manager (0: --chunk-mib)")
+    p.add_argument("--zipf-chunk-mib", type=int, default=32,
+                   help="staging chunk of the churn's manager (0: --chunk-mib); "
+                        "32 MiB measured best for its 64-2048-block requests")
     p.add_argument("--zipf-host-threads", type=int, default=0,
                    help="host copy threads of the churn's bounce lanes (0: the library's 8)")
     p.add_argument("--zipf-inflight", type=int, default=1,
