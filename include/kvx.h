@@ -65,12 +65,19 @@ extern "C" {
  *   KVX_MODE_ZERO_COPY: one kernel moves the blocks between the pool and the
  *     pinned host mirror directly over PCIe (needs KVX_HOST_PINNED);
  *   KVX_MODE_AUTO: staged when a copy's host runs average at least 4 MiB per
- *     storage, zero-copy below that.
+ *     storage, zero-copy below that;
+ *   KVX_MODE_LANES: short runs of a pinned mirror go through the bounce lanes
+ *     of pageable mirrors (host threads gather and scatter the host side,
+ *     whole staging chunks cross on fixed SDMA engines). A load and a save at
+ *     once then share PCIe as well as two DMAs do (96 against about 80 GB/s
+ *     zero-copy) at the cost of host CPU time and of about 6 % on a lone
+ *     small copy; for callers such as a KV store that issue both together.
  * A pageable mirror (KVX_HOST_MALLOC, KVX_HOST_SHM) is always staged, through
  * the pinned bounce lanes (see host_copy_threads). */
 #define KVX_MODE_AUTO 0
 #define KVX_MODE_STAGED 1
 #define KVX_MODE_ZERO_COPY 2
+#define KVX_MODE_LANES 3
 
 /* Staging orders for kvx_manager_gather / kvx_manager_scatter. */
 #define KVX_LAYER_MAJOR 0 /* [storage][n][block_bytes] */

@@ -4,6 +4,8 @@ manager, non-contiguous or expanded, or spanning more bytes than its storage
 is rejected with ValueError; a column split also needs a contiguous 2-D
 weight and outputs of the weight's dtype. Tensors that claim to be on a
 device are CPU tensors behind a wrapper: the checks run on the host only."""
+import ctypes
+
 import pytest
 
 torch = pytest.importorskip("torch")
@@ -90,3 +92,24 @@ def test_weight_synchronizer_rejects_host_tensors_and_staging(kvx):
             fn(torch.empty(64, dtype=torch.uint8), stream=0)
         with pytest.raises(ValueError, match="device 1"):
             fn(FakeDeviceTensor(torch.empty(64, dtype=torch.uint8), 1), stream=0)
+
+
+@pytest.mark.parametrize("mode,threads,ok", [(3, 0, True), (3, 4, True), (3, -1, False),
+                                             (4, 0, False), (-1, 0, False)])
+def test_transfer_mode_validated_at_create(kvx, mode, threads, ok):
+    """KVX_MODE_LANES needs the lanes' host threads; modes outside 0..3 are
+    rejected before anything is allocated."""
+    lib = kvx._capi.load()
+    cfg = kvx._capi.ManagerConfig()
+    cfg.num_layers, cfg.num_shards = 1, 1
+    cfg.slice_byte_size, cfg.host_blocks = 64, 4
+    cfg.host_alloc = kvx._capi.HOST_MALLOC
+    cfg.transfer_mode = mode
+    cfg.host_copy_threads = threads
+    m = ctypes.c_void_p()
+    rc = lib.kvx_manager_create(ctypes.byref(cfg), ctypes.byref(m))
+    if ok:
+        assert rc == 0, lib.kvx_last_error()
+        lib.kvx_manager_destroy(m)
+    else:
+        assert rc == 3 and not m.value

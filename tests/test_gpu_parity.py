@@ -107,6 +107,9 @@ PATHS = {
     # instead of fixed SDMA engines.
     "bounce_hip": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                        host_alloc="malloc", host_copy_threads=3),
+    # A pinned mirror whose short runs also go through the bounce lanes.
+    "lanes": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                  host_alloc="pinned", transfer_mode="lanes", host_copy_threads=3),
     # Pageable mirror left to the runtime's per-run hipMemcpyAsync.
     "pageable": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                      host_alloc="malloc", host_copy_threads=-1),
@@ -115,7 +118,7 @@ MODES = ["staged", "zero_copy"]
 
 
 @pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "bounce_hip",
-                                  "pageable"])
+                                  "lanes", "pageable"])
 @pytest.mark.parametrize("bb", [32768, 61424, 12992, 1024, 48, 36, 3])
 def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
     if path == "bounce_hip":
@@ -140,16 +143,17 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
         assert mir.transfer(d2h, src, dst, sizes, layer, shard) == 0
         mir.check(mgr, dev)
     stats = mgr.engine_stats()
-    if path in ("staged", "bounce", "bounce_hip", "pageable"):
+    if path in ("staged", "bounce", "bounce_hip", "lanes", "pageable"):
         assert stats["direct_copies"] == 0 and stats["staged_copies"] == 12
         assert stats["chunks"] > 12 or bb < 1024
-        assert stats["bounce_copies"] == (12 if path.startswith("bounce") else 0)
+        lanes = path.startswith("bounce") or path == "lanes"
+        assert stats["bounce_copies"] == (12 if lanes else 0)
     elif path == "zero_copy":
         assert stats["zero_copy_copies"] == 12 and stats["memcpy_calls"] == 0
     else:
         assert stats["staged_copies"] == 0 and stats["zero_copy_copies"] == 0
     # The lanes' DMAs: one SDMA engine bit per direction, or hipMemcpyAsync.
-    if path == "bounce":
+    if path in ("bounce", "lanes"):
         engines = mgr.lane_dma_engines
         assert engines is not None and all(e and e & (e - 1) == 0 for e in engines), engines
     elif path == "bounce_hip":

@@ -55,12 +55,13 @@ SPARSE = {"tag": "sparse", "base": 0, "block_stride": 4096, "num_blocks": 96,
           "regions": [("k", 0, 80, 32, 40, 1), ("s", 3216, 16, 8, 4, 1)]}
 
 
-@pytest.mark.parametrize("host_alloc", ["pinned", "malloc", "malloc_runtime"])
+@pytest.mark.parametrize("host_alloc", ["pinned", "malloc", "malloc_runtime", "pinned_lanes"])
 @pytest.mark.parametrize("pool", [FA, SPARSE], ids=["fa", "sparse"])
 def test_pool_copies_move_exactly_the_live_bytes(kvx, cuda, host_alloc, pool):
     """pinned: the strided kernel reads/writes the mapped mirror; malloc: the
     bounce lane (staging chunks of 48 KiB, so extents split across chunks);
-    malloc_runtime: one pageable hipMemcpyAsync per (storage, extent)."""
+    malloc_runtime: one pageable hipMemcpyAsync per (storage, extent);
+    pinned_lanes: a pinned mirror in transfer_mode "lanes" (the bounce lane)."""
     rng = np.random.default_rng(11)
     nbytes = O.storage_extent_end(pool) + 1000
     nbytes += (-nbytes) % pool["block_stride"]
@@ -69,6 +70,9 @@ def test_pool_copies_move_exactly_the_live_bytes(kvx, cuda, host_alloc, pool):
     kw = {"host_alloc": host_alloc}
     if host_alloc == "malloc":
         kw.update(staging_chunk_bytes=48 << 10, staging_chunks=2)
+    elif host_alloc == "pinned_lanes":
+        kw.update(host_alloc="pinned", transfer_mode="lanes", staging_chunk_bytes=48 << 10,
+                  staging_chunks=2)
     elif host_alloc == "malloc_runtime":
         kw.update(host_alloc="malloc", host_copy_threads=-1)
     mgr = kvx.KVCacheManager([shards], host_blocks_to_allocate=major, **kw)
@@ -82,7 +86,7 @@ def test_pool_copies_move_exactly_the_live_bytes(kvx, cuda, host_alloc, pool):
     after = mgr.engine_stats()
     if host_alloc == "pinned":
         assert after["extent_kernel_copies"] == before["extent_kernel_copies"] + 1
-    elif host_alloc == "malloc":
+    elif host_alloc in ("malloc", "pinned_lanes"):
         # Packed into staging chunks, one DMA per chunk through a bounce lane.
         assert after["bounce_copies"] == before["bounce_copies"] + 1
     else:

@@ -22,7 +22,7 @@ STATUS_NAMES = {
 }
 
 HOST_MALLOC, HOST_PINNED, HOST_SHM, HOST_AUTO = 0, 1, 2, 3
-MODES = {"auto": 0, "staged": 1, "zero_copy": 2}
+MODES = {"auto": 0, "staged": 1, "zero_copy": 2, "lanes": 3}
 LAYER_MAJOR, BLOCK_MAJOR = 0, 1
 
 

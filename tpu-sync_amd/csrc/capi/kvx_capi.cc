@@ -128,8 +128,11 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   if (cfg->staging_chunks > 0) c.engine.staging_chunks = static_cast<int>(cfg->staging_chunks);
   if (cfg->direct_min_bytes > 0) c.engine.direct_min_bytes = cfg->direct_min_bytes;
   c.engine.profile_kernels = cfg->profile_kernels != 0;
-  if (cfg->transfer_mode < KVX_MODE_AUTO || cfg->transfer_mode > KVX_MODE_ZERO_COPY) {
+  if (cfg->transfer_mode < KVX_MODE_AUTO || cfg->transfer_mode > KVX_MODE_LANES) {
     return Fail(KVX_INVALID_ARGUMENT, "unknown transfer_mode");
+  }
+  if (cfg->transfer_mode == KVX_MODE_LANES && cfg->host_copy_threads < 0) {
+    return Fail(KVX_INVALID_ARGUMENT, "transfer_mode lanes needs host copy threads");
   }
   if (cfg->transfer_mode == KVX_MODE_ZERO_COPY && kind != KVX_HOST_PINNED) {
     return Fail(KVX_INVALID_ARGUMENT, "zero-copy transfers need KVX_HOST_PINNED host memory");

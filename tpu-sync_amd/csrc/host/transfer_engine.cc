@@ -565,6 +565,9 @@ StatusOr<CopyFuture> TransferEngine::Copy(
   }
   std::vector<int64_t> cdev, chost;
   KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
+  if (opts_.mode == TransferMode::kLanes && opts_.host_copy_threads > 0) {
+    return CopyPageable(dir, storages, cdev, chost, {}, dep);
+  }
   bool zero_copy = opts_.mode == TransferMode::kZeroCopy;
   if (opts_.mode == TransferMode::kAuto && host_ok) {
     // The staged path costs one hipMemcpyAsync per (storage, host run) and
@@ -730,9 +733,9 @@ StatusOr<CopyFuture> TransferEngine::CopyExtents(
   bool host_ok = true;
   for (const StorageView& s : storages) host_ok = host_ok && s.host_kernel_access;
   if (total == 0 || storages.empty()) return CopyFuture();
-  if (!host_ok && opts_.host_copy_threads > 0) {
-    // Pageable host memory: live bytes packed into staging chunks and
-    // moved through a bounce lane.
+  if ((!host_ok || opts_.mode == TransferMode::kLanes) && opts_.host_copy_threads > 0) {
+    // Pageable host memory (or lanes mode): live bytes packed into staging
+    // chunks and moved through a bounce lane.
     return CopyPageable(dir, storages, {}, {}, extents, dep);
   }
   kernel &= host_ok && any_short;

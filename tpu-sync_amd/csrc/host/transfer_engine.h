@@ -67,9 +67,13 @@ struct ByteExtent {
 //          storage at least auto_staged_min_run_bytes); zero-copy otherwise.
 //          Host memory the GPU cannot map always goes staged (through the
 //          pageable lanes).
+//   kLanes: pinned host memory too goes through the pageable lanes (host
+//          threads move the host side, whole chunks cross on SDMA): a load
+//          and a save at once reach the link's duplex rate, where zero-copy
+//          kernels in both directions interfere.
 // Copies whose runs are all at least direct_min_bytes use one
 // hipMemcpyAsync per (storage, run) in every mode.
-enum class TransferMode : int { kAuto = 0, kStaged = 1, kZeroCopy = 2 };
+enum class TransferMode : int { kAuto = 0, kStaged = 1, kZeroCopy = 2, kLanes = 3 };
 
 struct EngineOptions {
   int device = 0;

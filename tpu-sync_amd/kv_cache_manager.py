@@ -189,8 +189,10 @@ class KVCacheManager:
         "inline".
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
       transfer_mode: "auto" (staged when a copy's host runs average at least
-        4 MiB per storage, zero-copy below), "staged" or "zero_copy" (pinned
-        mirror only); zero_copy_workgroups caps a zero-copy launch.
+        4 MiB per storage, zero-copy below), "staged", "zero_copy" (pinned
+        mirror only) or "lanes" (a pinned mirror's short runs through the
+        bounce lanes, for callers that load and save at once);
+        zero_copy_workgroups caps a zero-copy launch.
       host_copy_threads: a pageable host mirror ("malloc", "shm") moves
         through pinned bounce buffers that this many host threads fill and
         drain (0: 8; -1: per-run pageable copies by the HIP runtime).
