@@ -67,9 +67,9 @@ def parse_args():
                    help="skip the per-mode, one-direction and PCIe-peak measurements")
     p.add_argument("--mode", default="auto", choices=["auto", "staged", "zero_copy"],
                    help="transfer mode of the headline offload/reload loop")
-    p.add_argument("--configs", default="fp8,weights,pools,zipf",
+    p.add_argument("--configs", default="fp8,weights,pools,lanes,zipf",
                    help="comma list of extra workloads to measure after the headline "
-                        "(fp8, weights, pools, zipf; empty for none)")
+                        "(fp8, weights, pools, lanes, zipf; empty for none)")
     p.add_argument("--zipf-host-blocks", type=int, default=0,
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks (0: "
                         "the configured 256 GB budget, capped by free /dev/shm, available "
@@ -91,6 +91,9 @@ def parse_args():
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
                         "request's load and save finish before the next is issued)")
+    p.add_argument("--configs-only", action="store_true",
+                   help="measure only the --configs workloads (no headline, no CPU "
+                        "baseline) and print them; for profiling one of them")
     p.add_argument("--rocpd-summary", metavar="DB",
                    help="print per-kernel (name, grid) duration statistics of a "
                         "rocprofv3 results database and exit")
@@ -155,6 +158,28 @@ def rocpd_summary(db_path):
         for name, cnt, size, avg, tot in rows:
             print(f"{name:<32} {cnt:>6} {size / 1e9:>9.3f} {avg / 1e3:>9.2f} "
                   f"{size / tot if tot else 0:>9.2f}")
+        # How long copies of both directions were in flight together, against
+        # the time any copy was: a load and a save issued at once should
+        # overlap for nearly all of their shorter side.
+        ev = []
+        for name, start, end in cur.execute("select name, start, end from memory_copies"):
+            d = "h2d" if "HOST_TO_DEVICE" in name else ("d2h" if "DEVICE_TO_HOST" in name else None)
+            if d:
+                ev += [(start, 1, d), (end, -1, d)]
+        ev.sort()
+        act = {"h2d": 0, "d2h": 0}
+        both = anyt = 0
+        last = ev[0][0] if ev else 0
+        for ts, k, d in ev:
+            if act["h2d"] and act["d2h"]:
+                both += ts - last
+            if act["h2d"] or act["d2h"]:
+                anyt += ts - last
+            act[d] += k
+            last = ts
+        if anyt:
+            print(f"\ncopies in flight: any {anyt / 1e6:.1f} ms, both directions at once "
+                  f"{both / 1e6:.1f} ms ({both / anyt:.1%})")
 
 
 def timed_events(torch, fn, reps, stream):
@@ -716,6 +741,81 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     return out
 
 
+def bench_lanes(torch, pkg, dev, args, rng):
+    """Loads and saves through the pageable lanes on the Llama-3-70B block
+    shape (160 storages x 32 KiB per block): a 2048-block /dev/shm tier,
+    requests of 64 and 512 random blocks, each direction alone and both at
+    once (a store request issues its load and save together), 32 MiB staging
+    chunks. Median over the repetitions; GB/s counts both directions' bytes."""
+    S, P, bb, HB = 160, 4096, 32768, 2048
+    log(f"lanes: {S} x {P} x {bb} B pool, {HB}-block /dev/shm tier")
+    pools = [torch.empty(P, bb, dtype=torch.uint8, device=dev) for _ in range(S)]
+    for p in pools:
+        p.random_(0, 256)
+    key = f"kvx_lanes_{os.getpid()}"
+    mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=HB, staging_chunk_bytes=32 << 20,
+                             staging_chunks=4, host_alloc="shm", shm_key=key)
+    out = {"workload": "Llama-3-70B block shape (160 storages x 32 KiB), /dev/shm tier of "
+                       f"{HB} blocks, random device and host ids, 32 MiB staging chunks"}
+    for nb, reps in ((64, 12), (512, 6)):
+        t = {"save_ms": [], "load_ms": [], "load_and_save_ms": []}
+        one = [1] * nb
+        for r in range(reps + 1):
+            dev_ids = rng.permutation(P)[:nb].tolist()
+            host_ids = rng.permutation(HB)[:nb].tolist()
+            dev2 = rng.permutation(P)[:nb].tolist()
+            host2 = rng.permutation(HB)[:nb].tolist()
+            t0 = time.perf_counter()
+            mgr.d2h(dev_ids, host_ids, one).Await()
+            a = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            mgr.h2d(host_ids, dev2, one).Await()
+            b = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            f1 = mgr.h2d(host_ids, dev_ids, one)
+            f2 = mgr.d2h(dev2, host2, one)
+            f1.Await()
+            f2.Await()
+            c = time.perf_counter() - t0
+            if r > 0:  # the first round warms the lanes
+                t["save_ms"].append(a * 1e3)
+                t["load_ms"].append(b * 1e3)
+                t["load_and_save_ms"].append(c * 1e3)
+        nbytes = nb * S * bb
+        res = {}
+        for k, v in t.items():
+            med = float(np.median(v))
+            res[k] = round(med, 2)
+            res[k.replace("_ms", "_gbps")] = round((2 if "and" in k else 1) * nbytes / med / 1e6, 2)
+        out[f"requests_of_{nb}_blocks"] = res
+        log(f"lanes {nb} blocks: {res}")
+    out["lane_dma_engines"] = mgr.lane_dma_engines
+    mgr.close()
+    seg = f"/dev/shm/{key}_dev_{dev.index or 0}"
+    if os.path.exists(seg):
+        os.unlink(seg)
+    del pools
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_configs(torch, pkg, dev, args, rng, peaks):
+    configs = {}
+    wanted = [c for c in args.configs.split(",") if c]
+    if "fp8" in wanted:
+        configs["fp8_kv_scales"] = bench_fp8_scales(torch, pkg, dev, args, rng)
+    if "weights" in wanted:
+        configs["weight_sync_pack"] = bench_weight_sync(torch, pkg, dev, args)
+    if "pools" in wanted:
+        configs["sparse_pool_copies"] = bench_pools(torch, pkg, dev, args, rng)
+    if "lanes" in wanted:
+        configs["shm_lanes_load_and_save"] = bench_lanes(torch, pkg, dev, args, rng)
+    if "zipf" in wanted:
+        configs["llama3_70b_zipf_churn"] = bench_zipf_store(torch, pkg, dev, args, rng,
+                                                            peaks=peaks)
+    return configs
+
+
 def main():
     args = parse_args()
     args.sub_steps = max(1, min(args.steps, 20))
@@ -730,6 +830,13 @@ def main():
     sys.path.insert(0, ROOT)
     import __graft_entry__
     pkg = __graft_entry__.load_package()
+    if args.configs_only:
+        # Only the extra workloads (for traces of one of them): no headline,
+        # no CPU baseline; not the benchmark's result line.
+        configs = run_configs(torch, pkg, torch.device("cuda:0"), args,
+                              np.random.default_rng(1), None)
+        print(json.dumps({"configs_only": True, "configs": configs}), flush=True)
+        return
 
     w = WORKLOADS[args.workload]
     L, n, P = w["layers"], w["batch"], w["pool_blocks"]
@@ -878,17 +985,7 @@ def main():
     torch.cuda.empty_cache()
 
     # The other workloads of the path, each measured on its own shape.
-    configs = {}
-    wanted = [c for c in args.configs.split(",") if c]
-    if "fp8" in wanted:
-        configs["fp8_kv_scales"] = bench_fp8_scales(torch, pkg, dev, args, rng)
-    if "weights" in wanted:
-        configs["weight_sync_pack"] = bench_weight_sync(torch, pkg, dev, args)
-    if "pools" in wanted:
-        configs["sparse_pool_copies"] = bench_pools(torch, pkg, dev, args, rng)
-    if "zipf" in wanted:
-        configs["llama3_70b_zipf_churn"] = bench_zipf_store(torch, pkg, dev, args, rng,
-                                                            peaks=measured_peaks)
+    configs = run_configs(torch, pkg, dev, args, rng, measured_peaks)
 
     cpu = None
     if args.cpu_seconds > 0:
