@@ -694,16 +694,22 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     t_run = time.perf_counter() - t0
     moved = (saved + loaded) * S * bb
     # PCIe bound of this request stream: a request's load (H2D) and save (D2H)
-    # run at once, each at most at its direction's measured pinned peak, and
-    # requests follow one another, so the stream needs at least
-    # sum(max(load bytes / H2D peak, save bytes / D2H peak)).
-    pcie_bound = None
+    # run at once, each at most at its direction's measured pinned peak and
+    # together at most at the measured bidirectional peak, and requests
+    # follow one another, so the stream needs at least
+    # sum(max(load / H2D peak, save / D2H peak, (load + save) / bidir peak)).
+    # pcie_bound_per_direction_gbps leaves out the bidirectional term.
+    pcie_bound = pcie_bound_dir = None
     if peaks and inflight == 1:
-        t_min = sum(max(l * S * bb / (peaks["pcie_h2d_gbps"] * 1e9),
-                        sv * S * bb / (peaks["pcie_d2h_gbps"] * 1e9))
-                    for l, sv in per_request)
+        t_dir = t_min = 0.0
+        for l, sv in per_request:
+            tl = l * S * bb / (peaks["pcie_h2d_gbps"] * 1e9)
+            ts = sv * S * bb / (peaks["pcie_d2h_gbps"] * 1e9)
+            t_dir += max(tl, ts)
+            t_min += max(tl, ts, (l + sv) * S * bb / (peaks["pcie_bidir_gbps"] * 1e9))
         if t_min > 0:
             pcie_bound = moved / t_min / 1e9
+            pcie_bound_dir = moved / t_dir / 1e9
     out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
                        "churn through the KV store: requests are prefixes (64-2048 blocks) of "
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
@@ -722,6 +728,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
            "pcie_bound_gbps": round(pcie_bound, 2) if pcie_bound else None,
            "frac_of_pcie_bound": round(moved / t_run / 1e9 / pcie_bound, 4)
                                  if pcie_bound else None,
+           "pcie_bound_per_direction_gbps": round(pcie_bound_dir, 2) if pcie_bound_dir else None,
            "blocks_per_s": round((saved + loaded) / t_run, 1),
            "latency_ms": ({"all_requests": percentiles_ms([t for _, t in latency]),
                            "requests_64_to_127_blocks": percentiles_ms(
