@@ -10,7 +10,7 @@
 #include "../kernels/block_copy.h"
 #include "../kernels/strided_copy.h"
 #include "hip_util.h"
-#include "stream_copy.h"
+#include "host_copy_pool.h"
 
 namespace kvx {
 namespace {
@@ -85,11 +85,7 @@ StatusOr<StagingLayout> DeviceStagingLayout(const std::vector<int64_t>& block_by
 // Pinned bounce buffers of a pageable lane (one per staging-ring slot) and
 // the host threads that move bytes between them and pageable host memory.
 struct TransferEngine::Bounce {
-  struct Segment {
-    uint8_t* dst;
-    const uint8_t* src;
-    size_t bytes;
-  };
+  using Segment = HostCopyPool::Segment;
   std::vector<uint8_t*> bufs;
   std::vector<hipEvent_t> dma_done;  // last DMA into (D2H) or out of (H2D) bufs[k]
   // With fixed SDMA engines (sdma != null) the DMAs are ROCr copies and
@@ -100,6 +96,15 @@ struct TransferEngine::Bounce {
   std::vector<std::vector<Segment>> owed;  // D2H: host copies still due from bufs[k]
   std::vector<std::vector<CopyFuture>> waiters;  // D2H: copies complete once bufs[k] drains
   std::deque<size_t> order;                // D2H: slots with copies owed, oldest first
+  HostCopyPool pool;                       // the lane's host copy threads
+
+  explicit Bounce(int threads) : pool(threads) {}
+  ~Bounce() {
+    WaitAllDma();
+    for (hsa_signal_t s : dma_sig) SdmaEngines::DestroySignal(s);
+    for (uint8_t* b : bufs) (void)hipHostFree(b);
+    for (hipEvent_t e : dma_done) (void)hipEventDestroy(e);
+  }
 
   Status WaitDma(size_t k) {
     if (sdma != nullptr) return SdmaEngines::Wait(dma_sig[k]);
@@ -110,6 +115,8 @@ struct TransferEngine::Bounce {
   void WaitAllDma() {
     for (size_t k = 0; k < dma_sig.size(); ++k) (void)SdmaEngines::Wait(dma_sig[k]);
   }
+  // Moves the segments' bytes with the pool and the calling thread.
+  void Copy(const std::vector<Segment>& segs) { pool.Copy(segs); }
 
   // D2H: waits for the oldest slot's DMA, moves its bytes into place and
   // completes the copies waiting on it.
@@ -138,103 +145,6 @@ struct TransferEngine::Bounce {
     }
     return first;
   }
-
-  // A fixed pool of threads running parallel host copy batches.
-  explicit Bounce(int threads) {
-    for (int t = 0; t < threads; ++t) workers.emplace_back([this] { Work(); });
-  }
-  ~Bounce() {
-    {
-      std::lock_guard<std::mutex> l(mu);
-      stop = true;
-    }
-    cv.notify_all();
-    for (std::thread& t : workers) t.join();
-    WaitAllDma();
-    for (hsa_signal_t s : dma_sig) SdmaEngines::DestroySignal(s);
-    for (uint8_t* b : bufs) (void)hipHostFree(b);
-    for (hipEvent_t e : dma_done) (void)hipEventDestroy(e);
-  }
-  // Copies every segment (split into pieces of at most 4 MiB) with the pool
-  // and the calling thread; returns when all are done.
-  void Copy(const std::vector<Segment>& segs) {
-    constexpr size_t kPiece = 4u << 20;
-    std::vector<Segment> pieces;
-    for (const Segment& s : segs) {
-      for (size_t o = 0; o < s.bytes; o += kPiece) {
-        pieces.push_back(Segment{s.dst + o, s.src + o, std::min(kPiece, s.bytes - o)});
-      }
-    }
-    if (pieces.empty()) return;
-    {
-      std::lock_guard<std::mutex> l(mu);
-      batch = &pieces;
-      next.store(0);
-      left = pieces.size();
-      ++generation;
-    }
-    cv.notify_all();
-    Drain(&pieces);
-    std::unique_lock<std::mutex> l(mu);
-    done_cv.wait(l, [this] { return left == 0 && active == 0; });
-    batch = nullptr;
-  }
-
- private:
-  void Drain(std::vector<Segment>* p) {
-    const size_t n = p->size();
-    // Many small pieces (random blocks of a pageable tier: each crosses
-    // several 4 KiB pages) are taken four at a time, so a thread knows its
-    // next piece and prefetches it while it copies the current one; few
-    // pieces are taken one at a time to keep every thread busy.
-    const size_t take = n >= 64 * (workers.size() + 1) ? 4 : 1;
-    size_t finished = 0;
-    for (size_t i = next.fetch_add(take); i < n; i = next.fetch_add(take)) {
-      const size_t e = std::min(n, i + take);
-      if (take > 1) PrefetchSource((*p)[i].src, (*p)[i].bytes);
-      for (size_t j = i; j < e; ++j) {
-        if (j + 1 < e) PrefetchSource((*p)[j + 1].src, (*p)[j + 1].bytes);
-        // Streaming stores: the DMA engines read and write the same host
-        // memory meanwhile, and the bytes are not read again by this CPU.
-        StreamCopy((*p)[j].dst, (*p)[j].src, (*p)[j].bytes);
-        ++finished;
-      }
-    }
-    // Completion is published under `mu` below; the DMA that reads these
-    // bytes (or the caller that reads the pageable side) comes after it.
-    StreamFence();
-    if (finished > 0) {
-      std::lock_guard<std::mutex> l(mu);
-      left -= finished;
-      if (left == 0 && active == 0) done_cv.notify_all();
-    }
-  }
-  void Work() {
-    uint64_t seen = 0;
-    while (true) {
-      std::vector<Segment>* p = nullptr;
-      {
-        std::unique_lock<std::mutex> l(mu);
-        cv.wait(l, [&] { return stop || (generation != seen && batch != nullptr); });
-        if (stop) return;
-        seen = generation;
-        p = batch;
-        ++active;
-      }
-      Drain(p);
-      std::lock_guard<std::mutex> l(mu);
-      if (--active == 0 && left == 0) done_cv.notify_all();
-    }
-  }
-  std::vector<std::thread> workers;
-  std::mutex mu;
-  std::condition_variable cv, done_cv;
-  std::vector<Segment>* batch = nullptr;
-  std::atomic<size_t> next{0};
-  size_t left = 0;
-  int active = 0;  // workers inside Drain of the current batch
-  uint64_t generation = 0;
-  bool stop = false;
 };
 
 // One direction of pageable-host copies: a worker thread runs queued copies
