@@ -21,11 +21,12 @@ def test_stream_copy_matches_memcpy(tmp_path, avx2):
             if " avx2" not in f.read():
                 pytest.skip("this CPU has no AVX2")
     exe = tmp_path / "stream_copy_check"
+    env = {k: v for k, v in os.environ.items() if k != "LD_PRELOAD"}
     subprocess.run([cxx, "-O2", "-std=c++17", "-Wall", "-Werror", "-I", HOST,
                     f"-DKVX_STREAM_COPY_AVX2={avx2}",
                     os.path.join(ROOT, "tests", "stream_copy_check.cc"),
                     os.path.join(HOST, "stream_copy.cc"), "-o", str(exe)],
-                   check=True, capture_output=True, text=True)
-    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+                   check=True, capture_output=True, text=True, env=env)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "stream copy ok" in r.stdout
