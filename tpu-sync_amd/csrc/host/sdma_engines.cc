@@ -60,8 +60,11 @@ StatusOr<std::unique_ptr<SdmaEngines>> SdmaEngines::Create(int device) {
       hipDeviceGetAttribute(&dev, hipDeviceAttributePciDeviceId, device) != hipSuccess) {
     return FailedPreconditionError("PCI location of the device unknown");
   }
-  // The HIP runtime has initialised ROCr already; this takes a reference.
+  // The HIP runtime has initialised ROCr already; this takes a reference,
+  // which the object gives back.
   KVX_RETURN_IF_ERROR(HsaStatus(hsa_init(), "hsa_init"));
+  std::unique_ptr<SdmaEngines> e(new SdmaEngines());
+  e->hsa_ref_ = true;
   AgentSearch s;
   s.domain = static_cast<uint32_t>(domain);
   s.bus = static_cast<uint32_t>(bus);
@@ -70,7 +73,6 @@ StatusOr<std::unique_ptr<SdmaEngines>> SdmaEngines::Create(int device) {
   if (!s.gpu_found || !s.cpu_found) {
     return NotFoundError("no ROCr agent at the device's PCI location");
   }
-  std::unique_ptr<SdmaEngines> e(new SdmaEngines());
   e->gpu_ = s.gpu;
   e->cpu_ = s.cpu;
   uint32_t avail_h2d = 0, avail_d2h = 0, pref_h2d = 0, pref_d2h = 0;
@@ -89,6 +91,10 @@ StatusOr<std::unique_ptr<SdmaEngines>> SdmaEngines::Create(int device) {
   e->h2d_engine_ = h2d;
   e->d2h_engine_ = d2h;
   return e;
+}
+
+SdmaEngines::~SdmaEngines() {
+  if (hsa_ref_) (void)hsa_shut_down();
 }
 
 Status SdmaEngines::Start(bool d2h, void* dst, const void* src, size_t bytes,

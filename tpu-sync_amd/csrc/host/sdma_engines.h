@@ -28,6 +28,10 @@ class SdmaEngines {
   // device offers two. An error if ROCr cannot provide them; callers then
   // copy with hipMemcpyAsync.
   static StatusOr<std::unique_ptr<SdmaEngines>> Create(int device);
+  // Gives back the ROCr reference Create took (HIP holds its own).
+  ~SdmaEngines();
+  SdmaEngines(const SdmaEngines&) = delete;
+  SdmaEngines& operator=(const SdmaEngines&) = delete;
 
   // Starts a copy of `bytes` from `src` to `dst` on the direction's engine:
   // device memory to pinned host memory (d2h) or the reverse. `done` is set
@@ -45,6 +49,8 @@ class SdmaEngines {
   uint32_t engine(bool d2h) const { return d2h ? d2h_engine_ : h2d_engine_; }
 
  private:
+  SdmaEngines() = default;
+  bool hsa_ref_ = false;
   hsa_agent_t gpu_{};
   hsa_agent_t cpu_{};
   uint32_t h2d_engine_ = 0;
