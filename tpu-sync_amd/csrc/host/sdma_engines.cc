@@ -74,15 +74,21 @@ StatusOr<std::unique_ptr<SdmaEngines>> SdmaEngines::Create(int device) {
     return NotFoundError("no ROCr agent at the device's PCI location");
   }
   e->gpu_ = s.gpu;
-  e->cpu_ = s.cpu;
+  // The host side of the copies: the CPU agent nearest the device when ROCr
+  // names one (the first CPU agent otherwise).
+  hsa_agent_t nearest{};
+  e->cpu_ = hsa_agent_get_info(s.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
+                               &nearest) == HSA_STATUS_SUCCESS && nearest.handle != 0
+                ? nearest
+                : s.cpu;
   uint32_t avail_h2d = 0, avail_d2h = 0, pref_h2d = 0, pref_d2h = 0;
-  KVX_RETURN_IF_ERROR(HsaStatus(hsa_amd_memory_copy_engine_status(s.gpu, s.cpu, &avail_h2d),
+  KVX_RETURN_IF_ERROR(HsaStatus(hsa_amd_memory_copy_engine_status(e->gpu_, e->cpu_, &avail_h2d),
                                 "copy engine status (host to device)"));
-  KVX_RETURN_IF_ERROR(HsaStatus(hsa_amd_memory_copy_engine_status(s.cpu, s.gpu, &avail_d2h),
+  KVX_RETURN_IF_ERROR(HsaStatus(hsa_amd_memory_copy_engine_status(e->cpu_, e->gpu_, &avail_d2h),
                                 "copy engine status (device to host)"));
   // Preferences are hints (0: none); an engine must be available.
-  (void)hsa_amd_memory_get_preferred_copy_engine(s.gpu, s.cpu, &pref_h2d);
-  (void)hsa_amd_memory_get_preferred_copy_engine(s.cpu, s.gpu, &pref_d2h);
+  (void)hsa_amd_memory_get_preferred_copy_engine(e->gpu_, e->cpu_, &pref_h2d);
+  (void)hsa_amd_memory_get_preferred_copy_engine(e->cpu_, e->gpu_, &pref_d2h);
   const uint32_t h2d = LowestBit((pref_h2d & avail_h2d) != 0 ? (pref_h2d & avail_h2d) : avail_h2d);
   uint32_t d2h = LowestBit(pref_d2h & avail_d2h & ~h2d);
   if (d2h == 0) d2h = LowestBit(avail_d2h & ~h2d);
