@@ -101,8 +101,8 @@ struct EngineOptions {
   int64_t auto_staged_min_run_bytes = 4ll << 20;
   // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
   // bounce buffers that this many host threads fill and drain, one lane per
-  // direction with its own streams and staging ring (0: leave such copies to
-  // the runtime's pageable hipMemcpyAsync).
+  // direction with its own streams, staging ring and SDMA engine (0: leave
+  // such copies to the runtime's pageable hipMemcpyAsync).
   int host_copy_threads = 8;
 };
 
