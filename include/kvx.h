@@ -131,6 +131,11 @@ typedef struct kvx_manager_config {
   int32_t host_copy_threads;    /* pageable host mirrors (malloc, shm): host
                                    threads of the pinned bounce lanes; 0 = 8,
                                    -1 = per-run pageable hipMemcpyAsync */
+  int32_t gather_workgroups_per_cu; /* gathers of one block per workgroup
+                                   reserve LDS so at most this many share a
+                                   CU (faster random reads; keeps LDS-heavy
+                                   kernels of other streams off those CUs
+                                   meanwhile); 0 = 2, -1 = no limit */
 } kvx_manager_config;
 
 /* D2h/H2d dispatch (kv_cache_manager_base.cc:452-512, 2575-2630): ENV (0)

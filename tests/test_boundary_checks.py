@@ -113,3 +113,21 @@ def test_transfer_mode_validated_at_create(kvx, mode, threads, ok):
         lib.kvx_manager_destroy(m)
     else:
         assert rc == 3 and not m.value
+
+
+@pytest.mark.parametrize("cap,ok", [(-1, True), (0, True), (1, True), (32, True), (-2, False),
+                                    (33, False)])
+def test_gather_workgroups_per_cu_validated_at_create(kvx, cap, ok):
+    lib = kvx._capi.load()
+    cfg = kvx._capi.ManagerConfig()
+    cfg.num_layers, cfg.num_shards = 1, 1
+    cfg.slice_byte_size, cfg.host_blocks = 64, 4
+    cfg.host_alloc = kvx._capi.HOST_MALLOC
+    cfg.gather_workgroups_per_cu = cap
+    m = ctypes.c_void_p()
+    rc = lib.kvx_manager_create(ctypes.byref(cfg), ctypes.byref(m))
+    if ok:
+        assert rc == 0, lib.kvx_last_error()
+        lib.kvx_manager_destroy(m)
+    else:
+        assert rc == 3 and not m.value

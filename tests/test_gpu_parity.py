@@ -747,16 +747,18 @@ def test_on_ready_callbacks(kvx, cuda):
     qm.close()
 
 
+@pytest.mark.parametrize("cap", [0, -1, 1, 8])
 @pytest.mark.parametrize("layers", [3, 4])
-def test_gather_scatter_every_block_of_the_pool(kvx, cuda, layers):
+def test_gather_scatter_every_block_of_the_pool(kvx, cuda, layers, cap):
     """Maximum size for a pool: all P block ids, permuted, gathered into one
     staging buffer (storage pairs when the storage count is even, storage-
     major when odd) and scattered back under the inverse permutation into a
-    zeroed pool: the pool must come back byte for byte."""
+    zeroed pool: the pool must come back byte for byte. `cap` is the gather's
+    workgroups-per-CU limit (0: the default, -1: none)."""
     rng = np.random.default_rng(24 + layers)
     P, bb = 512, 16384
     host, dev = dev_pools(rng, cuda, layers, 1, P, bb)
-    mgr = make_mgr(kvx, dev, 4)
+    mgr = make_mgr(kvx, dev, 4, gather_workgroups_per_cu=cap)
     perm = rng.permutation(P)
     stg = torch.empty(layers * P * bb, dtype=torch.uint8, device=cuda)
     mgr.gather(perm.tolist(), stg).Await()

@@ -60,6 +60,7 @@ class ManagerConfig(ctypes.Structure):
         ("numa_node", ctypes.c_int32),
         ("dispatch", ctypes.c_int32),
         ("host_copy_threads", ctypes.c_int32),
+        ("gather_workgroups_per_cu", ctypes.c_int32),
     ]
 
 

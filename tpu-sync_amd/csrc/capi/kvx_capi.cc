@@ -171,6 +171,13 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   if (cfg->host_copy_threads != 0) {
     c.engine.host_copy_threads = cfg->host_copy_threads < 0 ? 0 : cfg->host_copy_threads;
   }
+  if (cfg->gather_workgroups_per_cu < -1 || cfg->gather_workgroups_per_cu > 32) {
+    return Fail(KVX_INVALID_ARGUMENT, "gather_workgroups_per_cu must be -1, 0 or 1..32");
+  }
+  if (cfg->gather_workgroups_per_cu != 0) {
+    c.engine.gather_workgroups_per_cu =
+        cfg->gather_workgroups_per_cu < 0 ? 0 : cfg->gather_workgroups_per_cu;
+  }
   if (cfg->zero_copy_workgroups > 0) {
     c.engine.zero_copy_d2h_workgroups = cfg->zero_copy_workgroups;
     c.engine.zero_copy_h2d_workgroups = cfg->zero_copy_workgroups;

@@ -304,8 +304,10 @@ Status TransferEngine::LaunchCopy(const CopyLaunch& l, bool gather, int vec,
     KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.stop));
     KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.start, stream));
   }
+  CopyLaunch cl = l;
+  cl.gather_workgroups_per_cu = opts_.gather_workgroups_per_cu;
   KVX_HIP_RETURN_IF_ERROR(LaunchBlockCopy(
-      l, gather ? CopyDir::kGather : CopyDir::kScatter, vec, stream));
+      cl, gather ? CopyDir::kGather : CopyDir::kScatter, vec, stream));
   ++stats_.kernel_launches;
   if (opts_.profile_kernels) {
     KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.stop, stream));

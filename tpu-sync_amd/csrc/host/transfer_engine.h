@@ -27,6 +27,7 @@
 #include <mutex>
 #include <vector>
 
+#include "../kernels/block_copy.h"
 #include "arg_ring.h"
 #include "copy_future.h"
 #include "sdma_engines.h"
@@ -104,6 +105,9 @@ struct EngineOptions {
   // direction with its own streams, staging ring and SDMA engine (0: leave
   // such copies to the runtime's pageable hipMemcpyAsync).
   int host_copy_threads = 8;
+  // Workgroups of a one-block-per-workgroup gather that may share a CU
+  // (CopyLaunch::gather_workgroups_per_cu; 0: no limit).
+  int gather_workgroups_per_cu = kDefaultGatherWorkgroupsPerCu;
 };
 
 // Where DeviceCopy puts block k of storage s in its staging buffer:

@@ -400,17 +400,23 @@ bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, int* order) {
   return true;
 }
 
+// LDS of one CU on gfx950.
+constexpr uint32_t kLdsPerCu = 160u << 10;
+
 template <typename V, int kUnroll>
-hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, hipStream_t stream) {
+hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, int wg_per_cu,
+                  hipStream_t stream) {
   FastParams F;
   int order = kStorageMajor;
   if (BuildFastParams(P, dir, &F, &order)) {
+    // Gathers reserve (unused) LDS to cap their workgroups per CU.
+    const uint32_t lds = wg_per_cu > 0 ? kLdsPerCu / static_cast<uint32_t>(wg_per_cu) : 0;
     if (dir == CopyDir::kGather && order == kStoragePairs) {
       hipLaunchKernelGGL((block_copy_fast_kernel<V, true, kUnroll, kStoragePairs>), dim3(grid),
-                         dim3(kThreads), 0, stream, F);
+                         dim3(kThreads), lds, stream, F);
     } else if (dir == CopyDir::kGather) {
       hipLaunchKernelGGL((block_copy_fast_kernel<V, true, kUnroll, kStorageMajor>), dim3(grid),
-                         dim3(kThreads), 0, stream, F);
+                         dim3(kThreads), lds, stream, F);
     } else if (order == kAllStorages) {
       hipLaunchKernelGGL((block_copy_fast_kernel<V, false, kUnroll, kAllStorages>), dim3(grid),
                          dim3(kThreads), 0, stream, F);
@@ -456,13 +462,17 @@ hipError_t LaunchBlockCopy(const CopyLaunch& l, CopyDir dir, int vec_bytes,
   KParams P;
   uint32_t grid = 0;
   if (!BuildParams(l, vec_bytes, &P, &grid)) return hipErrorInvalidValue;
+  if (l.gather_workgroups_per_cu < 0 || l.gather_workgroups_per_cu > 32) {
+    return hipErrorInvalidValue;
+  }
+  const int cap = l.gather_workgroups_per_cu;
   switch (vec_bytes) {
     case 16:
-      return Launch<u32x4, 8>(P, grid, dir, stream);
+      return Launch<u32x4, 8>(P, grid, dir, cap, stream);
     case 4:
-      return Launch<uint32_t, 8>(P, grid, dir, stream);
+      return Launch<uint32_t, 8>(P, grid, dir, cap, stream);
     case 1:
-      return Launch<uint8_t, 8>(P, grid, dir, stream);
+      return Launch<uint8_t, 8>(P, grid, dir, cap, stream);
     default:
       return hipErrorInvalidValue;
   }

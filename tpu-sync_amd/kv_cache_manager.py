@@ -196,6 +196,10 @@ class KVCacheManager:
       host_copy_threads: a pageable host mirror ("malloc", "shm") moves
         through pinned bounce buffers that this many host threads fill and
         drain (0: 8; -1: per-run pageable copies by the HIP runtime).
+      gather_workgroups_per_cu: gathers of one block per workgroup reserve
+        LDS so that at most this many share a CU, which serves their random
+        reads faster but keeps LDS-heavy kernels of other streams off those
+        CUs while they run (0: 2; -1: no limit).
       The remaining reference arguments (ports, worker id, timeout,
       parallelism, unsafe_skip_buffer_lock) configure its networking, which
       this single-GPU build does not have; they are accepted and ignored.
@@ -215,7 +219,8 @@ class KVCacheManager:
                  model_uid: Optional[str] = None, profile_kernels: bool = False,
                  transfer_mode: str = "auto", zero_copy_workgroups: int = 0,
                  scale_tables: Optional[List[Any]] = None, numa: Any = "auto",
-                 dispatch: str = "env", host_copy_threads: int = 0):
+                 dispatch: str = "env", host_copy_threads: int = 0,
+                 gather_workgroups_per_cu: int = 0):
         if host_blocks_to_allocate is None:
             if max_blocks is None or num_slots is None:
                 raise ValueError("Must specify either (max_blocks, num_slots) or"
@@ -251,7 +256,7 @@ class KVCacheManager:
                    host_blocks_to_allocate, host_alloc, staging_chunk_bytes,
                    staging_chunks, direct_min_bytes, shm_key, shm_server_name,
                    model_uid, profile_kernels, transfer_mode, zero_copy_workgroups, numa,
-                   dispatch, host_copy_threads)
+                   dispatch, host_copy_threads, gather_workgroups_per_cu)
         self.node_id = node_id
         if max_blocks is not None and num_slots is not None:
             # kv_cache_manager_with_transfer.cc:483-503: slot geometry, then
@@ -294,7 +299,8 @@ class KVCacheManager:
               slice_byte_size, host_blocks, host_alloc, chunk_bytes, chunks,
               direct_min_bytes, shm_key, shm_server_name, model_uid,
               profile_kernels=False, transfer_mode="auto", zero_copy_workgroups=0,
-              numa="auto", dispatch="env", host_copy_threads=0):
+              numa="auto", dispatch="env", host_copy_threads=0,
+              gather_workgroups_per_cu=0):
         lib = _capi.load()
         kinds = {"malloc": _capi.HOST_MALLOC, "pinned": _capi.HOST_PINNED,
                  "shm": _capi.HOST_SHM, None: _capi.HOST_AUTO}
@@ -322,6 +328,7 @@ class KVCacheManager:
         cfg.zero_copy_workgroups = zero_copy_workgroups
         cfg.dispatch = {"env": 0, "queued": 1, "inline": 2}[dispatch]
         cfg.host_copy_threads = host_copy_threads
+        cfg.gather_workgroups_per_cu = gather_workgroups_per_cu
         if numa == "auto":
             cfg.numa_policy = 0
         elif numa in ("off", None):
