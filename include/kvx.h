@@ -131,7 +131,7 @@ typedef struct kvx_manager_config {
   int32_t host_copy_threads;    /* pageable host mirrors (malloc, shm): host
                                    threads of the pinned bounce lanes; 0 = 8,
                                    -1 = per-run pageable hipMemcpyAsync */
-  int32_t gather_workgroups_per_cu; /* gathers of one block per workgroup
+  int32_t gather_workgroups_per_cu; /* device gathers (not zero-copy ones)
                                    reserve LDS so at most this many share a
                                    CU (faster random reads; keeps LDS-heavy
                                    kernels of other streams off those CUs

@@ -56,14 +56,14 @@ struct CopyLaunch {
   // consecutive blocks, which leaves CUs free for other work (a PCIe-bound
   // zero-copy kernel needs only a few hundred workgroups in flight).
   int64_t max_workgroups = 0;
-  // Gathers of one block per workgroup (the common launch) reserve LDS so
-  // that at most this many of their workgroups share a CU (0: no limit).
-  // Fewer random 32 KiB reads in flight per CU let the DRAM serve them more
-  // efficiently: 2 measured 74.5 -> 76.0 % of HBM peak for 512 x 64 blocks
-  // of 32 KiB (1 and 3 the same, 4 and 6 no gain; the scatter gains
-  // nothing). The LDS is not used, but while such a gather runs it keeps
-  // LDS-hungry kernels of other streams off its CUs; 0 leaves every CU's
-  // LDS to them.
+  // Gathers (other than capped zero-copy grids) reserve LDS so that at most
+  // this many of their workgroups share a CU (0: no limit). Fewer random
+  // reads in flight per CU let the DRAM serve them more efficiently: 2
+  // measured 74.5 -> 76.0 % of HBM peak for 512 x 64 blocks of 32 KiB (1 and
+  // 3 the same, 4 and 6 no gain) and 67.2 -> 69.9 % for fp8 payload (16 KiB)
+  // + scales; the scatter gains nothing. The LDS is not used, but while such
+  // a gather runs it keeps LDS-hungry kernels of other streams off its CUs;
+  // 0 leaves every CU's LDS to them.
   int32_t gather_workgroups_per_cu = kDefaultGatherWorkgroupsPerCu;
 };
 

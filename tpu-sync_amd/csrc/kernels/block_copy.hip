@@ -403,9 +403,12 @@ bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, int* order) {
 // LDS of one CU on gfx950.
 constexpr uint32_t kLdsPerCu = 160u << 10;
 
+// LDS the general kernel declares (the small-block path's address tables).
+constexpr uint32_t kStaticLds = 2 * kSmallMaxBlocks * sizeof(uint64_t);
+
 template <typename V, int kUnroll>
 hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, int wg_per_cu,
-                  hipStream_t stream) {
+                  bool capped_grid, hipStream_t stream) {
   FastParams F;
   int order = kStorageMajor;
   if (BuildFastParams(P, dir, &F, &order)) {
@@ -427,8 +430,13 @@ hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, int wg_per_cu,
     return hipGetLastError();
   }
   if (dir == CopyDir::kGather) {
+    // HBM-bound gathers (not the capped grids of zero-copy copies) take the
+    // same cap, minus the kernel's own 4 KiB of address tables.
+    const uint32_t glds = wg_per_cu > 0 && !capped_grid
+                              ? kLdsPerCu / static_cast<uint32_t>(wg_per_cu) - kStaticLds
+                              : 0;
     hipLaunchKernelGGL((block_copy_kernel<V, true, kUnroll>), dim3(grid),
-                       dim3(kThreads), 0, stream, P);
+                       dim3(kThreads), glds, stream, P);
   } else {
     hipLaunchKernelGGL((block_copy_kernel<V, false, kUnroll>), dim3(grid),
                        dim3(kThreads), 0, stream, P);
@@ -468,11 +476,11 @@ hipError_t LaunchBlockCopy(const CopyLaunch& l, CopyDir dir, int vec_bytes,
   const int cap = l.gather_workgroups_per_cu;
   switch (vec_bytes) {
     case 16:
-      return Launch<u32x4, 8>(P, grid, dir, cap, stream);
+      return Launch<u32x4, 8>(P, grid, dir, cap, l.max_workgroups > 0, stream);
     case 4:
-      return Launch<uint32_t, 8>(P, grid, dir, cap, stream);
+      return Launch<uint32_t, 8>(P, grid, dir, cap, l.max_workgroups > 0, stream);
     case 1:
-      return Launch<uint8_t, 8>(P, grid, dir, cap, stream);
+      return Launch<uint8_t, 8>(P, grid, dir, cap, l.max_workgroups > 0, stream);
     default:
       return hipErrorInvalidValue;
   }

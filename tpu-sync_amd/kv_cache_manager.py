@@ -196,7 +196,7 @@ class KVCacheManager:
       host_copy_threads: a pageable host mirror ("malloc", "shm") moves
         through pinned bounce buffers that this many host threads fill and
         drain (0: 8; -1: per-run pageable copies by the HIP runtime).
-      gather_workgroups_per_cu: gathers of one block per workgroup reserve
+      gather_workgroups_per_cu: device gathers (not zero-copy ones) reserve
         LDS so that at most this many share a CU, which serves their random
         reads faster but keeps LDS-heavy kernels of other streams off those
         CUs while they run (0: 2; -1: no limit).
