@@ -58,7 +58,8 @@ int StridedVectorBytes(const std::vector<StridedCopy>& copies);
 // Launches the copy of a device-resident table of `n` entries (built by
 // BuildStridedTable, `tiles` from its *grid) on `stream`. max_workgroups > 0
 // caps the grid (each workgroup then walks tiles with a stride of the grid),
-// for copies bound by PCIe rather than HBM.
+// for copies bound by PCIe rather than HBM; otherwise the launch reserves
+// LDS so that at most 2 of its workgroups share a CU.
 hipError_t LaunchStridedCopy(const StridedEntryDev* table_dev, uint32_t n,
                              uint32_t tiles, int vec_bytes, hipStream_t stream,
                              uint32_t max_workgroups = 0);
