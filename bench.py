@@ -700,16 +700,32 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     # sum(max(load / H2D peak, save / D2H peak, (load + save) / bidir peak)).
     # pcie_bound_per_direction_gbps leaves out the bidirectional term.
     pcie_bound = pcie_bound_dir = None
+    small_vs_bound = None
     if peaks and inflight == 1:
         t_dir = t_min = 0.0
+        req_bound = []  # each request's own PCIe time at the measured peaks
         for l, sv in per_request:
             tl = l * S * bb / (peaks["pcie_h2d_gbps"] * 1e9)
             ts = sv * S * bb / (peaks["pcie_d2h_gbps"] * 1e9)
             t_dir += max(tl, ts)
-            t_min += max(tl, ts, (l + sv) * S * bb / (peaks["pcie_bidir_gbps"] * 1e9))
+            req_bound.append(max(tl, ts, (l + sv) * S * bb / (peaks["pcie_bidir_gbps"] * 1e9)))
+            t_min += req_bound[-1]
         if t_min > 0:
             pcie_bound = moved / t_min / 1e9
             pcie_bound_dir = moved / t_dir / 1e9
+        # Small requests (64-127 blocks): latency against the request's own
+        # PCIe time, which separates per-request overhead from bytes moved.
+        small = [(t, b, l + sv) for (nb, t), b, (l, sv) in zip(latency, req_bound, per_request)
+                 if nb < 128 and b > 0]
+        if small:
+            ratios = sorted(t / b for t, b, _ in small)
+            over_ms = sorted((t - b) * 1e3 for t, b, _ in small)
+            small_vs_bound = {
+                "count": len(small),
+                "median_blocks_moved": int(np.median([m for _, _, m in small])),
+                "median_pcie_bound_ms": round(float(np.median([b for _, b, _ in small])) * 1e3, 2),
+                "median_latency_over_bound": round(ratios[len(ratios) // 2], 3),
+                "median_ms_above_bound": round(over_ms[len(over_ms) // 2], 2)}
     out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
                        "churn through the KV store: requests are prefixes (64-2048 blocks) of "
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
@@ -733,7 +749,8 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
            "latency_ms": ({"all_requests": percentiles_ms([t for _, t in latency]),
                            "requests_64_to_127_blocks": percentiles_ms(
                                [t for nb, t in latency if nb < 128])}
-                          if latency else None)}
+                          if latency else None),
+           "requests_64_to_127_blocks_vs_pcie_bound": small_vs_bound}
     log(f"zipf: {out}")
     mgr.close()
     store.close()
@@ -840,8 +857,10 @@ def main():
     if args.configs_only:
         # Only the extra workloads (for traces of one of them): no headline,
         # no CPU baseline; not the benchmark's result line.
-        configs = run_configs(torch, pkg, torch.device("cuda:0"), args,
-                              np.random.default_rng(1), None)
+        dev = torch.device("cuda:0")
+        # The churn's PCIe bound needs the link's measured peaks.
+        peaks = pcie_peaks(torch, dev) if "zipf" in args.configs.split(",") else None
+        configs = run_configs(torch, pkg, dev, args, np.random.default_rng(1), peaks)
         print(json.dumps({"configs_only": True, "configs": configs}), flush=True)
         return
 
