@@ -851,6 +851,19 @@ typedef struct kvx_strided_entry {
 int kvx_copy_strided(int32_t device, const kvx_strided_entry* entries, int64_t n,
                      void* stream, kvx_future** out);
 
+/* The same entries with their device table built and uploaded once (no
+ * reference counterpart: PushWeightsResharded expands the same entries on
+ * every push, weight_synchronizer_base.cc:626-666). create validates the
+ * entries as kvx_copy_strided does, then allocates and uploads the table;
+ * run is one launch on `stream` with no host table work; destroy waits for
+ * the plan's runs still in flight. The addresses the entries name must stay
+ * valid while the plan is run. */
+typedef struct kvx_strided_plan kvx_strided_plan;
+int kvx_strided_plan_create(int32_t device, const kvx_strided_entry* entries, int64_t n,
+                            kvx_strided_plan** out);
+int kvx_strided_plan_run(kvx_strided_plan* p, void* stream, kvx_future** out);
+void kvx_strided_plan_destroy(kvx_strided_plan* p);
+
 /*
  * Raw device kernels (no manager): gather / scatter block ids of W storages.
  * storage_table: device array of W uint64 base addresses; ids: device array

@@ -131,3 +131,30 @@ def test_gather_workgroups_per_cu_validated_at_create(kvx, cap, ok):
         lib.kvx_manager_destroy(m)
     else:
         assert rc == 3 and not m.value
+
+
+def test_strided_plan_validates_entries_before_the_device(kvx):
+    """kvx_strided_plan_create rejects what kvx_copy_strided rejects (empty
+    rows, negative strides, overlapping destination rows, a null array) with
+    INVALID_ARGUMENT before it touches a device; an empty plan needs none."""
+    lib = kvx._capi.load()
+
+    def create(entries, n=None):
+        arr = (kvx._capi.StridedEntryC * max(len(entries), 1))()
+        for a, e in zip(arr, entries):
+            a.src, a.dst, a.size_bytes, a.count, a.src_stride_bytes, a.dst_stride_bytes = e
+        p = ctypes.c_void_p()
+        rc = lib.kvx_strided_plan_create(0, arr, len(entries) if n is None else n,
+                                         ctypes.byref(p))
+        return rc, p
+
+    for bad in [(1, 2, 0, 1, 0, 0), (1, 2, 64, 1, -1, 0), (1, 2, 64, 3, 64, 32)]:
+        rc, p = create([bad])
+        assert rc == 3 and not p.value, bad
+        assert lib.kvx_last_error()
+    rc, p = create([], n=-1)
+    assert rc == 3 and not p.value
+    rc, p = create([])
+    assert rc == 0 and p.value
+    lib.kvx_strided_plan_destroy(p)
+    assert lib.kvx_strided_plan_create(0, None, 0, None) == 3

@@ -55,6 +55,59 @@ def test_strided_copy_random_entries_match_oracle(kvx, cuda):
         assert np.array_equal(u8(dst), want), align
 
 
+def test_strided_plan_matches_oracle_on_every_run(kvx, cuda):
+    """A StridedPlan's device table (uploaded once) gives the oracle's bytes on
+    every run: random entries of each vector width, three runs into cleared
+    outputs, runs on two streams at once (disjoint outputs), an empty plan,
+    and a plan closed while its last run may still be in flight."""
+    rng = np.random.default_rng(11)
+    src_np = rng.integers(0, 256, 1 << 21, dtype=np.uint8)
+    src = torch.from_numpy(src_np).to(cuda)
+    streams = [torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)]
+    for align in (16, 8, 4, 2, 1):
+        dsts = [torch.zeros(1 << 21, dtype=torch.uint8, device=cuda) for _ in range(2)]
+        wants = [np.zeros(1 << 21, np.uint8) for _ in range(2)]
+        plans = []
+        for dst, want in zip(dsts, wants):
+            entries, ora, dpos = [], [], 0
+            for _ in range(int(rng.integers(2, 30))):
+                size = int(rng.integers(1, 300)) * align
+                count = int(rng.integers(1, 10))
+                s_stride = size + int(rng.integers(0, 5)) * align
+                d_stride = size + int(rng.integers(0, 3)) * align
+                s_off = int(rng.integers(0, 1000)) * align
+                if s_off + (count - 1) * s_stride + size > src_np.size:
+                    continue
+                if dpos + (count - 1) * d_stride + size > want.size:
+                    break
+                entries.append(kvx.StridedEntry(src.data_ptr() + s_off, dst.data_ptr() + dpos,
+                                                size, count, s_stride, d_stride))
+                ora.append((s_off, dpos, size, count, s_stride, d_stride))
+                dpos += (count - 1) * d_stride + size
+                dpos = (dpos + align - 1) // align * align
+            W.apply_entries(src_np, want, ora)
+            plans.append(kvx.StridedPlan(entries))
+        for run in range(3):
+            for dst in dsts:
+                dst.zero_()
+            torch.cuda.synchronize()
+            futs = [kvx.copy_strided(p, stream=s, device=0) for p, s in zip(plans, streams)]
+            for f in futs:
+                f.Await()
+            for dst, want in zip(dsts, wants):
+                assert np.array_equal(u8(dst), want), (align, run)
+        # Closing right after a run: the plan waits for it before freeing.
+        dsts[0].zero_()
+        torch.cuda.synchronize()
+        kvx.copy_strided(plans[0], stream=streams[0], device=0)
+        plans[0].close()
+        assert np.array_equal(u8(dsts[0]), wants[0]), align
+        plans[1].close()
+    empty = kvx.StridedPlan([])
+    kvx.copy_strided(empty, device=0).Await()  # no launch; completes at once
+    empty.close()
+
+
 def _tensors(rng, cuda, sizes, dtype=torch.bfloat16):
     out = []
     for n in sizes:

@@ -355,6 +355,10 @@ PROTOTYPES = {
                                             ctypes.POINTER(ctypes.c_double), _i64p]),
     "kvx_copy_strided": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64, _vp,
                                 ctypes.POINTER(_vp)]),
+    "kvx_strided_plan_create": (_int, [_i32, ctypes.POINTER(StridedEntryC), _i64,
+                                       ctypes.POINTER(_vp)]),
+    "kvx_strided_plan_run": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "kvx_strided_plan_destroy": (None, [_vp]),
     "kvx_manager_numa_node": (_i32, [_vp]),
     "kvx_manager_host_ptr": (_u64, [_vp, _i64, _i64]),
     "kvx_manager_host_size": (_i64, [_vp, _i64, _i64]),

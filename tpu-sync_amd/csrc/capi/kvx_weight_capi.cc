@@ -9,6 +9,10 @@ struct kvx_weight_sync {
   std::unique_ptr<kvx::WeightSynchronizer> impl;
 };
 
+struct kvx_strided_plan {
+  std::unique_ptr<kvx::StridedCopyPlan> impl;
+};
+
 namespace {
 
 using kvx_capi::BadArray;
@@ -18,6 +22,31 @@ using kvx_capi::Fail;
 int Emit(kvx::StatusOr<kvx::CopyFuture> r, kvx_future** out) {
   if (!r.ok()) return Fail(r.status());
   *out = new kvx_future{std::move(r).value()};
+  return KVX_OK;
+}
+
+// Validates the C entries and converts them (offsets folded into addresses).
+int ToCopies(const kvx_strided_entry* entries, int64_t n, std::vector<kvx::StridedCopy>* out) {
+  if (BadArray(entries, n)) return Fail(KVX_INVALID_ARGUMENT, "bad arguments");
+  out->assign(static_cast<size_t>(n), kvx::StridedCopy{});
+  for (int64_t i = 0; i < n; ++i) {
+    const kvx_strided_entry& e = entries[i];
+    if (e.size_bytes <= 0 || e.src_stride_bytes < 0 || e.dst_stride_bytes < 0) {
+      return Fail(KVX_INVALID_ARGUMENT, "entry sizes and strides must be non-negative, size > 0");
+    }
+    const int64_t count = e.count > 0 ? e.count : 1;
+    // Rows of one entry must not overlap in the destination.
+    if (count > 1 && e.dst_stride_bytes < e.size_bytes) {
+      return Fail(KVX_INVALID_ARGUMENT, "destination rows overlap (dst_stride < size)");
+    }
+    kvx::StridedCopy& c = (*out)[static_cast<size_t>(i)];
+    c.src = e.src + static_cast<uint64_t>(e.src_offset_bytes);
+    c.dst = e.dst + static_cast<uint64_t>(e.dst_offset_bytes);
+    c.size = e.size_bytes;
+    c.count = count;
+    c.src_stride = e.src_stride_bytes;
+    c.dst_stride = e.dst_stride_bytes;
+  }
   return KVX_OK;
 }
 
@@ -129,26 +158,31 @@ int kvx_weight_sync_kernel_times(kvx_weight_sync* w, int32_t pack, int32_t reset
 
 int kvx_copy_strided(int32_t device, const kvx_strided_entry* entries, int64_t n,
                      void* stream, kvx_future** out) {
-  if (out == nullptr || BadArray(entries, n)) return Fail(KVX_INVALID_ARGUMENT, "bad arguments");
-  std::vector<kvx::StridedCopy> copies(static_cast<size_t>(n));
-  for (int64_t i = 0; i < n; ++i) {
-    const kvx_strided_entry& e = entries[i];
-    if (e.size_bytes <= 0 || e.src_stride_bytes < 0 || e.dst_stride_bytes < 0) {
-      return Fail(KVX_INVALID_ARGUMENT, "entry sizes and strides must be non-negative, size > 0");
-    }
-    const int64_t count = e.count > 0 ? e.count : 1;
-    // Rows of one entry must not overlap in the destination.
-    if (count > 1 && e.dst_stride_bytes < e.size_bytes) {
-      return Fail(KVX_INVALID_ARGUMENT, "destination rows overlap (dst_stride < size)");
-    }
-    copies[i].src = e.src + static_cast<uint64_t>(e.src_offset_bytes);
-    copies[i].dst = e.dst + static_cast<uint64_t>(e.dst_offset_bytes);
-    copies[i].size = e.size_bytes;
-    copies[i].count = count;
-    copies[i].src_stride = e.src_stride_bytes;
-    copies[i].dst_stride = e.dst_stride_bytes;
-  }
+  if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "bad arguments");
+  std::vector<kvx::StridedCopy> copies;
+  const int rc = ToCopies(entries, n, &copies);
+  if (rc != KVX_OK) return rc;
   return Emit(kvx::CopyStridedOnDevice(device, copies, static_cast<hipStream_t>(stream)), out);
 }
+
+int kvx_strided_plan_create(int32_t device, const kvx_strided_entry* entries, int64_t n,
+                            kvx_strided_plan** out) {
+  if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
+  *out = nullptr;
+  std::vector<kvx::StridedCopy> copies;
+  const int rc = ToCopies(entries, n, &copies);
+  if (rc != KVX_OK) return rc;
+  auto p = kvx::StridedCopyPlan::Create(device, copies);
+  if (!p.ok()) return Fail(p.status());
+  *out = new kvx_strided_plan{std::move(p).value()};
+  return KVX_OK;
+}
+
+int kvx_strided_plan_run(kvx_strided_plan* p, void* stream, kvx_future** out) {
+  if (p == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  return Emit(p->impl->Run(static_cast<hipStream_t>(stream)), out);
+}
+
+void kvx_strided_plan_destroy(kvx_strided_plan* p) { delete p; }
 
 }  // extern "C"

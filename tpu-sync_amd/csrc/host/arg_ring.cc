@@ -88,6 +88,16 @@ Status ArgRing::Commit(int64_t off, int64_t bytes, hipStream_t stream) {
   return OkStatus();
 }
 
+void WriteStridedImage(const std::vector<StridedEntryDev>& table, uint32_t grid, uint8_t* out) {
+  const size_t tbytes = table.size() * sizeof(StridedEntryDev);
+  std::memcpy(out, table.data(), tbytes);
+  uint32_t* map = reinterpret_cast<uint32_t*>(out + tbytes);
+  for (size_t e = 0; e < table.size(); ++e) {
+    const uint32_t end = e + 1 < table.size() ? table[e + 1].tile_begin : grid;
+    for (uint32_t t = table[e].tile_begin; t < end; ++t) map[t] = static_cast<uint32_t>(e);
+  }
+}
+
 Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& copies,
                                 hipStream_t stream, uint32_t max_workgroups,
                                 hipEvent_t kernel_start) {
@@ -98,17 +108,11 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
   if (!BuildStridedTable(copies, vec, &table, &grid)) {
     return InvalidArgumentError("strided copy entry out of the kernel's limits");
   }
-  const int64_t tbytes = static_cast<int64_t>(table.size() * sizeof(StridedEntryDev));
-  const int64_t bytes = tbytes + static_cast<int64_t>(grid) * 4;
+  const int64_t bytes = StridedImageBytes(table.size(), grid);
   KVX_ASSIGN_OR_RETURN(int64_t off, ring.Alloc(bytes));
   ArgSliceGuard keep([&ring, off, bytes, stream] { return ring.Commit(off, bytes, stream); },
                      stream);
-  std::memcpy(ring.host(off), table.data(), static_cast<size_t>(tbytes));
-  uint32_t* map = reinterpret_cast<uint32_t*>(ring.host(off) + tbytes);
-  for (size_t e = 0; e < table.size(); ++e) {
-    const uint32_t end = e + 1 < table.size() ? table[e + 1].tile_begin : grid;
-    for (uint32_t t = table[e].tile_begin; t < end; ++t) map[t] = static_cast<uint32_t>(e);
-  }
+  WriteStridedImage(table, grid, ring.host(off));
   KVX_RETURN_IF_ERROR(ring.Upload(off, bytes, stream));
   if (kernel_start != nullptr) KVX_HIP_RETURN_IF_ERROR(hipEventRecord(kernel_start, stream));
   KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(

@@ -83,6 +83,14 @@ class ArgSliceGuard {
   bool done_ = false;
 };
 
+// The device image a strided launch reads: the entry table followed by the
+// tile -> entry map (one uint32 per workgroup of `grid`).
+inline int64_t StridedImageBytes(size_t entries, uint32_t grid) {
+  return static_cast<int64_t>(entries * sizeof(StridedEntryDev)) + static_cast<int64_t>(grid) * 4;
+}
+// Writes that image to `out` (StridedImageBytes(table.size(), grid) bytes).
+void WriteStridedImage(const std::vector<StridedEntryDev>& table, uint32_t grid, uint8_t* out);
+
 // Uploads the table and tile map of `copies` through `ring` and launches the
 // strided-copy kernel on `stream` (at most max_workgroups workgroups when
 // > 0); the ring region stays reserved until the launch ends. A non-null

@@ -317,4 +317,61 @@ StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCo
   return CopyFuture::FromEvents({done}, {});
 }
 
+StatusOr<std::unique_ptr<StridedCopyPlan>> StridedCopyPlan::Create(
+    int device, const std::vector<StridedCopy>& copies) {
+  std::unique_ptr<StridedCopyPlan> p(new StridedCopyPlan());
+  p->device_ = device;
+  std::vector<StridedEntryDev> table;
+  if (!copies.empty()) {
+    p->vec_ = StridedVectorBytes(copies);
+    if (!BuildStridedTable(copies, p->vec_, &table, &p->grid_)) {
+      return InvalidArgumentError("strided copy entry out of the kernel's limits");
+    }
+  }
+  p->n_ = static_cast<uint32_t>(table.size());
+  if (p->grid_ == 0) return p;
+  DeviceGuard g(device);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  std::vector<uint8_t> image(static_cast<size_t>(StridedImageBytes(table.size(), p->grid_)));
+  WriteStridedImage(table, p->grid_, image.data());
+  KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p->image_, image.size()));
+  KVX_HIP_RETURN_IF_ERROR(
+      hipMemcpy(p->image_, image.data(), image.size(), hipMemcpyHostToDevice));
+  return p;
+}
+
+StridedCopyPlan::~StridedCopyPlan() {
+  DeviceGuard g(device_);
+  for (hipEvent_t e : runs_) {
+    (void)hipEventSynchronize(e);
+    (void)hipEventDestroy(e);
+  }
+  if (image_ != nullptr) (void)hipFree(image_);
+}
+
+StatusOr<CopyFuture> StridedCopyPlan::Run(hipStream_t stream) {
+  DeviceGuard g(device_);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  std::lock_guard<std::mutex> l(mu_);
+  if (grid_ > 0) {
+    // Runs that have finished no longer read the image.
+    for (auto it = runs_.begin(); it != runs_.end();) {
+      if (hipEventQuery(*it) == hipSuccess) {
+        (void)hipEventDestroy(*it);
+        it = runs_.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    KVX_ASSIGN_OR_RETURN(hipEvent_t ran, NewEvent());
+    runs_.push_back(ran);
+    KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(static_cast<const StridedEntryDev*>(image_), n_,
+                                              grid_, vec_, stream));
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ran, stream));
+  }
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
+  return CopyFuture::FromEvents({done}, {});
+}
+
 }  // namespace kvx

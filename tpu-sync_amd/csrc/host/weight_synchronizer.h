@@ -15,7 +15,8 @@
 //     reference issues.
 // Pack / Unpack run the same kernel against a caller device buffer laid out
 // by the offset table (device-side contiguous staging), and CopyStrided runs
-// arbitrary strided push entries (column-split resharding) on the device.
+// arbitrary strided push entries (column-split resharding) on the device;
+// StridedCopyPlan keeps such entries' device table for repeated runs.
 // TPU tiled layouts do not exist here, so there is no tile/detile step.
 #ifndef KVX_HOST_WEIGHT_SYNCHRONIZER_H_
 #define KVX_HOST_WEIGHT_SYNCHRONIZER_H_
@@ -117,6 +118,35 @@ class WeightSynchronizer {
 // `stream` (no synchronizer needed); returns a future for the launch.
 StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCopy>& copies,
                                          hipStream_t stream);
+
+// Strided entries whose device image (entry table + tile map) is built and
+// uploaded once, for callers that run the same entries again and again: a
+// weight push repeats the same expansion every time
+// (weight_synchronizer_base.cc:626-666). A run is one launch with no host
+// table work and no upload. The addresses the entries name must stay valid
+// while the plan is run. Runs may come from any thread.
+class StridedCopyPlan {
+ public:
+  static StatusOr<std::unique_ptr<StridedCopyPlan>> Create(int device,
+                                                           const std::vector<StridedCopy>& copies);
+  // Waits for every run still in flight, then frees the image.
+  ~StridedCopyPlan();
+  StridedCopyPlan(const StridedCopyPlan&) = delete;
+  StridedCopyPlan& operator=(const StridedCopyPlan&) = delete;
+
+  StatusOr<CopyFuture> Run(hipStream_t stream);
+  uint32_t workgroups() const { return grid_; }
+
+ private:
+  StridedCopyPlan() = default;
+  int device_ = 0;
+  int vec_ = 16;
+  uint32_t n_ = 0;
+  uint32_t grid_ = 0;
+  void* image_ = nullptr;
+  std::mutex mu_;
+  std::vector<hipEvent_t> runs_;  // one per run that may still read the image
+};
 
 }  // namespace kvx
 

@@ -92,18 +92,45 @@ def column_split_entries(weight, outputs: Sequence[Any]) -> List[StridedEntry]:
 
 class StridedPlan:
     """Entries converted once into the C-ABI's entry array, for callers that
-    run the same entries repeatedly (the same column split every sync)."""
+    run the same entries repeatedly (the same column split every sync). The
+    first copy_strided of the plan on a device also builds and uploads its
+    device table there (kvx_strided_plan_create); later runs on that device
+    are one launch each. The tensors the entries address must outlive the
+    plan's runs; close() (or garbage collection) frees the device tables
+    after the runs in flight."""
 
     def __init__(self, entries: Sequence[StridedEntry]):
         import numpy as np
         self.n = len(entries)
         self._arr = (_capi.StridedEntryC * max(self.n, 1))()
+        self._device_plans = {}  # device -> kvx_strided_plan handle
         if self.n:
             rows = np.frombuffer(self._arr, dtype=np.uint64).reshape(-1, 8)
             vals = np.array([e.as_tuple() for e in entries], dtype=np.uint64)
             rows[:, 0:2] = vals[:, 0:2]     # src, dst
             rows[:, 2:4] = 0                # src/dst offsets (folded into src/dst)
             rows[:, 4:8] = vals[:, 2:6]     # size, count, src_stride, dst_stride
+
+    def _device_plan(self, device: int) -> ctypes.c_void_p:
+        h = self._device_plans.get(device)
+        if h is None:
+            h = ctypes.c_void_p()
+            _capi.check(_capi.load().kvx_strided_plan_create(device, self._arr, self.n,
+                                                             ctypes.byref(h)),
+                        "StridedPlan")
+            self._device_plans[device] = h
+        return h
+
+    def close(self) -> None:
+        plans, self._device_plans = getattr(self, "_device_plans", {}), {}
+        for h in plans.values():
+            _capi.load().kvx_strided_plan_destroy(h)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def copy_strided(entries, stream=None, device: int = 0, keep_alive=None) -> RaidenFuture:
@@ -112,8 +139,13 @@ def copy_strided(entries, stream=None, device: int = 0, keep_alive=None) -> Raid
     if stream is None:
         import torch
         stream = torch.cuda.current_stream(device)
-    plan = entries if isinstance(entries, StridedPlan) else StridedPlan(entries)
     out = ctypes.c_void_p()
+    if isinstance(entries, StridedPlan):
+        _capi.check(_capi.load().kvx_strided_plan_run(entries._device_plan(device),
+                                                      ctypes.c_void_p(_stream_ptr(stream)),
+                                                      ctypes.byref(out)), "copy_strided")
+        return RaidenFuture(out, keep_alive, "copy_strided")
+    plan = StridedPlan(entries)
     _capi.check(_capi.load().kvx_copy_strided(device, plan._arr, plan.n,
                                               ctypes.c_void_p(_stream_ptr(stream)),
                                               ctypes.byref(out)), "copy_strided")
