@@ -254,6 +254,7 @@ extern "C" int kvx_manager_gather_no_alloc(kvx_manager* m, const int64_t* ids, i
     CopyLaunch cl;
     cl.ids = reinterpret_cast<const int64_t*>(scratch_addr);
     cl.n = n;
+    cl.gather_workgroups_per_cu = mgr.engine()->gather_workgroups_per_cu();
     for (int g = g0; g < ngroups && g < g0 + kMaxPieces; ++g) {
       const int64_t W = gcount[g];
       const int64_t B = gbytes[g];

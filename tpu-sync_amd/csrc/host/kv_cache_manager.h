@@ -283,6 +283,7 @@ class KVCacheManager {
   // assigned_numa_node), or -1.
   int assigned_numa_node() const { return numa_node_; }
   TransferEngine* engine() { return engine_.get(); }
+  const TransferEngine* engine() const { return engine_.get(); }
   bool queued_dispatch() const { return queued_; }
   // The kinds ('D' = D2h, 'H' = H2d) of the last dispatched copies, oldest
   // first (at most 256).

@@ -191,9 +191,9 @@ class TransferEngine {
                                   uint64_t staging, bool block_major,
                                   hipStream_t stream);
 
-  // Device-side scale/payload groups for one launch: storages that share a
-  // block size form one piece of the kernel (see block_copy.h).
   int device() const { return opts_.device; }
+  // The occupancy cap the engine's device gathers launch with.
+  int gather_workgroups_per_cu() const { return opts_.gather_workgroups_per_cu; }
   EngineStats stats() const;
   // SDMA engine bits of the pageable lanes' DMAs, (device-to-host << 16) |
   // host-to-device; 0 while no lane exists or when the lanes use
