@@ -33,11 +33,11 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and, in a
 # second run, WRITE_SIZE (KiB per dispatch), each divided by the factor the
 # same counter reads for a plain 1 GiB device copy in the same runs (FETCH
-# 0.50001, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
+# 0.50002, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
 # (kernel, algorithmic bytes per launch).
 MEASURED_TRAFFIC = {
-    ("gather", 2 * 512 * 64 * 32768): int((524444.9 / 0.50001 + 1048579.5 / 1.0) * 1024),
-    ("scatter", 2 * 512 * 64 * 32768): int((524338.5 / 0.50001 + 1048596.7 / 1.0) * 1024),
+    ("gather", 2 * 512 * 64 * 32768): int((524450.1 / 0.50002 + 1048615.4 / 1.0) * 1024),
+    ("scatter", 2 * 512 * 64 * 32768): int((524337.8 / 0.50002 + 1048598.7 / 1.0) * 1024),
 }
 
 WORKLOADS = {
