@@ -88,6 +88,8 @@ def parse_args():
                         "32 MiB measured best for its 64-2048-block requests")
     p.add_argument("--zipf-host-threads", type=int, default=0,
                    help="host copy threads of the churn's bounce lanes (0: the library's 8)")
+    p.add_argument("--zipf-mode", default="auto", choices=["auto", "staged", "zero_copy", "lanes"],
+                   help="transfer mode of the churn's manager")
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
                         "request's load and save finish before the next is issued)")
@@ -603,6 +605,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                              staging_chunk_bytes=(args.zipf_chunk_mib or args.chunk_mib) << 20,
                              staging_chunks=args.chunks,
                              host_copy_threads=args.zipf_host_threads,
+                             transfer_mode=args.zipf_mode,
                              raiden_controller_address=store.raiden_controller_address,
                              **tier)
     t_tier = time.perf_counter() - t_tier
@@ -734,6 +737,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
            "host_tier_limit": tier_limit, "host_tier_setup_s": round(t_tier, 1),
            "batches": args.zipf_batches, "requests_in_flight": inflight,
            "staging_chunk_mib": args.zipf_chunk_mib or args.chunk_mib,
+           "transfer_mode": args.zipf_mode, "engine_stats": mgr.engine_stats(),
            "host_copy_threads": args.zipf_host_threads or 8,
            "blocks_saved": saved, "blocks_loaded": loaded,
            "blocks_skipped": skipped, "device_hits": device_hits,

@@ -186,6 +186,56 @@ def test_scattered_ids_match_oracle_many_chunks(kvx, cuda, mode):
     mgr.close()
 
 
+def test_auto_moves_long_pinned_copies_through_the_lanes(kvx, cuda):
+    """Auto mode on a pinned mirror: a copy of more than 32 staging chunks
+    goes through the lanes (issued chunk by chunk), a shorter one stays on
+    the stream-ordered paths (zero-copy here: its host runs are shorter than
+    4 MiB); every copy, and a load and a save in flight together, byte for
+    byte the oracle's. 8 storages x 4 KiB blocks, 64 KiB chunks: 32 chunks
+    are 64 blocks."""
+    rng = np.random.default_rng(41)
+    layers, blocks, hb, bb = 8, 1024, 700, 4096
+    host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
+    mgr = make_mgr(kvx, dev, hb, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                   direct_min_bytes=1 << 40, host_copy_threads=3)
+    mir = Mirror(host, hb)
+    want = {"bounce_copies": 0, "zero_copy_copies": 0, "staged_copies": 0}
+    for n, scattered, path in ((64, True, "zero_copy_copies"), (65, True, "bounce_copies"),
+                               (300, True, "bounce_copies"), (300, False, "bounce_copies"),
+                               (48, False, "zero_copy_copies")):
+        ids = rng.choice(blocks, size=n, replace=False).tolist()
+        hids = (rng.choice(hb, size=n, replace=False) if scattered
+                else np.arange(n) + int(rng.integers(0, hb - n))).tolist()
+        print(f"n={n} scattered={scattered} expect {path}", flush=True)
+        mgr.d2h(ids, hids).Await()
+        assert mir.transfer(True, ids, hids, []) == 0
+        mir.check(mgr, dev)
+        back = rng.choice(blocks, size=n, replace=False).tolist()
+        mgr.h2d(hids, back).Await()
+        assert mir.transfer(False, hids, back, []) == 0
+        mir.check(mgr, dev)
+        want[path] += 2
+        if path == "bounce_copies":
+            want["staged_copies"] += 2  # a lane copy is a staged copy too
+        stats = mgr.engine_stats()
+        assert {k: stats[k] for k in want} == want, (n, scattered, stats)
+    # A long load and a long save in flight together (disjoint host ranges).
+    hids = rng.choice(hb, size=600, replace=False).tolist()
+    ids = rng.choice(blocks, size=300, replace=False).tolist()
+    mgr.d2h(ids, hids[:300]).Await()
+    assert mir.transfer(True, ids, hids[:300], []) == 0
+    back = rng.choice(blocks, size=300, replace=False).tolist()
+    save_ids = [b for b in rng.permutation(blocks).tolist() if b not in set(back)][:300]
+    f1 = mgr.h2d(hids[:300], back)
+    f2 = mgr.d2h(save_ids, hids[300:])
+    f1.Await()
+    f2.Await()
+    assert mir.transfer(True, save_ids, hids[300:], []) == 0
+    assert mir.transfer(False, hids[:300], back, []) == 0
+    mir.check(mgr, dev)
+    mgr.close()
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_duplicate_destinations_last_wins(kvx, cuda, mode):
     rng = np.random.default_rng(3)

@@ -480,6 +480,16 @@ StatusOr<CopyFuture> TransferEngine::Copy(
   if (opts_.mode == TransferMode::kLanes && opts_.host_copy_threads > 0) {
     return CopyPageable(dir, storages, cdev, chost, {}, dep);
   }
+  if (opts_.mode == TransferMode::kAuto && opts_.host_copy_threads > 0) {
+    // Long copies leave the stream-ordered paths for the lanes, which issue
+    // one chunk at a time (auto_lanes_min_chunks).
+    int64_t per_block = 0;  // bytes of one block over every storage
+    for (const StorageView& s : storages) per_block += s.block_bytes;
+    const int64_t limit = opts_.auto_lanes_min_chunks * opts_.staging_chunk_bytes;
+    if (per_block > 0 && static_cast<int64_t>(cdev.size()) > limit / per_block) {
+      return CopyPageable(dir, storages, cdev, chost, {}, dep);
+    }
+  }
   bool zero_copy = opts_.mode == TransferMode::kZeroCopy;
   if (opts_.mode == TransferMode::kAuto && host_ok) {
     // The staged path costs one hipMemcpyAsync per (storage, host run) and

@@ -65,9 +65,10 @@ struct ByteExtent {
 //   kZeroCopy: one kernel moves every block between the pool and the pinned
 //            host mirror directly (GPU loads/stores over PCIe), no staging;
 //   kAuto: staged when the host ids form long runs (average run of a
-//          storage at least auto_staged_min_run_bytes); zero-copy otherwise.
-//          Host memory the GPU cannot map always goes staged (through the
-//          pageable lanes).
+//          storage at least auto_staged_min_run_bytes); zero-copy otherwise;
+//          a copy of more than auto_lanes_min_chunks staging chunks goes
+//          through the lanes (as kLanes). Host memory the GPU cannot map
+//          always goes staged (through the pageable lanes).
 //   kLanes: pinned host memory too goes through the pageable lanes (host
 //          threads move the host side, whole chunks cross on SDMA): a load
 //          and a save at once reach the link's duplex rate, where zero-copy
@@ -100,6 +101,18 @@ struct EngineOptions {
   // for H2D) wins from 4 MiB runs (83 against 79 GB/s; 16 MiB: 93 against
   // 82) and loses at 2 MiB and below (71 against 73; 1 MiB: 51 against 64).
   int64_t auto_staged_min_run_bytes = 4ll << 20;
+  // kAuto moves a pinned-mirror copy of more than this many staging chunks
+  // through the lanes (when host_copy_threads > 0). The staged path enqueues
+  // every chunk of a copy at once (kernels, copies and the events that chain
+  // them over two streams), and far more than the ring's depth in flight
+  // slows the runtime's copies: 1024 blocks of 5 MiB in 32 MiB chunks (160
+  // chunks) took 220-270 ms D2H alone against 97 ms with the host issuing a
+  // chunk only once its ring slot was free, and a load and a save of that
+  // size at once fell to 25 GB/s. The lanes issue chunk by chunk from their
+  // own threads: 96.7 ms alone and 113 ms both ways (90 GB/s); zero-copy
+  // 96.3 / 127.5 ms. Below the threshold the staged and zero-copy paths are
+  // as fast or faster (a lone 64-block copy: zero-copy 6.1 ms, lanes 6.5).
+  int64_t auto_lanes_min_chunks = 32;
   // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
   // bounce buffers that this many host threads fill and drain, one lane per
   // direction with its own streams, staging ring and SDMA engine (0: leave
