@@ -65,8 +65,10 @@ extern "C" {
  *   KVX_MODE_ZERO_COPY: one kernel moves the blocks between the pool and the
  *     pinned host mirror directly over PCIe (needs KVX_HOST_PINNED);
  *   KVX_MODE_AUTO: staged when a copy's host runs average at least 4 MiB per
- *     storage, zero-copy below that; a copy of more than 32 staging chunks
- *     goes through the lanes (below), which issue it chunk by chunk;
+ *     storage, zero-copy below that; a copy of more than 32 staging chunks,
+ *     or a staged one that would leave more than 32 staged chunks of its
+ *     direction in flight, goes through the lanes (below), which issue it
+ *     chunk by chunk;
  *   KVX_MODE_LANES: short runs of a pinned mirror go through the bounce lanes
  *     of pageable mirrors (host threads gather and scatter the host side,
  *     whole staging chunks cross on fixed SDMA engines). A load and a save at

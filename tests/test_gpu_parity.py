@@ -236,6 +236,39 @@ def test_auto_moves_long_pinned_copies_through_the_lanes(kvx, cuda):
     mgr.close()
 
 
+def test_auto_bounds_staged_chunks_in_flight(kvx, cuda):
+    """Auto mode keeps at most 32 staged chunks of a direction in flight: five
+    staged offloads of 8 chunks each, issued while the stream they depend on
+    is held by a spin kernel, go staged four times and through the lanes the
+    fifth time; all five land byte for byte. 8 storages x 1 MiB blocks, 4 MiB
+    chunks: 4 contiguous blocks are 4 MiB runs (staged), 8 chunks."""
+    rng = np.random.default_rng(43)
+    layers, blocks, hb, bb = 8, 64, 24, 1 << 20
+    host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
+    mgr = make_mgr(kvx, dev, hb, staging_chunk_bytes=4 << 20, staging_chunks=2,
+                   direct_min_bytes=1 << 40, host_copy_threads=3)
+    mir = Mirror(host, hb)
+    hold = torch.cuda.Stream(cuda)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(hold):
+        torch.cuda._sleep(200_000_000)  # bounded spin, well past the issue below
+    futs, copies = [], []
+    for k in range(5):
+        ids = rng.choice(blocks, size=4, replace=False).tolist()
+        hids = list(range(4 * k, 4 * k + 4))
+        futs.append(mgr.d2h(ids, hids, stream=hold))
+        copies.append((ids, hids))
+    for f in futs:
+        f.Await()
+    for ids, hids in copies:
+        assert mir.transfer(True, ids, hids, []) == 0
+    mir.check(mgr, dev)
+    stats = mgr.engine_stats()
+    assert stats["staged_copies"] == 5 and stats["bounce_copies"] == 1, stats
+    assert stats["zero_copy_copies"] == 0 and stats["direct_copies"] == 0, stats
+    mgr.close()
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_duplicate_destinations_last_wins(kvx, cuda, mode):
     rng = np.random.default_rng(3)

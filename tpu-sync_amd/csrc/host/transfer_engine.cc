@@ -244,6 +244,12 @@ TransferEngine::~TransferEngine() {
   }
   for (ArgSlice& s : arg_inflight_) (void)hipEventDestroy(s.done);
   arg_inflight_.clear();
+  for (std::deque<StagedInFlight>& q : staged_inflight_) {
+    for (const StagedInFlight& s : q) (void)hipEventDestroy(s.done);
+    q.clear();
+  }
+  for (hipEvent_t e : spare_events_) (void)hipEventDestroy(e);
+  spare_events_.clear();
   extent_args_.reset();
   for (KernelSample& s : samples_) {
     (void)hipEventDestroy(s.start);
@@ -480,16 +486,6 @@ StatusOr<CopyFuture> TransferEngine::Copy(
   if (opts_.mode == TransferMode::kLanes && opts_.host_copy_threads > 0) {
     return CopyPageable(dir, storages, cdev, chost, {}, dep);
   }
-  if (opts_.mode == TransferMode::kAuto && opts_.host_copy_threads > 0) {
-    // Long copies leave the stream-ordered paths for the lanes, which issue
-    // one chunk at a time (auto_lanes_min_chunks).
-    int64_t per_block = 0;  // bytes of one block over every storage
-    for (const StorageView& s : storages) per_block += s.block_bytes;
-    const int64_t limit = opts_.auto_lanes_min_chunks * opts_.staging_chunk_bytes;
-    if (per_block > 0 && static_cast<int64_t>(cdev.size()) > limit / per_block) {
-      return CopyPageable(dir, storages, cdev, chost, {}, dep);
-    }
-  }
   bool zero_copy = opts_.mode == TransferMode::kZeroCopy;
   if (opts_.mode == TransferMode::kAuto && host_ok) {
     // The staged path costs one hipMemcpyAsync per (storage, host run) and
@@ -501,6 +497,23 @@ StatusOr<CopyFuture> TransferEngine::Copy(
     }
     zero_copy = static_cast<int64_t>(chost.size()) * max_block <
                 opts_.auto_staged_min_run_bytes * runs;
+  }
+  if (opts_.mode == TransferMode::kAuto && opts_.host_copy_threads > 0) {
+    // A copy of more than auto_lanes_min_chunks staging chunks goes through
+    // the lanes, which issue one chunk at a time; so does a staged copy that
+    // would leave more than that many staged chunks of its direction in
+    // flight together with the copies before it.
+    int64_t per_block = 0;  // bytes of one block over every storage
+    for (const StorageView& s : storages) per_block += s.block_bytes;
+    const int64_t n = static_cast<int64_t>(cdev.size());
+    const int64_t chunk = opts_.staging_chunk_bytes;
+    bool lanes = per_block > 0 && n > opts_.auto_lanes_min_chunks * chunk / per_block;
+    if (!lanes && !zero_copy) {
+      const int64_t own = (n * per_block + chunk - 1) / chunk;
+      std::lock_guard<std::mutex> l(mu_);
+      lanes = own + StagedChunksInFlightLocked(dir) > opts_.auto_lanes_min_chunks;
+    }
+    if (lanes) return CopyPageable(dir, storages, cdev, chost, {}, dep);
   }
   if (zero_copy) {
     if (!host_ok) {
@@ -808,9 +821,39 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
   lane.ring = d2h ? &out_ring_ : &in_ring_;
   KVX_RETURN_IF_ERROR(EnsureRing(lane.ring));
   hipEvent_t done = nullptr;
+  const int64_t chunks_before = stats_.chunks;
   KVX_RETURN_IF_ERROR(StagedOnLane(lane, dir, storages, cdev, chost, dep, &done));
   ++stats_.staged_copies;
+  // Track the chunks this copy keeps in flight (Copy() keeps the total
+  // bounded; see EngineOptions::auto_lanes_min_chunks).
+  hipEvent_t track = nullptr;
+  if (!spare_events_.empty()) {
+    track = spare_events_.back();
+    spare_events_.pop_back();
+  } else {
+    KVX_ASSIGN_OR_RETURN(track, NewEvent());
+  }
+  const hipError_t rec = hipEventRecord(track, d2h ? lane.cs : lane.ks);
+  if (rec == hipSuccess) {
+    staged_inflight_[static_cast<int>(dir)].push_back(
+        StagedInFlight{track, stats_.chunks - chunks_before});
+  } else {
+    (void)hipEventDestroy(track);
+  }
   return CopyFuture::FromEvents({done}, {});
+}
+
+int64_t TransferEngine::StagedChunksInFlightLocked(Direction dir) {
+  std::deque<StagedInFlight>& q = staged_inflight_[static_cast<int>(dir)];
+  // Copies finish in order on their streams: drop finished ones from the
+  // front.
+  while (!q.empty() && hipEventQuery(q.front().done) == hipSuccess) {
+    spare_events_.push_back(q.front().done);
+    q.pop_front();
+  }
+  int64_t chunks = 0;
+  for (const StagedInFlight& s : q) chunks += s.chunks;
+  return chunks;
 }
 
 Status TransferEngine::PipelineBounceSdma(const LaneView& lane, Direction dir,

@@ -66,9 +66,11 @@ struct ByteExtent {
 //            host mirror directly (GPU loads/stores over PCIe), no staging;
 //   kAuto: staged when the host ids form long runs (average run of a
 //          storage at least auto_staged_min_run_bytes); zero-copy otherwise;
-//          a copy of more than auto_lanes_min_chunks staging chunks goes
-//          through the lanes (as kLanes). Host memory the GPU cannot map
-//          always goes staged (through the pageable lanes).
+//          a copy of more than auto_lanes_min_chunks staging chunks, or a
+//          staged one that would leave more than that many staged chunks of
+//          its direction in flight, goes through the lanes (as kLanes). Host
+//          memory the GPU cannot map always goes staged (through the
+//          pageable lanes).
 //   kLanes: pinned host memory too goes through the pageable lanes (host
 //          threads move the host side, whole chunks cross on SDMA): a load
 //          and a save at once reach the link's duplex rate, where zero-copy
@@ -102,16 +104,21 @@ struct EngineOptions {
   // 82) and loses at 2 MiB and below (71 against 73; 1 MiB: 51 against 64).
   int64_t auto_staged_min_run_bytes = 4ll << 20;
   // kAuto moves a pinned-mirror copy of more than this many staging chunks
-  // through the lanes (when host_copy_threads > 0). The staged path enqueues
-  // every chunk of a copy at once (kernels, copies and the events that chain
-  // them over two streams), and far more than the ring's depth in flight
-  // slows the runtime's copies: 1024 blocks of 5 MiB in 32 MiB chunks (160
-  // chunks) took 220-270 ms D2H alone against 97 ms with the host issuing a
-  // chunk only once its ring slot was free, and a load and a save of that
-  // size at once fell to 25 GB/s. The lanes issue chunk by chunk from their
-  // own threads: 96.7 ms alone and 113 ms both ways (90 GB/s); zero-copy
-  // 96.3 / 127.5 ms. Below the threshold the staged and zero-copy paths are
-  // as fast or faster (a lone 64-block copy: zero-copy 6.1 ms, lanes 6.5).
+  // through the lanes (when host_copy_threads > 0), and a staged copy too
+  // when its chunks and those of the direction's staged copies still in
+  // flight exceed it. The staged path enqueues every chunk of a copy at once
+  // (kernels and copies chained over two streams by events), and chains far
+  // deeper than the ring slow the runtime's copies: 1024 blocks of 5 MiB in
+  // 32 MiB chunks (160 chunks) took 220-270 ms D2H alone against 97 ms with
+  // the host issuing a chunk only once its ring slot was free; a load and a
+  // save of that size at once fell to 25 GB/s; eight 640 MiB offloads issued
+  // together took 148, 233, then 390 ms (the same copies one by one: 109 ms
+  // each time). The same slowdown shows with torch's own copies chained
+  // that way, and not on one stream. The lanes issue chunk by chunk from
+  // their own threads: 96.7 ms alone and 113 ms both ways for the 1024
+  // blocks; zero-copy 96.3 / 127.5 ms. Below the threshold the staged and
+  // zero-copy paths are as fast or faster (a lone 64-block copy: zero-copy
+  // 6.1 ms, lanes 6.5).
   int64_t auto_lanes_min_chunks = 32;
   // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
   // bounce buffers that this many host threads fill and drain, one lane per
@@ -360,6 +367,17 @@ class TransferEngine {
   std::unique_ptr<SdmaEngines> sdma_;
   bool sdma_tried_ = false;
   EngineStats stats_;
+  // Stream-ordered staged copies still in flight, per direction (under
+  // mu_): an event recorded after each copy and the chunks it enqueued.
+  struct StagedInFlight {
+    hipEvent_t done;
+    int64_t chunks;
+  };
+  std::deque<StagedInFlight> staged_inflight_[2];  // by Direction
+  std::vector<hipEvent_t> spare_events_;           // finished ones, for reuse
+  // Chunks of the direction's staged copies not yet finished (drops the
+  // finished ones). Needs mu_.
+  int64_t StagedChunksInFlightLocked(Direction dir);
 };
 
 }  // namespace kvx

@@ -190,7 +190,8 @@ class KVCacheManager:
       staging_chunk_bytes / staging_chunks: device staging ring per direction.
       transfer_mode: "auto" (staged when a copy's host runs average at least
         4 MiB per storage, zero-copy below; copies of more than 32 staging
-        chunks through the lanes), "staged", "zero_copy" (pinned
+        chunks, and staged copies beyond 32 chunks in flight per direction,
+        through the lanes), "staged", "zero_copy" (pinned
         mirror only) or "lanes" (a pinned mirror's short runs through the
         bounce lanes, for callers that load and save at once);
         zero_copy_workgroups caps a zero-copy launch.
