@@ -8,8 +8,8 @@
 // 256-byte aligned; bytes between tensors are unspecified), so the whole
 // parameter set moves as a few large DMAs:
 //   * D2h: the offset-table pack kernel gathers the scattered tensors chunk by
-//     chunk into a device staging ring; each chunk crosses PCIe as one
-//     hipMemcpyAsync while the next chunk is packed;
+//     chunk into a device staging ring; each chunk then crosses PCIe as one
+//     hipMemcpyAsync on the same stream;
 //   * H2d: the mirror image (one H2D per chunk, then the unpack kernel);
 //   * D2hLayer / H2dLayer: one direct copy per shard of that weight, as the
 //     reference issues.
@@ -107,8 +107,8 @@ class WeightSynchronizer {
   hipStream_t d2h_ = nullptr;
   hipStream_t h2d_ = nullptr;
   std::vector<uint64_t> ring_;
-  std::vector<hipEvent_t> ready_, free_;
-  std::vector<bool> used_;
+  std::vector<hipEvent_t> free_;           // recorded after each use of a slot
+  std::vector<hipStream_t> slot_stream_;  // the stream of that use (null: none)
   size_t next_ = 0;
   ArgRing args_;
   std::vector<Sample> samples_;
