@@ -1107,20 +1107,40 @@ Status TransferEngine::StagedOnLane(const LaneView& lane, Direction dir,
 
   // Chunk plan over the layer-major staging layout of all groups.
   const int64_t cap = opts_.staging_chunk_bytes;
+  // On a bounce lane the first chunk's host fill (H2D) comes before any DMA
+  // and the last chunk's host copy (D2H) after the last one; chunks that grow
+  // from cap/8 to cap over the first three and shrink to half of what is
+  // left towards the end shorten both.
+  const bool ramp = lane.bounce != nullptr;
+  int64_t left = 0;  // bytes not yet planned
+  for (const Group& gr : groups) {
+    left += static_cast<int64_t>(gr.members.size()) * n * gr.block_bytes;
+  }
+  auto chunk_cap = [&](size_t index) -> int64_t {
+    if (!ramp) return cap;
+    int64_t c = index < 3 ? cap >> (3 - index) : cap;
+    c = std::min(c, std::max(cap / 8, (left + 1) / 2));
+    return std::max<int64_t>(c, 1);
+  };
   std::vector<std::vector<PiecePlan>> plans;
   {
     std::vector<PiecePlan> cur;
     int64_t used = 0;
+    int64_t cur_cap = chunk_cap(0);
     for (size_t gi = 0; gi < groups.size(); ++gi) {
       const int64_t B = groups[gi].block_bytes;
       const int64_t F = static_cast<int64_t>(groups[gi].members.size()) * n;
       int64_t f = 0;
       while (f < F) {
-        int64_t fit = (cap - used) / B;
+        int64_t fit = (cur_cap - used) / B;
+        // A chunk holds at least one block (B <= cap: the ring's buffers).
+        if (fit == 0 && used == 0) fit = 1;
         if (fit == 0) {
           plans.push_back(std::move(cur));
           cur.clear();
+          left -= used;
           used = 0;
+          cur_cap = chunk_cap(plans.size());
           continue;
         }
         const int64_t take = std::min(fit, F - f);
