@@ -113,12 +113,16 @@ PATHS = {
     # Pageable mirror left to the runtime's per-run hipMemcpyAsync.
     "pageable": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                      host_alloc="malloc", host_copy_threads=-1),
+    # Auto mode on a pinned mirror with 64 KiB chunks: copies of more than
+    # 32 chunks (2 MiB) go through the lanes, shorter ones zero-copy.
+    "auto": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
+                 host_copy_threads=3),
 }
 MODES = ["staged", "zero_copy"]
 
 
 @pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "bounce_hip",
-                                  "lanes", "pageable"])
+                                  "lanes", "pageable", "auto"])
 @pytest.mark.parametrize("bb", [32768, 61424, 12992, 1024, 48, 36, 3])
 def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
     if path == "bounce_hip":
@@ -150,6 +154,12 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
         assert stats["bounce_copies"] == (12 if lanes else 0)
     elif path == "zero_copy":
         assert stats["zero_copy_copies"] == 12 and stats["memcpy_calls"] == 0
+    elif path == "auto":
+        # Every copy is zero-copy or (past 32 chunks) a lane copy.
+        assert stats["zero_copy_copies"] + stats["bounce_copies"] == 12, stats
+        assert stats["staged_copies"] == stats["bounce_copies"], stats
+        if bb >= 32768:
+            assert stats["bounce_copies"] > 0, stats
     else:
         assert stats["staged_copies"] == 0 and stats["zero_copy_copies"] == 0
     # The lanes' DMAs: one SDMA engine bit per direction, or hipMemcpyAsync.
