@@ -103,6 +103,9 @@ struct TransferEngine::Bounce {
   // dma_sig[k] stands in for dma_done[k].
   const SdmaEngines* sdma = nullptr;
   std::vector<hsa_signal_t> dma_sig;
+  // The slot's last DMA was a stream-ordered hipMemcpyAsync recorded in
+  // dma_done[k] even with SDMA engines (the last chunk of an H2D copy).
+  std::vector<bool> event_dma;
   std::vector<bool> used;
   std::vector<std::vector<Segment>> owed;  // D2H: host copies still due from bufs[k]
   std::vector<std::vector<CopyFuture>> waiters;  // D2H: copies complete once bufs[k] drains
@@ -118,13 +121,19 @@ struct TransferEngine::Bounce {
   }
 
   Status WaitDma(size_t k) {
-    if (sdma != nullptr) return SdmaEngines::Wait(dma_sig[k]);
+    if (sdma != nullptr && !event_dma[k]) return SdmaEngines::Wait(dma_sig[k]);
     return HipStatus(hipEventSynchronize(dma_done[k]), "bounce buffer DMA");
   }
   // Waits for every DMA still in flight (SDMA copies are on no stream, so a
   // stream synchronisation does not cover them).
   void WaitAllDma() {
-    for (size_t k = 0; k < dma_sig.size(); ++k) (void)SdmaEngines::Wait(dma_sig[k]);
+    for (size_t k = 0; k < dma_sig.size(); ++k) {
+      if (event_dma[k]) {
+        (void)hipEventSynchronize(dma_done[k]);
+      } else {
+        (void)SdmaEngines::Wait(dma_sig[k]);
+      }
+    }
   }
   // Moves the segments' bytes with the pool and the calling thread.
   void Copy(const std::vector<Segment>& segs) { pool.Copy(segs); }
@@ -935,8 +944,21 @@ Status TransferEngine::PipelineBounceSdma(const LaneView& lane, Direction dir,
     std::vector<Bounce::Segment> segs;
     segments(ch, b->bufs[k], &segs);
     b->Copy(segs);
-    KVX_RETURN_IF_ERROR(dma.Start(/*d2h=*/false, reinterpret_cast<void*>(ring.bufs[k]),
-                                  b->bufs[k], static_cast<size_t>(ch.bytes), b->dma_sig[k]));
+    const bool last = &ch == &chunks.back();
+    if (last) {
+      // The last chunk crosses on the lane's copy stream and its scatter
+      // follows on the kernel stream, so this thread need not wait for it:
+      // the next copy's first host fill and DMA overlap this one's end.
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(ring.bufs[k]), b->bufs[k],
+                                             static_cast<size_t>(ch.bytes),
+                                             hipMemcpyHostToDevice, lane.cs));
+      KVX_HIP_RETURN_IF_ERROR(hipEventRecord(b->dma_done[k], lane.cs));
+      b->event_dma[k] = true;
+    } else {
+      KVX_RETURN_IF_ERROR(dma.Start(/*d2h=*/false, reinterpret_cast<void*>(ring.bufs[k]),
+                                    b->bufs[k], static_cast<size_t>(ch.bytes), b->dma_sig[k]));
+      b->event_dma[k] = false;
+    }
     ++*memcpys;
     b->used[k] = true;
     ring.used[k] = true;
@@ -944,7 +966,11 @@ Status TransferEngine::PipelineBounceSdma(const LaneView& lane, Direction dir,
     prev = &ch;
     prev_k = k;
   }
-  if (prev != nullptr) KVX_RETURN_IF_ERROR(scatter(*prev, prev_k));
+  if (prev != nullptr) {
+    KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(lane.ks, b->dma_done[prev_k], 0));
+    KVX_RETURN_IF_ERROR(prev->kernel(ring.bufs[prev_k]));
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ring.free[prev_k], lane.ks));
+  }
   guard.armed = false;
   return OkStatus();
 }
@@ -1364,6 +1390,7 @@ StatusOr<TransferEngine::PageableLane*> TransferEngine::Lane(Direction dir) {
     lane->bounce->bufs.push_back(static_cast<uint8_t*>(h));
     KVX_ASSIGN_OR_RETURN(hipEvent_t dma, NewEvent());
     lane->bounce->dma_done.push_back(dma);
+    lane->bounce->event_dma.push_back(false);
     lane->bounce->used.push_back(false);
     lane->bounce->owed.emplace_back();
     lane->bounce->waiters.emplace_back();
