@@ -845,20 +845,23 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
   KVX_RETURN_IF_ERROR(StagedOnLane(lane, dir, storages, cdev, chost, dep, &done));
   ++stats_.staged_copies;
   // Track the chunks this copy keeps in flight (Copy() keeps the total
-  // bounded; see EngineOptions::auto_lanes_min_chunks).
+  // bounded; see EngineOptions::auto_lanes_min_chunks). The copy is already
+  // enqueued: if no event can be had it goes untracked rather than failing.
   hipEvent_t track = nullptr;
   if (!spare_events_.empty()) {
     track = spare_events_.back();
     spare_events_.pop_back();
   } else {
-    KVX_ASSIGN_OR_RETURN(track, NewEvent());
+    StatusOr<hipEvent_t> e = NewEvent();
+    if (e.ok()) track = e.value();
   }
-  const hipError_t rec = hipEventRecord(track, d2h ? lane.cs : lane.ks);
-  if (rec == hipSuccess) {
-    staged_inflight_[static_cast<int>(dir)].push_back(
-        StagedInFlight{track, stats_.chunks - chunks_before});
-  } else {
-    (void)hipEventDestroy(track);
+  if (track != nullptr) {
+    if (hipEventRecord(track, d2h ? lane.cs : lane.ks) == hipSuccess) {
+      staged_inflight_[static_cast<int>(dir)].push_back(
+          StagedInFlight{track, stats_.chunks - chunks_before});
+    } else {
+      (void)hipEventDestroy(track);
+    }
   }
   return CopyFuture::FromEvents({done}, {});
 }

@@ -352,6 +352,9 @@ StatusOr<CopyFuture> StridedCopyPlan::Run(hipStream_t stream) {
   DeviceGuard g(device_);
   if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
   std::lock_guard<std::mutex> l(mu_);
+  // Both events exist before the launch, so a launched run is always
+  // tracked and always has a future.
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   if (grid_ > 0) {
     // Runs that have finished no longer read the image.
     for (auto it = runs_.begin(); it != runs_.end();) {
@@ -362,14 +365,26 @@ StatusOr<CopyFuture> StridedCopyPlan::Run(hipStream_t stream) {
         ++it;
       }
     }
-    KVX_ASSIGN_OR_RETURN(hipEvent_t ran, NewEvent());
-    runs_.push_back(ran);
-    KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(static_cast<const StridedEntryDev*>(image_), n_,
-                                              grid_, vec_, stream));
-    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(ran, stream));
+    StatusOr<hipEvent_t> ran = NewEvent();
+    if (!ran.ok()) {
+      (void)hipEventDestroy(done);
+      return ran.status();
+    }
+    runs_.push_back(ran.value());
+    const hipError_t e = LaunchStridedCopy(static_cast<const StridedEntryDev*>(image_), n_,
+                                           grid_, vec_, stream);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(done);
+      return HipStatus(e, "strided copy launch");
+    }
+    // The image must outlive the launch: without its event, wait here.
+    if (hipEventRecord(ran.value(), stream) != hipSuccess) (void)hipStreamSynchronize(stream);
   }
-  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
-  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
+  const hipError_t rec = hipEventRecord(done, stream);
+  if (rec != hipSuccess) {
+    (void)hipEventDestroy(done);
+    return HipStatus(rec, "hipEventRecord");
+  }
   return CopyFuture::FromEvents({done}, {});
 }
 
