@@ -438,12 +438,22 @@ int64_t kvx_strings_count(const kvx_strings* s);
 int kvx_strings_get(const kvx_strings* s, int64_t i, const uint8_t** data,
                     int64_t* len);
 void kvx_strings_release(kvx_strings* s);
+/* The whole list at once (no reference counterpart: one call instead of one
+ * per item for bindings that convert long lists): item i is
+ * data[offsets[i], offsets[i + 1]), offsets has count + 1 entries. Both stay
+ * valid until kvx_strings_release. */
+int kvx_strings_flat(kvx_strings* s, const uint8_t** data, const int64_t** offsets);
 int64_t kvx_slices_count(const kvx_slices* s);
 /* Pointers written to *hash and the strings of *out stay valid until
  * kvx_slices_release. */
 int kvx_slices_get(const kvx_slices* s, int64_t i, const uint8_t** hash,
                    int64_t* hash_len, kvx_block_slice* out);
 void kvx_slices_release(kvx_slices* s);
+/* The whole list at once, as kvx_strings_flat: hash i is
+ * hashes[offsets[i], offsets[i + 1]) and blocks[i] its slice (count entries);
+ * all valid until kvx_slices_release. */
+int kvx_slices_flat(kvx_slices* s, const uint8_t** hashes, const int64_t** offsets,
+                    const kvx_block_slice** blocks);
 
 /* KVCacheStore::Create (kv_cache_store.cc:170-360). A surviving metadata
  * table is recovered from at construction (kv_cache_store_wrapper.cc:170-185). */

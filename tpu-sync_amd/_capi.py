@@ -283,10 +283,13 @@ PROTOTYPES = {
     "kvx_strings_count": (_i64, [_vp]),
     "kvx_strings_get": (_int, [_vp, _i64, ctypes.POINTER(_vp), _i64p]),
     "kvx_strings_release": (None, [_vp]),
+    "kvx_strings_flat": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_i64p)]),
     "kvx_slices_count": (_i64, [_vp]),
     "kvx_slices_get": (_int, [_vp, _i64, ctypes.POINTER(_vp), _i64p,
                               ctypes.POINTER(BlockSlice)]),
     "kvx_slices_release": (None, [_vp]),
+    "kvx_slices_flat": (_int, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_i64p),
+                               ctypes.POINTER(ctypes.POINTER(BlockSlice))]),
     "kvx_store_create": (_int, [ctypes.POINTER(StoreConfig), ctypes.POINTER(_vp)]),
     "kvx_store_destroy": (None, [_vp]),
     "kvx_store_controller_address": (ctypes.c_char_p, [_vp]),
@@ -490,28 +493,40 @@ def i32_array(values):
 
 
 def pack_bytes(items):
-    """Packs byte strings back to back: (buffer, offsets[n + 1], n)."""
-    items = [bytes(b) for b in items]
-    offs = [0]
-    for b in items:
-        offs.append(offs[-1] + len(b))
+    """Packs byte strings back to back: (buffer, offsets[n + 1], n). The
+    offsets pointer keeps its numpy array alive."""
+    import numpy as np
+    items = [b if type(b) is bytes else bytes(b) for b in items]
+    n = len(items)
+    offs = np.zeros(n + 1, dtype=np.int64)
+    if n:
+        np.cumsum(np.fromiter(map(len, items), dtype=np.int64, count=n), out=offs[1:])
     blob = b"".join(items)
     buf = ctypes.create_string_buffer(blob, max(len(blob), 1))
-    arr = (ctypes.c_int64 * len(offs))(*offs)
-    return buf, arr, len(items)
+    return buf, offs.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), n
+
+
+def split_flat(data, offsets, n):
+    """Items [offsets[i], offsets[i + 1]) of a flat byte buffer of n items."""
+    if n == 0:
+        return []
+    offs = offsets[:n + 1]
+    blob = ctypes.string_at(data, offs[n]) if offs[n] else b""
+    return [blob[offs[i]:offs[i + 1]] for i in range(n)]
 
 
 def take_strings(handle):
-    """Copies a kvx_strings list into Python bytes and releases it."""
+    """Copies a kvx_strings list into Python bytes (one library call for the
+    whole list) and releases it."""
     lib = load()
     if not handle:
         return []
     try:
-        out = []
-        data, ln = ctypes.c_void_p(), ctypes.c_int64()
-        for i in range(lib.kvx_strings_count(handle)):
-            check(lib.kvx_strings_get(handle, i, ctypes.byref(data), ctypes.byref(ln)))
-            out.append(ctypes.string_at(data, ln.value) if ln.value else b"")
-        return out
+        n = lib.kvx_strings_count(handle)
+        if n == 0:
+            return []
+        data, offsets = ctypes.c_void_p(), _i64p()
+        check(lib.kvx_strings_flat(handle, ctypes.byref(data), ctypes.byref(offsets)))
+        return split_flat(data, offsets, n)
     finally:
         lib.kvx_strings_release(handle)

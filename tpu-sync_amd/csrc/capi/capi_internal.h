@@ -32,6 +32,10 @@ struct kvx_future {
 
 struct kvx_strings {
   std::vector<std::string> items;
+  // kvx_strings_flat: the items back to back and their offsets (built on
+  // first use).
+  std::string flat;
+  std::vector<int64_t> offsets;
 };
 
 namespace kvx {

@@ -18,6 +18,11 @@ struct kvx_store {
 
 struct kvx_slices {
   kvx::BlockSliceList items;
+  // kvx_slices_flat: the hashes back to back, their offsets and one
+  // kvx_block_slice per item (built on first use).
+  std::string hashes;
+  std::vector<int64_t> offsets;
+  std::vector<kvx_block_slice> blocks;
 };
 
 struct kvx_lru {
@@ -102,6 +107,23 @@ int kvx_strings_get(const kvx_strings* s, int64_t i, const uint8_t** data,
   return KVX_OK;
 }
 
+int kvx_strings_flat(kvx_strings* s, const uint8_t** data, const int64_t** offsets) {
+  if (s == nullptr || data == nullptr || offsets == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null list or output");
+  }
+  if (s->offsets.empty()) {
+    s->offsets.reserve(s->items.size() + 1);
+    s->offsets.push_back(0);
+    for (const std::string& it : s->items) {
+      s->flat += it;
+      s->offsets.push_back(static_cast<int64_t>(s->flat.size()));
+    }
+  }
+  *data = reinterpret_cast<const uint8_t*>(s->flat.data());
+  *offsets = s->offsets.data();
+  return KVX_OK;
+}
+
 void kvx_strings_release(kvx_strings* s) { delete s; }
 
 int64_t kvx_slices_count(const kvx_slices* s) {
@@ -124,6 +146,49 @@ int kvx_slices_get(const kvx_slices* s, int64_t i, const uint8_t** hash,
   out->job_name = p.second.raiden_id.job_name.c_str();
   out->job_replica_id = p.second.raiden_id.job_replica_id.c_str();
   out->data_name = p.second.raiden_id.data_name.c_str();
+  return KVX_OK;
+}
+
+int kvx_slices_flat(kvx_slices* s, const uint8_t** hashes, const int64_t** offsets,
+                    const kvx_block_slice** blocks) {
+  if (s == nullptr || hashes == nullptr || offsets == nullptr || blocks == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null list or output");
+  }
+  if (s->offsets.empty()) {
+    s->offsets.reserve(s->items.size() + 1);
+    s->offsets.push_back(0);
+    s->blocks.reserve(s->items.size());
+    // Slices with equal owner names share the first one's name pointers, so
+    // a binding can recognise the owner by pointer (a store's slices nearly
+    // always have one owner).
+    std::vector<const kvx::RaidenId*> owners;
+    for (const auto& p : s->items) {
+      s->hashes += p.first;
+      s->offsets.push_back(static_cast<int64_t>(s->hashes.size()));
+      const kvx::RaidenId& id = p.second.raiden_id;
+      const kvx::RaidenId* owner = &id;
+      for (const kvx::RaidenId* o : owners) {
+        if (o->job_name == id.job_name && o->job_replica_id == id.job_replica_id &&
+            o->data_name == id.data_name) {
+          owner = o;
+          break;
+        }
+      }
+      if (owner == &id) owners.push_back(owner);
+      kvx_block_slice b{};
+      b.host_block_id = p.second.host_block_id;
+      b.device_block_id = p.second.device_block_id;
+      b.status = static_cast<int32_t>(p.second.status);
+      b.data_replica_idx = id.data_replica_idx;
+      b.job_name = owner->job_name.c_str();
+      b.job_replica_id = owner->job_replica_id.c_str();
+      b.data_name = owner->data_name.c_str();
+      s->blocks.push_back(b);
+    }
+  }
+  *hashes = reinterpret_cast<const uint8_t*>(s->hashes.data());
+  *offsets = s->offsets.data();
+  *blocks = s->blocks.data();
   return KVX_OK;
 }
 

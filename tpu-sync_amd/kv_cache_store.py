@@ -19,6 +19,8 @@ import ctypes
 import enum
 from typing import List, Optional, Sequence, Tuple
 
+import numpy as np
+
 from . import _capi
 from .kv_cache_manager import LogicalBlockManager
 
@@ -76,6 +78,8 @@ class RaidenId:
 class RaidenBlockId:
     """Where a block lives (tpu_sync/api/torch/kv_cache_store.py:89-151)."""
 
+    __slots__ = ("_raiden_id", "_host_block_id", "_device_block_id", "_status")
+
     def __init__(self, raiden_id: Optional[RaidenId] = None, host_block_id: int = -1,
                  device_block_id: int = -1, status: BlockStatus = BlockStatus.INIT):
         self._raiden_id = raiden_id if raiden_id is not None else RaidenId()
@@ -91,6 +95,17 @@ class RaidenBlockId:
     job_replica_id = property(lambda self: self._raiden_id.job_replica_id)
     data_name = property(lambda self: self._raiden_id.data_name)
     data_replica_idx = property(lambda self: self._raiden_id.data_replica_idx)
+
+    @classmethod
+    def _of(cls, raiden_id: "RaidenId", host_block_id: int, device_block_id: int,
+            status: BlockStatus) -> "RaidenBlockId":
+        """Construction from already-typed fields (the library's lists)."""
+        b = cls.__new__(cls)
+        b._raiden_id = raiden_id
+        b._host_block_id = host_block_id
+        b._device_block_id = device_block_id
+        b._status = status
+        return b
 
     def __eq__(self, other) -> bool:
         return (isinstance(other, RaidenBlockId) and self._raiden_id == other._raiden_id
@@ -120,22 +135,57 @@ def _c_slices(slices: Sequence) -> Tuple[ctypes.Array, int, list]:
     return arr, len(slices), keep
 
 
+# kvx_block_slice as numpy reads it: four int32 fields, then the three name
+# pointers.
+_SLICE_DTYPE = np.dtype([("host", "<i4"), ("dev", "<i4"), ("status", "<i4"),
+                         ("replica", "<i4"), ("names", "<u8", (3,))])
+assert _SLICE_DTYPE.itemsize == ctypes.sizeof(_capi.BlockSlice)
+_STATUS_BY_VALUE = {int(s): s for s in BlockStatus}
+
+
+def _c_string(ptr: int) -> str:
+    return ctypes.string_at(ptr).decode() if ptr else ""
+
+
 def _take_slices(handle) -> List[Tuple[bytes, RaidenBlockId]]:
+    """The (hash, RaidenBlockId) pairs of a kvx_slices list, fetched with one
+    library call for the whole list; releases the list."""
     lib = _capi.load()
-    out = []
     try:
-        h, hl, bs = ctypes.c_void_p(), ctypes.c_int64(), _capi.BlockSlice()
-        for i in range(lib.kvx_slices_count(handle)):
-            _capi.check(lib.kvx_slices_get(handle, i, ctypes.byref(h), ctypes.byref(hl),
-                                           ctypes.byref(bs)))
-            rid = RaidenId((bs.job_name or b"").decode(), (bs.job_replica_id or b"").decode(),
-                           (bs.data_name or b"").decode(), bs.data_replica_idx)
-            out.append((ctypes.string_at(h, hl.value) if hl.value else b"",
-                        RaidenBlockId(rid, bs.host_block_id, bs.device_block_id,
-                                      BlockStatus(bs.status))))
+        n = lib.kvx_slices_count(handle)
+        if n == 0:
+            return []
+        hashes, offsets = ctypes.c_void_p(), _capi._i64p()
+        blocks = ctypes.POINTER(_capi.BlockSlice)()
+        _capi.check(lib.kvx_slices_flat(handle, ctypes.byref(hashes), ctypes.byref(offsets),
+                                        ctypes.byref(blocks)))
+        keys = _capi.split_flat(hashes, offsets, n)
+        raw = np.frombuffer(ctypes.string_at(blocks, n * _SLICE_DTYPE.itemsize),
+                            dtype=_SLICE_DTYPE)
+        hosts, devs = raw["host"].tolist(), raw["dev"].tolist()
+        stats, reps = raw["status"].tolist(), raw["replica"].tolist()
+        status = [_STATUS_BY_VALUE[v] for v in stats]
+        make = RaidenBlockId._of
+        names = raw["names"]
+        if (names == names[0]).all() and (raw["replica"] == reps[0]).all():
+            # One owner (the library shares equal owners' name pointers).
+            p = names[0].tolist()
+            rid = RaidenId(_c_string(p[0]), _c_string(p[1]), _c_string(p[2]), reps[0])
+            return [(k, make(rid, h, d, st))
+                    for k, h, d, st in zip(keys, hosts, devs, status)]
+        ids = {}  # one RaidenId per distinct owner
+        out = []
+        for i, row in enumerate(names.tolist()):
+            owner = (*row, reps[i])
+            rid = ids.get(owner)
+            if rid is None:
+                rid = RaidenId(_c_string(owner[0]), _c_string(owner[1]), _c_string(owner[2]),
+                               owner[3])
+                ids[owner] = rid
+            out.append((keys[i], make(rid, hosts[i], devs[i], status[i])))
+        return out
     finally:
         lib.kvx_slices_release(handle)
-    return out
 
 
 class KVCacheStore:
