@@ -915,6 +915,45 @@ def test_store_construction_rules(kvx):
     s.close()
 
 
+def test_store_lists_cross_whole(kvx):
+    """Lists fetched with one library call each (kvx_slices_flat,
+    kvx_strings_flat) give every hash and slice as fetching them one by one
+    does: slices of two owners interleaved (each with its own RaidenId),
+    empty and long hashes, statuses, and a poll's string lists."""
+    s = kvx.KVCacheStore(64, num_shards=1, store_server_ip="127.0.0.1")
+    a = kvx.RaidenId("job-a", "0", "cache", 0)
+    b = kvx.RaidenId("job-b", "3", "other", 2)
+    hashes = [b"", b"x" * 111] + [b"h%03d" % i for i in range(30)]
+    slices = [kvx.RaidenBlockId(a if i % 3 else b, -1, 100 + i, kvx.BlockStatus.HBM)
+              for i in range(len(hashes))]
+    assert s.insert(hashes, slices, on_host=False)
+    found = s.lookup(hashes, pin_found=False)
+    assert [h for h, _ in found] == hashes
+    assert [x for _, x in found] == slices
+    assert all(x.raiden_id == (a if i % 3 else b) for i, (_, x) in enumerate(found))
+    lib = kvx._capi.load()
+    import ctypes
+    buf, offs, n = kvx._capi.pack_bytes(hashes)
+    out = ctypes.c_void_p()
+    assert lib.kvx_store_lookup(s._h, buf, offs, n, 0, ctypes.byref(out)) == 0
+    h, hl, bs = ctypes.c_void_p(), ctypes.c_int64(), kvx._capi.BlockSlice()
+    for i, (hash_, x) in enumerate(found):
+        assert lib.kvx_slices_get(out, i, ctypes.byref(h), ctypes.byref(hl), ctypes.byref(bs)) == 0
+        assert ctypes.string_at(h, hl.value) == hash_
+        assert (bs.job_name.decode(), bs.job_replica_id.decode(), bs.data_name.decode(),
+                bs.data_replica_idx) == (x.job_name, x.job_replica_id, x.data_name,
+                                         x.data_replica_idx)
+        assert (bs.device_block_id, bs.status) == (x.device_block_id, int(x.status))
+    lib.kvx_slices_release(out)
+    assert lib.kvx_slices_flat(None, None, None, None) == 3
+    assert lib.kvx_strings_flat(None, None, None) == 3
+    # Saves through no worker fail in the poll: the failed list comes whole.
+    assert s.save(hashes[:5])
+    done, failed = s.poll_save_status()[:2]
+    assert done == [] and sorted(failed) == sorted(hashes[:5])
+    s.close()
+
+
 def test_manager_joins_the_store_controller(kvx):
     """A manager created with the store's controller address becomes its
     worker; an unknown address is an error."""
