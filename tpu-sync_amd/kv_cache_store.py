@@ -118,29 +118,48 @@ class RaidenBlockId:
                 f"device_block_id={self._device_block_id}, status={self._status.name})")
 
 
-def _c_slices(slices: Sequence) -> Tuple[ctypes.Array, int, list]:
-    keep = []
-    arr = (_capi.BlockSlice * max(len(slices), 1))()
-    for i, s in enumerate(slices):
-        if isinstance(s, RaidenId):
-            s = RaidenBlockId(raiden_id=s)
-        rid = s.raiden_id
-        strs = [rid.job_name.encode(), rid.job_replica_id.encode(), rid.data_name.encode()]
-        keep.extend(strs)
-        arr[i].host_block_id = s.host_block_id
-        arr[i].device_block_id = s.device_block_id
-        arr[i].status = int(s.status)
-        arr[i].data_replica_idx = rid.data_replica_idx
-        arr[i].job_name, arr[i].job_replica_id, arr[i].data_name = strs
-    return arr, len(slices), keep
-
-
-# kvx_block_slice as numpy reads it: four int32 fields, then the three name
-# pointers.
+# kvx_block_slice as numpy lays it out: four int32 fields, then the three
+# name pointers.
 _SLICE_DTYPE = np.dtype([("host", "<i4"), ("dev", "<i4"), ("status", "<i4"),
                          ("replica", "<i4"), ("names", "<u8", (3,))])
 assert _SLICE_DTYPE.itemsize == ctypes.sizeof(_capi.BlockSlice)
 _STATUS_BY_VALUE = {int(s): s for s in BlockStatus}
+
+
+def _c_slices(slices: Sequence):
+    """kvx_block_slice array of `slices` (RaidenBlockId, or RaidenId for a
+    bare owner): (pointer, count, objects that must outlive the call). Each
+    distinct owner's names are encoded once."""
+    keep = []
+    owners = {}  # id(RaidenId) -> its three name addresses
+    hosts, devs, stats, reps, names = [], [], [], [], []
+    for s in slices:
+        if isinstance(s, RaidenId):
+            s = RaidenBlockId(raiden_id=s)
+        rid = s._raiden_id
+        row = owners.get(id(rid))
+        if row is None:
+            encoded = [rid.job_name.encode(), rid.job_replica_id.encode(),
+                       rid.data_name.encode()]
+            keep.extend(encoded)
+            keep.append(rid)  # keeps id(rid) unique while the table is used
+            row = [ctypes.cast(ctypes.c_char_p(b), ctypes.c_void_p).value for b in encoded]
+            owners[id(rid)] = row
+        hosts.append(s._host_block_id)
+        devs.append(s._device_block_id)
+        stats.append(s._status)
+        reps.append(rid.data_replica_idx)
+        names.append(row)
+    n = len(hosts)
+    raw = np.zeros(max(n, 1), dtype=_SLICE_DTYPE)
+    if n:
+        raw["host"][:n] = hosts
+        raw["dev"][:n] = devs
+        raw["status"][:n] = stats
+        raw["replica"][:n] = reps
+        raw["names"][:n] = names
+    keep.append(raw)
+    return raw.ctypes.data_as(ctypes.POINTER(_capi.BlockSlice)), n, keep
 
 
 def _c_string(ptr: int) -> str:
