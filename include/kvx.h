@@ -441,7 +441,8 @@ void kvx_strings_release(kvx_strings* s);
 /* The whole list at once (no reference counterpart: one call instead of one
  * per item for bindings that convert long lists): item i is
  * data[offsets[i], offsets[i + 1]), offsets has count + 1 entries. Both stay
- * valid until kvx_strings_release. */
+ * valid until kvx_strings_release. The first call builds them: calls on one
+ * list from several threads at once must be serialised by the caller. */
 int kvx_strings_flat(kvx_strings* s, const uint8_t** data, const int64_t** offsets);
 int64_t kvx_slices_count(const kvx_slices* s);
 /* Pointers written to *hash and the strings of *out stay valid until
@@ -451,7 +452,9 @@ int kvx_slices_get(const kvx_slices* s, int64_t i, const uint8_t** hash,
 void kvx_slices_release(kvx_slices* s);
 /* The whole list at once, as kvx_strings_flat: hash i is
  * hashes[offsets[i], offsets[i + 1]) and blocks[i] its slice (count entries);
- * all valid until kvx_slices_release. */
+ * all valid until kvx_slices_release, with the same threading rule. Slices
+ * whose owner names are equal to one of the list's first 16 distinct owners
+ * share that owner's name pointers. */
 int kvx_slices_flat(kvx_slices* s, const uint8_t** hashes, const int64_t** offsets,
                     const kvx_block_slice** blocks);
 

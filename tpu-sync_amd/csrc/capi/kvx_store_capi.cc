@@ -160,7 +160,9 @@ int kvx_slices_flat(kvx_slices* s, const uint8_t** hashes, const int64_t** offse
     s->blocks.reserve(s->items.size());
     // Slices with equal owner names share the first one's name pointers, so
     // a binding can recognise the owner by pointer (a store's slices nearly
-    // always have one owner).
+    // always have one owner). At most kMaxOwners are interned, which bounds
+    // the search per slice.
+    constexpr size_t kMaxOwners = 16;
     std::vector<const kvx::RaidenId*> owners;
     for (const auto& p : s->items) {
       s->hashes += p.first;
@@ -174,7 +176,7 @@ int kvx_slices_flat(kvx_slices* s, const uint8_t** hashes, const int64_t** offse
           break;
         }
       }
-      if (owner == &id) owners.push_back(owner);
+      if (owner == &id && owners.size() < kMaxOwners) owners.push_back(owner);
       kvx_block_slice b{};
       b.host_block_id = p.second.host_block_id;
       b.device_block_id = p.second.device_block_id;
