@@ -844,9 +844,13 @@ StatusOr<CopyFuture> TransferEngine::CopyStaged(
   const int64_t chunks_before = stats_.chunks;
   KVX_RETURN_IF_ERROR(StagedOnLane(lane, dir, storages, cdev, chost, dep, &done));
   ++stats_.staged_copies;
-  // Track the chunks this copy keeps in flight (Copy() keeps the total
-  // bounded; see EngineOptions::auto_lanes_min_chunks). The copy is already
-  // enqueued: if no event can be had it goes untracked rather than failing.
+  // Track the chunks this copy keeps in flight (in auto mode Copy() keeps the
+  // total bounded; see EngineOptions::auto_lanes_min_chunks). Finished copies
+  // leave the list first, so it holds only copies still in flight. The copy
+  // is already enqueued: if no event can be had it goes untracked rather than
+  // failing.
+  if (opts_.mode != TransferMode::kAuto) return CopyFuture::FromEvents({done}, {});
+  (void)StagedChunksInFlightLocked(dir);
   hipEvent_t track = nullptr;
   if (!spare_events_.empty()) {
     track = spare_events_.back();
