@@ -806,6 +806,36 @@ int kvx_manager_h2d_pool_blocks(kvx_manager* m, int64_t pool_idx,
  * ------------------------------------------------------------------------- */
 typedef struct kvx_weight_sync kvx_weight_sync;
 
+/* A tiled tensor layout, the xla::Shape + xla::Layout pair the reference's
+ * tiling routines take (tpu_sync/weight_sync/tiling_utils.h:27-36), written
+ * out as numbers: element size, logical dimensions (row-major), their
+ * minor-to-major order, and up to 4 tiles applied in turn (dimensions >= 1).
+ * num_tiles = 0 means row-major bytes with no tiling. */
+#define KVX_TILED_MAX_RANK 8
+#define KVX_TILED_MAX_TILES 4
+typedef struct kvx_tiled_layout {
+  int32_t itemsize;                       /* 1, 2, 4 or 8 */
+  int32_t rank;                           /* 0..8 */
+  int64_t dims[KVX_TILED_MAX_RANK];
+  int32_t minor_to_major[KVX_TILED_MAX_RANK];
+  int32_t num_tiles;                      /* 0..4 */
+  int32_t tile_rank[KVX_TILED_MAX_TILES]; /* 1..8 each */
+  int32_t reserved;
+  int64_t tile_dims[KVX_TILED_MAX_TILES][KVX_TILED_MAX_RANK];
+} kvx_tiled_layout;
+
+/* GetTiledBufferElements (tiling_utils.cc:905-957): elements of the tiled
+ * buffer, padding included. Host only. */
+int kvx_tiled_buffer_elements(const kvx_tiled_layout* layout, int64_t* out);
+/* TileBuffer / DetileBuffer (tiling_utils.cc:959-1036) on device buffers:
+ * the linear image holds the logical elements row-major, the tiled buffer
+ * kvx_tiled_buffer_elements() elements; tiling writes zero into padding.
+ * Enqueued on `stream`; the future completes with the copy. */
+int kvx_tile_buffer(int32_t device, const kvx_tiled_layout* layout, uint64_t src_linear,
+                    uint64_t dst_tiled, void* stream, kvx_future** out);
+int kvx_detile_buffer(int32_t device, const kvx_tiled_layout* layout, uint64_t src_tiled,
+                      uint64_t dst_linear, void* stream, kvx_future** out);
+
 typedef struct kvx_weight_sync_config {
   int32_t device;
   int32_t host_alloc;          /* KVX_HOST_PINNED or KVX_HOST_MALLOC */
@@ -817,6 +847,12 @@ typedef struct kvx_weight_sync_config {
   int64_t staging_chunks;      /* ring depth, 0 = 2 */
   int32_t profile_kernels;
   int32_t numa_off;            /* 1: OS placement of the host image; 0: GPU's node */
+  /* NULL, or one layout per tensor: a tensor whose layout has tiles is
+   * stored tiled on the device (device_bytes >= its tiled size) and its host
+   * copy is the linear image (D2hLayer detiles, H2dLayer tiles, as
+   * weight_synchronizer_base.cc:357-389, 473-510 do on the host); here the
+   * detile / tile runs in HBM on the staging chunks. */
+  const kvx_tiled_layout* layouts;
 } kvx_weight_sync_config;
 
 int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** out);

@@ -21,6 +21,12 @@ Parity status of each function (what pins it):
       numpy fancy indexing (pool[:, ids]) as an independent library routine,
       round trips, untouched-block checks and the reference's e2e known
       answers (shift copy, partial chunks, auto-allocate).
+  tiled_elements / tile / detile (XLA nested tiling, element by element):
+      the reference tiling tests' known answers (tests/golden/tiling_cases.json:
+      element counts and values at given physical positions, padding zeros),
+      an independent numpy formulation of 2-D tiling (pad, reshape, swap
+      axes) and of the (P, 1) row packing, round trips, and brute-force
+      bijection / padding checks (tests/test_tiling_oracle.py).
 """
 import ctypes
 import os
@@ -66,6 +72,13 @@ def lib():
                                         ctypes.c_int, ctypes.c_void_p]
         l.oracle_write_block.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_int64]
+        _i32p = ctypes.POINTER(ctypes.c_int32)
+        l.oracle_tiled_elements.restype = ctypes.c_int64
+        l.oracle_tiled_elements.argtypes = [ctypes.c_int, _i64p, _i32p, ctypes.c_int,
+                                            _i32p, _i64p]
+        for fn in (l.oracle_tile, l.oracle_detile):
+            fn.argtypes = [ctypes.c_int, ctypes.c_int, _i64p, _i32p, ctypes.c_int, _i32p,
+                           _i64p, ctypes.c_void_p, ctypes.c_void_p]
         for fn in (l.oracle_extract, l.oracle_insert):
             fn.argtypes = [_u8pp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                            _i64p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
@@ -190,3 +203,63 @@ def insert(pools, block_bytes, ids, staging, order=0, nthreads=1):
     staging = np.ascontiguousarray(staging, dtype=np.uint8)
     return lib().oracle_insert(pp, len(pools), pools[0].nbytes, block_bytes, ap, len(a),
                                staging.ctypes.data, order, nthreads)
+
+
+def _layout_arrays(layout):
+    """(itemsize, dims, minor_to_major, tiles) of a dict or an object."""
+    get = (lambda k: layout[k]) if isinstance(layout, dict) else (lambda k: getattr(layout, k))
+    itemsize = int(get("itemsize"))
+    dims = np.ascontiguousarray(np.asarray(get("dims"), dtype=np.int64).reshape(-1))
+    mtm = np.ascontiguousarray(np.asarray(get("minor_to_major"), dtype=np.int32).reshape(-1))
+    tiles = [list(t) for t in get("tiles")]
+    trank = np.asarray([len(t) for t in tiles] or [0], dtype=np.int32)
+    tdims = np.zeros((max(len(tiles), 1), 8), dtype=np.int64)
+    for i, t in enumerate(tiles):
+        tdims[i, : len(t)] = t
+    if dims.size == 0:
+        dims = np.zeros(1, np.int64)
+        mtm = np.zeros(1, np.int32)
+        rank = 0
+    else:
+        rank = int(dims.size)
+    i32 = ctypes.POINTER(ctypes.c_int32)
+    keep = (dims, mtm, trank, tdims)
+    args = (rank, dims.ctypes.data_as(_i64p), mtm.ctypes.data_as(i32), len(tiles),
+            trank.ctypes.data_as(i32), tdims.ctypes.data_as(_i64p))
+    return itemsize, args, keep
+
+
+def tiled_elements(layout):
+    """GetTiledBufferElements of a layout (dict or object with itemsize, dims,
+    minor_to_major, tiles)."""
+    _, args, keep = _layout_arrays(layout)
+    return int(lib().oracle_tiled_elements(*args))
+
+
+def logical_elements(layout):
+    _, args, keep = _layout_arrays(layout)
+    return int(np.prod(keep[0])) if args[0] > 0 else 1
+
+
+def tile(layout, linear):
+    """TileBuffer: linear bytes -> tiled bytes (padding zero)."""
+    itemsize, args, keep = _layout_arrays(layout)
+    linear = np.ascontiguousarray(np.asarray(linear).view(np.uint8).reshape(-1))
+    n = tiled_elements(layout) if len(layout["tiles"] if isinstance(layout, dict)
+                                      else layout.tiles) else logical_elements(layout)
+    out = np.full(n * itemsize, 0xA5, np.uint8)
+    rc = lib().oracle_tile(itemsize, *args, linear.ctypes.data, out.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle_tile failed: %d" % rc)
+    return out
+
+
+def detile(layout, tiled):
+    """DetileBuffer: tiled bytes -> linear bytes."""
+    itemsize, args, keep = _layout_arrays(layout)
+    tiled = np.ascontiguousarray(np.asarray(tiled).view(np.uint8).reshape(-1))
+    out = np.zeros(logical_elements(layout) * itemsize, np.uint8)
+    rc = lib().oracle_detile(itemsize, *args, tiled.ctypes.data, out.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle_detile failed: %d" % rc)
+    return out

@@ -23,6 +23,10 @@
  *                          contiguous staging buffer, layer-major
  *                          (tpu_sync/core/kv_cache_manager_with_transfer.cc:1807-1857
  *                          lays a slot out per layer).
+ *   oracle_tiled_elements / oracle_tile / oracle_detile
+ *                          tpu_sync/weight_sync/tiling_utils.cc:905-1036
+ *                          (GetTiledBufferElements, TileBuffer, DetileBuffer:
+ *                          XLA's nested tiling, element by element)
  * The reference C++ cannot be compiled here (Bazel, abseil, XLA/PJRT and
  * generated protos are absent), so there is no oracle/_ref build.
  */
@@ -294,4 +298,146 @@ int oracle_insert(uint8_t* const* pools, int64_t nstor, int64_t pool_bytes,
                   const uint8_t* staging, int order, int nthreads) {
   return pack(1, pools, nstor, pool_bytes, block_bytes, ids, n,
               (uint8_t*)staging, order, nthreads);
+}
+
+/* ---------------------------------------------------------------------------
+ * Tiled layouts. A layout: element size, logical dimensions (row-major),
+ * minor_to_major, and tiles applied in turn (tile t has tile_rank[t]
+ * dimensions at tile_dims[t * 8 ...]). The shape the tiles apply to is the
+ * logical shape in major-to-minor order (rank 1: (1, d0)); a tile of rank k
+ * turns the k minor-most dimensions d into ceil(d / t) followed by t, after
+ * padding the shape with leading 1s if k exceeds its rank
+ * (tiling_utils.cc:905-957). An element's physical position is its index
+ * carried through the same steps (i -> i / t and i % t) and linearised
+ * row-major over the final shape; positions no element reaches are padding.
+ * ------------------------------------------------------------------------- */
+#define TILED_MAX 48
+
+typedef struct {
+  int n;
+  int64_t size[TILED_MAX];
+  int64_t idx[TILED_MAX];
+} tiled_vec;
+
+/* Carries a logical index (or, with idx NULL, only the shape) through the
+ * tiles. Returns 0, or -1 if the shape grows past TILED_MAX dimensions. */
+static int tiled_walk(int rank, const int64_t* dims, const int32_t* mtm, int ntiles,
+                      const int32_t* tile_rank, const int64_t* tile_dims,
+                      const int64_t* idx, tiled_vec* v) {
+  v->n = 0;
+  if (rank == 1) {
+    v->size[0] = 1;
+    v->idx[0] = 0;
+    v->size[1] = dims[0];
+    v->idx[1] = idx ? idx[0] : 0;
+    v->n = 2;
+  } else {
+    for (int i = rank - 1; i >= 0; --i) {
+      v->size[v->n] = dims[mtm[i]];
+      v->idx[v->n] = idx ? idx[mtm[i]] : 0;
+      v->n++;
+    }
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    const int k = tile_rank[t];
+    const int64_t* td = tile_dims + 8 * t;
+    tiled_vec nv;
+    int pad = k > v->n ? k - v->n : 0;
+    if (v->n + pad + k > TILED_MAX) return -1;
+    /* Leading 1s when the tile has more dimensions than the shape. */
+    nv.n = 0;
+    for (int i = 0; i < pad; ++i) {
+      nv.size[nv.n] = 1;
+      nv.idx[nv.n] = 0;
+      nv.n++;
+    }
+    for (int i = 0; i < v->n; ++i) {
+      nv.size[nv.n] = v->size[i];
+      nv.idx[nv.n] = v->idx[i];
+      nv.n++;
+    }
+    const int start = nv.n - k;
+    tiled_vec out;
+    out.n = 0;
+    for (int i = 0; i < start; ++i) {
+      out.size[out.n] = nv.size[i];
+      out.idx[out.n] = nv.idx[i];
+      out.n++;
+    }
+    for (int i = 0; i < k; ++i) {
+      out.size[out.n] = (nv.size[start + i] + td[i] - 1) / td[i];
+      out.idx[out.n] = nv.idx[start + i] / td[i];
+      out.n++;
+    }
+    for (int i = 0; i < k; ++i) {
+      out.size[out.n] = td[i];
+      out.idx[out.n] = nv.idx[start + i] % td[i];
+      out.n++;
+    }
+    *v = out;
+  }
+  return 0;
+}
+
+int64_t oracle_tiled_elements(int rank, const int64_t* dims, const int32_t* mtm, int ntiles,
+                              const int32_t* tile_rank, const int64_t* tile_dims) {
+  if (rank == 0) return 1;
+  tiled_vec v;
+  if (tiled_walk(rank, dims, mtm, ntiles, tile_rank, tile_dims, NULL, &v) != 0) return -1;
+  int64_t n = 1;
+  for (int i = 0; i < v.n; ++i) n *= v.size[i];
+  return n;
+}
+
+static int64_t tiled_position(int rank, const int64_t* dims, const int32_t* mtm, int ntiles,
+                              const int32_t* tile_rank, const int64_t* tile_dims,
+                              const int64_t* idx) {
+  tiled_vec v;
+  if (tiled_walk(rank, dims, mtm, ntiles, tile_rank, tile_dims, idx, &v) != 0) return -1;
+  int64_t p = 0;
+  for (int i = 0; i < v.n; ++i) p = p * v.size[i] + v.idx[i];
+  return p;
+}
+
+static int tiled_copy(int tile, int itemsize, int rank, const int64_t* dims, const int32_t* mtm,
+                      int ntiles, const int32_t* tile_rank, const int64_t* tile_dims,
+                      const uint8_t* src, uint8_t* dst) {
+  int64_t logical = 1;
+  for (int i = 0; i < rank; ++i) logical *= dims[i];
+  if (ntiles == 0 || rank == 0) {
+    memcpy(dst, src, (size_t)(logical * itemsize));
+    return OK;
+  }
+  const int64_t phys =
+      oracle_tiled_elements(rank, dims, mtm, ntiles, tile_rank, tile_dims);
+  if (phys < 0) return INVALID_ARGUMENT;
+  if (tile && phys > logical) memset(dst, 0, (size_t)(phys * itemsize));
+  int64_t idx[8];
+  for (int64_t e = 0; e < logical; ++e) {
+    int64_t rest = e;
+    for (int r = rank - 1; r >= 0; --r) {
+      idx[r] = rest % dims[r];
+      rest /= dims[r];
+    }
+    const int64_t p = tiled_position(rank, dims, mtm, ntiles, tile_rank, tile_dims, idx);
+    if (p < 0 || p >= phys) return INVALID_ARGUMENT;
+    if (tile) {
+      memcpy(dst + p * itemsize, src + e * itemsize, (size_t)itemsize);
+    } else {
+      memcpy(dst + e * itemsize, src + p * itemsize, (size_t)itemsize);
+    }
+  }
+  return OK;
+}
+
+int oracle_tile(int itemsize, int rank, const int64_t* dims, const int32_t* mtm, int ntiles,
+                const int32_t* tile_rank, const int64_t* tile_dims, const uint8_t* linear,
+                uint8_t* tiled) {
+  return tiled_copy(1, itemsize, rank, dims, mtm, ntiles, tile_rank, tile_dims, linear, tiled);
+}
+
+int oracle_detile(int itemsize, int rank, const int64_t* dims, const int32_t* mtm, int ntiles,
+                  const int32_t* tile_rank, const int64_t* tile_dims, const uint8_t* tiled,
+                  uint8_t* linear) {
+  return tiled_copy(0, itemsize, rank, dims, mtm, ntiles, tile_rank, tile_dims, tiled, linear);
 }

@@ -9,7 +9,7 @@ from ._capi import KvxError
 from .kv_cache_manager import KVCacheManager, LogicalBlockManager, RaidenFuture
 from .kv_cache_store import (BlockStatus, KVCacheMetadata, KVCacheMetadataShmRegion,
                              KVCacheStore, LRUCache, RaidenBlockId, RaidenId)
-from . import copy_plan, pool_layout, transport
+from . import copy_plan, pool_layout, tiling, transport
 from .pool_layout import PoolSpec, RegionSpec
 from .weight_synchronizer import (StridedEntry, StridedPlan, WeightSynchronizer,
                                   column_split_entries, compute_nd_shard_slices, copy_strided)
@@ -18,7 +18,7 @@ __all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError",
            "KVCacheStore", "RaidenId", "RaidenBlockId", "BlockStatus", "LRUCache",
            "KVCacheMetadata", "KVCacheMetadataShmRegion", "WeightSynchronizer",
            "StridedEntry", "StridedPlan", "copy_strided", "column_split_entries",
-           "compute_nd_shard_slices", "pool_layout", "copy_plan", "transport", "PoolSpec", "RegionSpec",
+           "compute_nd_shard_slices", "pool_layout", "copy_plan", "tiling", "transport", "PoolSpec", "RegionSpec",
            "library_path"]
 
 

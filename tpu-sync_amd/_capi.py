@@ -95,6 +95,19 @@ class StoreConfig(ctypes.Structure):
     ]
 
 
+class TiledLayoutC(ctypes.Structure):
+    _fields_ = [
+        ("itemsize", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * 8),
+        ("minor_to_major", ctypes.c_int32 * 8),
+        ("num_tiles", ctypes.c_int32),
+        ("tile_rank", ctypes.c_int32 * 4),
+        ("reserved", ctypes.c_int32),
+        ("tile_dims", (ctypes.c_int64 * 8) * 4),
+    ]
+
+
 class WeightSyncConfig(ctypes.Structure):
     _fields_ = [
         ("device", ctypes.c_int32),
@@ -107,6 +120,7 @@ class WeightSyncConfig(ctypes.Structure):
         ("staging_chunks", ctypes.c_int64),
         ("profile_kernels", ctypes.c_int32),
         ("numa_off", ctypes.c_int32),
+        ("layouts", ctypes.POINTER(TiledLayoutC)),
     ]
 
 
@@ -362,6 +376,11 @@ PROTOTYPES = {
                                        ctypes.POINTER(_vp)]),
     "kvx_strided_plan_run": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
     "kvx_strided_plan_destroy": (None, [_vp]),
+    "kvx_tiled_buffer_elements": (_int, [ctypes.POINTER(TiledLayoutC), ctypes.POINTER(_i64)]),
+    "kvx_tile_buffer": (_int, [_i32, ctypes.POINTER(TiledLayoutC), _u64, _u64, _vp,
+                               ctypes.POINTER(_vp)]),
+    "kvx_detile_buffer": (_int, [_i32, ctypes.POINTER(TiledLayoutC), _u64, _u64, _vp,
+                                 ctypes.POINTER(_vp)]),
     "kvx_manager_numa_node": (_i32, [_vp]),
     "kvx_manager_host_ptr": (_u64, [_vp, _i64, _i64]),
     "kvx_manager_host_size": (_i64, [_vp, _i64, _i64]),

@@ -50,9 +50,64 @@ int ToCopies(const kvx_strided_entry* entries, int64_t n, std::vector<kvx::Strid
   return KVX_OK;
 }
 
+// Validates a C layout and converts it.
+int ToLayout(const kvx_tiled_layout* l, kvx::TiledLayout* out) {
+  if (l == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null layout");
+  if (l->rank < 0 || l->rank > KVX_TILED_MAX_RANK || l->num_tiles < 0 ||
+      l->num_tiles > KVX_TILED_MAX_TILES) {
+    return Fail(KVX_INVALID_ARGUMENT, "tiled layout: rank or tile count out of range");
+  }
+  out->itemsize = l->itemsize;
+  out->dims.assign(l->dims, l->dims + l->rank);
+  out->minor_to_major.assign(l->minor_to_major, l->minor_to_major + l->rank);
+  out->tiles.clear();
+  for (int t = 0; t < l->num_tiles; ++t) {
+    const int32_t k = l->tile_rank[t];
+    if (k < 1 || k > KVX_TILED_MAX_RANK) {
+      return Fail(KVX_INVALID_ARGUMENT, "tiled layout: a tile has 1 to 8 dimensions");
+    }
+    out->tiles.emplace_back(l->tile_dims[t], l->tile_dims[t] + k);
+  }
+  return KVX_OK;
+}
+
+int TileCall(int32_t device, const kvx_tiled_layout* layout, uint64_t linear, uint64_t tiled,
+             bool tile, void* stream, kvx_future** out) {
+  if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
+  kvx::TiledLayout l;
+  const int rc = ToLayout(layout, &l);
+  if (rc != KVX_OK) return rc;
+  auto plan = kvx::PlanTiled(l);
+  if (!plan.ok()) return Fail(plan.status());
+  return Emit(kvx::TileOnDevice(device, plan.value(), linear, tiled, tile,
+                                static_cast<hipStream_t>(stream)),
+              out);
+}
+
 }  // namespace
 
 extern "C" {
+
+int kvx_tiled_buffer_elements(const kvx_tiled_layout* layout, int64_t* out) {
+  if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
+  kvx::TiledLayout l;
+  const int rc = ToLayout(layout, &l);
+  if (rc != KVX_OK) return rc;
+  auto n = kvx::TiledBufferElements(l);
+  if (!n.ok()) return Fail(n.status());
+  *out = n.value();
+  return KVX_OK;
+}
+
+int kvx_tile_buffer(int32_t device, const kvx_tiled_layout* layout, uint64_t src_linear,
+                    uint64_t dst_tiled, void* stream, kvx_future** out) {
+  return TileCall(device, layout, src_linear, dst_tiled, true, stream, out);
+}
+
+int kvx_detile_buffer(int32_t device, const kvx_tiled_layout* layout, uint64_t src_tiled,
+                      uint64_t dst_linear, void* stream, kvx_future** out) {
+  return TileCall(device, layout, dst_linear, src_tiled, false, stream, out);
+}
 
 int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** out) {
   if (cfg == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null config or output");
@@ -78,6 +133,19 @@ int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** 
   if (cfg->staging_chunks > 0) c.staging_chunks = static_cast<int>(cfg->staging_chunks);
   c.profile_kernels = cfg->profile_kernels != 0;
   c.numa_local = cfg->numa_off == 0;
+  if (cfg->layouts != nullptr) {
+    c.tiled.resize(static_cast<size_t>(n));
+    for (int64_t k = 0; k < n; ++k) {
+      if (cfg->layouts[k].num_tiles == 0) continue;
+      kvx::TiledLayout l;
+      const int rc = ToLayout(&cfg->layouts[k], &l);
+      if (rc != KVX_OK) return rc;
+      auto plan = kvx::PlanTiled(l);
+      if (!plan.ok()) return Fail(plan.status());
+      c.tiled[static_cast<size_t>(k)] =
+          std::make_shared<const kvx::TiledPlan>(std::move(plan).value());
+    }
+  }
   auto r = kvx::WeightSynchronizer::Create(std::move(c));
   if (!r.ok()) return Fail(r.status());
   *out = new kvx_weight_sync{std::move(r).value()};

@@ -41,14 +41,30 @@ Status WeightSynchronizer::Init() {
   if (cfg_.chunk_bytes <= 0 || cfg_.staging_chunks <= 0) {
     return InvalidArgumentError("staging chunk size and count must be positive");
   }
+  if (!cfg_.tiled.empty() && static_cast<int64_t>(cfg_.tiled.size()) != n) {
+    return InvalidArgumentError("tiled layouts need num_layers * num_shards entries (or none)");
+  }
   off_.resize(n);
+  host_bytes_.resize(n);
   int64_t pos = 0;
   for (int64_t k = 0; k < n; ++k) {
     if (cfg_.device_bytes[k] < 0 || (cfg_.device_bytes[k] > 0 && cfg_.device_ptrs[k] == 0)) {
       return InvalidArgumentError("null device pointer or negative size");
     }
+    host_bytes_[k] = cfg_.device_bytes[k];
+    if (const TiledPlan* tp = plan(k)) {
+      if (cfg_.device_bytes[k] < tp->tiled_bytes) {
+        return InvalidArgumentError("tensor " + std::to_string(k) +
+                                    ": device buffer smaller than its tiled layout (" +
+                                    std::to_string(tp->tiled_bytes) + " bytes)");
+      }
+      if (tp->tiled_bytes > 0 && cfg_.device_ptrs[k] == 0) {
+        return InvalidArgumentError("null device pointer");
+      }
+      host_bytes_[k] = tp->logical_bytes;
+    }
     off_[k] = pos;
-    pos = AlignUp(pos + cfg_.device_bytes[k], kTensorAlign);
+    pos = AlignUp(pos + host_bytes_[k], kTensorAlign);
   }
   total_ = pos;
   DeviceGuard g(cfg_.device);
@@ -71,6 +87,17 @@ Status WeightSynchronizer::Init() {
   KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueues({&ks_, &d2h_, &h2d_}));
   const int64_t chunk = std::min<int64_t>(cfg_.chunk_bytes, std::max<int64_t>(total_, 1));
   cfg_.chunk_bytes = chunk;
+  // A chunk must hold one row group of every tiled tensor.
+  for (int64_t k = 0; k < n; ++k) {
+    const TiledPlan* tp = plan(k);
+    if (tp == nullptr || !tp->standard) continue;
+    const int64_t group = static_cast<int64_t>(tp->P * tp->W) * tp->layout.itemsize;
+    if (group > chunk) {
+      return InvalidArgumentError("tensor " + std::to_string(k) + ": a row group (" +
+                                  std::to_string(group) +
+                                  " bytes) does not fit a staging chunk");
+    }
+  }
   for (int k = 0; k < cfg_.staging_chunks; ++k) {
     void* p = nullptr;
     KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, chunk));
@@ -112,9 +139,13 @@ Status WeightSynchronizer::WaitDep(hipStream_t dep, hipStream_t on) {
   return st;
 }
 
-void WeightSynchronizer::RangeEntries(int64_t lo, int64_t hi, uint64_t image, bool pack,
-                                      std::vector<StridedCopy>* out) const {
+Status WeightSynchronizer::RangeEntries(int64_t lo, int64_t hi, uint64_t image, bool pack,
+                                        std::vector<StridedCopy>* out,
+                                        std::vector<TiledJob>* zero,
+                                        std::vector<TiledJob>* tiled) const {
   out->clear();
+  zero->clear();
+  tiled->clear();
   // Tensors are laid out in ascending offset order: find the first one that
   // ends after lo.
   const int64_t n = static_cast<int64_t>(off_.size());
@@ -122,8 +153,17 @@ void WeightSynchronizer::RangeEntries(int64_t lo, int64_t hi, uint64_t image, bo
   if (k < 0) k = 0;
   for (; k < n && off_[k] < hi; ++k) {
     const int64_t a = std::max(lo, off_[k]);
-    const int64_t b = std::min(hi, off_[k] + cfg_.device_bytes[k]);
+    const int64_t b = std::min(hi, off_[k] + host_bytes_[k]);
     if (a >= b) continue;
+    if (const TiledPlan* tp = plan(k)) {
+      // The linear image of tensor k starts (off_k - lo) bytes into `image`
+      // (only its bytes in [a, b) are touched).
+      const uint64_t origin = image + static_cast<uint64_t>(off_[k]) - static_cast<uint64_t>(lo);
+      KVX_RETURN_IF_ERROR(AppendTiledJobs(*tp, cfg_.device_ptrs[k], origin, a - off_[k],
+                                          b - off_[k], /*tile=*/!pack,
+                                          /*zero_pass=*/a == off_[k], zero, tiled));
+      continue;
+    }
     StridedCopy c;
     const uint64_t dev = cfg_.device_ptrs[k] + static_cast<uint64_t>(a - off_[k]);
     const uint64_t img = image + static_cast<uint64_t>(a - lo);
@@ -133,21 +173,43 @@ void WeightSynchronizer::RangeEntries(int64_t lo, int64_t hi, uint64_t image, bo
     c.count = 1;
     out->push_back(c);
   }
+  return OkStatus();
 }
 
-Status WeightSynchronizer::Launch(const std::vector<StridedCopy>& copies, bool pack,
+Status WeightSynchronizer::Launch(const std::vector<StridedCopy>& copies,
+                                  const std::vector<TiledJob>& zero,
+                                  const std::vector<TiledJob>& tiled, bool pack,
                                   hipStream_t stream) {
   Sample s;
   if (cfg_.profile_kernels) {
     KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.start));
     KVX_HIP_RETURN_IF_ERROR(hipEventCreate(&s.stop));
   }
-  // The start event goes on the stream after the table upload, so a sample
-  // times the kernel alone.
-  KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(args_, copies, stream, 0, s.start));
+  // The start event goes on the stream after the first table upload, so a
+  // sample times the kernels alone. Padding is cleared before any data of
+  // the same tensors is written.
+  hipEvent_t start = s.start;
+  if (!zero.empty()) {
+    KVX_RETURN_IF_ERROR(LaunchTiledThroughRing(args_, zero, stream, start));
+    start = nullptr;
+  }
+  if (!copies.empty()) {
+    KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(args_, copies, stream, 0, start));
+    start = nullptr;
+  }
+  if (!tiled.empty()) {
+    KVX_RETURN_IF_ERROR(LaunchTiledThroughRing(args_, tiled, stream, start));
+    start = nullptr;
+  }
   if (cfg_.profile_kernels) {
+    if (start != nullptr) KVX_HIP_RETURN_IF_ERROR(hipEventRecord(start, stream));
     KVX_HIP_RETURN_IF_ERROR(hipEventRecord(s.stop, stream));
     for (const StridedCopy& c : copies) s.bytes += c.size * (c.count > 0 ? c.count : 1);
+    for (const TiledJob& j : tiled) {
+      const bool std_form = j.dev.mode == kDetileStd || j.dev.mode == kTileStd;
+      s.bytes += static_cast<int64_t>(j.dev.count) *
+                 (std_form ? static_cast<int64_t>(j.dev.P) * j.vec : j.dev.itemsize);
+    }
     s.pack = pack;
     samples_.push_back(s);
   }
@@ -183,6 +245,61 @@ Status WeightSynchronizer::KernelTimes(bool pack, bool reset, int64_t* launches,
   return OkStatus();
 }
 
+StatusOr<int64_t> WeightSynchronizer::CutBelow(int64_t lo, int64_t x) const {
+  const int64_t n = static_cast<int64_t>(off_.size());
+  const int64_t k = std::upper_bound(off_.begin(), off_.end(), x) - off_.begin() - 1;
+  int64_t cut;
+  const TiledPlan* tp = k >= 0 && k < n ? plan(k) : nullptr;
+  if (tp != nullptr && x < off_[k] + host_bytes_[k]) {
+    cut = off_[k] + tp->CutAtOrBelow(x - off_[k]);
+  } else {
+    // Elsewhere keep chunk starts 256-byte aligned, like the tensors.
+    cut = x / kTensorAlign * kTensorAlign;
+    if (cut <= lo) cut = x;
+  }
+  if (cut <= lo) {
+    return InternalError("staging chunk holds no whole row group of tensor " + std::to_string(k));
+  }
+  return cut;
+}
+
+Status WeightSynchronizer::ChunkRange(bool d2h, int64_t range_lo, int64_t range_hi) {
+  hipStream_t cs = d2h ? d2h_ : h2d_;
+  const int64_t C = cfg_.chunk_bytes;
+  std::vector<StridedCopy> entries;
+  std::vector<TiledJob> zero, tiled;
+  int64_t hi = range_lo;
+  for (int64_t lo = range_lo; lo < range_hi; lo = hi) {
+    hi = std::min(range_hi, lo + C);
+    if (hi < range_hi) {
+      KVX_ASSIGN_OR_RETURN(hi, CutBelow(lo, hi));
+    }
+    const size_t k = next_;
+    next_ = (next_ + 1) % ring_.size();
+    const uint64_t buf = ring_[k];
+    KVX_RETURN_IF_ERROR(RangeEntries(lo, hi, buf, /*pack=*/d2h, &entries, &zero, &tiled));
+    // Both directions share the ring: a slot last used by the other
+    // direction's stream is reused once that use has finished.
+    if (slot_stream_[k] != nullptr && slot_stream_[k] != cs) {
+      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, free_[k], 0));
+    }
+    if (d2h) {
+      KVX_RETURN_IF_ERROR(Launch(entries, zero, tiled, true, cs));
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host_.ptr + lo, reinterpret_cast<void*>(buf),
+                                             static_cast<size_t>(hi - lo),
+                                             hipMemcpyDeviceToHost, cs));
+    } else {
+      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(buf), host_.ptr + lo,
+                                             static_cast<size_t>(hi - lo),
+                                             hipMemcpyHostToDevice, cs));
+      KVX_RETURN_IF_ERROR(Launch(entries, zero, tiled, false, cs));
+    }
+    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(free_[k], cs));
+    slot_stream_[k] = cs;
+  }
+  return OkStatus();
+}
+
 StatusOr<CopyFuture> WeightSynchronizer::Chunked(bool d2h, hipStream_t dep) {
   std::lock_guard<std::mutex> l(mu_);
   DeviceGuard g(cfg_.device);
@@ -196,33 +313,7 @@ StatusOr<CopyFuture> WeightSynchronizer::Chunked(bool d2h, hipStream_t dep) {
   // the previous chunk's DMA, a few percent of the DMA's time.
   hipStream_t cs = d2h ? d2h_ : h2d_;
   KVX_RETURN_IF_ERROR(WaitDep(dep, cs));
-  const int64_t C = cfg_.chunk_bytes;
-  std::vector<StridedCopy> entries;
-  for (int64_t lo = 0; lo < total_; lo += C) {
-    const int64_t hi = std::min(total_, lo + C);
-    const size_t k = next_;
-    next_ = (next_ + 1) % ring_.size();
-    const uint64_t buf = ring_[k];
-    RangeEntries(lo, hi, buf, /*pack=*/d2h, &entries);
-    // Both directions share the ring: a slot last used by the other
-    // direction's stream is reused once that use has finished.
-    if (slot_stream_[k] != nullptr && slot_stream_[k] != cs) {
-      KVX_HIP_RETURN_IF_ERROR(hipStreamWaitEvent(cs, free_[k], 0));
-    }
-    if (d2h) {
-      KVX_RETURN_IF_ERROR(Launch(entries, true, cs));
-      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host_.ptr + lo, reinterpret_cast<void*>(buf),
-                                             static_cast<size_t>(hi - lo),
-                                             hipMemcpyDeviceToHost, cs));
-    } else {
-      KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(buf), host_.ptr + lo,
-                                             static_cast<size_t>(hi - lo),
-                                             hipMemcpyHostToDevice, cs));
-      KVX_RETURN_IF_ERROR(Launch(entries, false, cs));
-    }
-    KVX_HIP_RETURN_IF_ERROR(hipEventRecord(free_[k], cs));
-    slot_stream_[k] = cs;
-  }
+  KVX_RETURN_IF_ERROR(ChunkRange(d2h, 0, total_));
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, cs));
   return CopyFuture::FromEvents({done}, {host_.owner});
@@ -238,7 +329,12 @@ StatusOr<CopyFuture> WeightSynchronizer::D2hLayer(int64_t layer, hipStream_t dep
   KVX_RETURN_IF_ERROR(WaitDep(dep, d2h_));
   for (int64_t s = 0; s < cfg_.num_shards; ++s) {
     const int64_t k = layer * cfg_.num_shards + s;
-    if (cfg_.device_bytes[k] == 0) continue;
+    if (host_bytes_[k] == 0) continue;
+    if (plan(k) != nullptr) {
+      // Detiled in HBM through the staging ring, as the whole set is.
+      KVX_RETURN_IF_ERROR(ChunkRange(true, off_[k], off_[k] + host_bytes_[k]));
+      continue;
+    }
     KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(host_.ptr + off_[k],
                                            reinterpret_cast<void*>(cfg_.device_ptrs[k]),
                                            static_cast<size_t>(cfg_.device_bytes[k]),
@@ -256,7 +352,11 @@ StatusOr<CopyFuture> WeightSynchronizer::H2dLayer(int64_t layer, hipStream_t dep
   KVX_RETURN_IF_ERROR(WaitDep(dep, h2d_));
   for (int64_t s = 0; s < cfg_.num_shards; ++s) {
     const int64_t k = layer * cfg_.num_shards + s;
-    if (cfg_.device_bytes[k] == 0) continue;
+    if (host_bytes_[k] == 0) continue;
+    if (plan(k) != nullptr) {
+      KVX_RETURN_IF_ERROR(ChunkRange(false, off_[k], off_[k] + host_bytes_[k]));
+      continue;
+    }
     KVX_HIP_RETURN_IF_ERROR(hipMemcpyAsync(reinterpret_cast<void*>(cfg_.device_ptrs[k]),
                                            host_.ptr + off_[k],
                                            static_cast<size_t>(cfg_.device_bytes[k]),
@@ -276,8 +376,9 @@ StatusOr<CopyFuture> WeightSynchronizer::WholeCopy(bool pack, uint64_t staging, 
   std::lock_guard<std::mutex> l(mu_);
   DeviceGuard g(cfg_.device);
   std::vector<StridedCopy> entries;
-  RangeEntries(0, total_, staging, pack, &entries);
-  KVX_RETURN_IF_ERROR(Launch(entries, pack, stream));
+  std::vector<TiledJob> zero, tiled;
+  KVX_RETURN_IF_ERROR(RangeEntries(0, total_, staging, pack, &entries, &zero, &tiled));
+  KVX_RETURN_IF_ERROR(Launch(entries, zero, tiled, pack, stream));
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
   return CopyFuture::FromEvents({done}, {});
@@ -293,13 +394,17 @@ StatusOr<CopyFuture> WeightSynchronizer::Unpack(uint64_t staging, int64_t bytes,
   return WholeCopy(false, staging, bytes, stream);
 }
 
-StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCopy>& copies,
-                                         hipStream_t stream) {
-  static std::mutex mu;
+namespace {
+
+// One argument ring per device for the stand-alone copies; callers hold
+// RingMutex().
+std::mutex& RingMutex() {
+  static std::mutex* mu = new std::mutex();
+  return *mu;
+}
+
+StatusOr<ArgRing*> DeviceRing(int device) {
   static std::map<int, ArgRing*>* rings = new std::map<int, ArgRing*>();
-  std::lock_guard<std::mutex> l(mu);
-  DeviceGuard g(device);
-  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
   ArgRing*& ring = (*rings)[device];
   if (ring == nullptr) {
     auto* r = new ArgRing();
@@ -310,7 +415,46 @@ StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCo
     }
     ring = r;
   }
+  return ring;
+}
+
+}  // namespace
+
+StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCopy>& copies,
+                                         hipStream_t stream) {
+  std::lock_guard<std::mutex> l(RingMutex());
+  DeviceGuard g(device);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  KVX_ASSIGN_OR_RETURN(ArgRing * ring, DeviceRing(device));
   KVX_RETURN_IF_ERROR(LaunchStridedThroughRing(*ring, copies, stream));
+  KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
+  KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
+  return CopyFuture::FromEvents({done}, {});
+}
+
+StatusOr<CopyFuture> TileOnDevice(int device, const TiledPlan& plan, uint64_t linear,
+                                  uint64_t tiled, bool tile, hipStream_t stream) {
+  if (plan.logical_bytes > 0 && (linear == 0 || tiled == 0)) {
+    return InvalidArgumentError("null buffer");
+  }
+  if (!plan.tiled) {
+    // No tiles: the bytes as they are (tiling_utils.cc:959-964, 993-998).
+    if (plan.logical_bytes == 0) return CopyStridedOnDevice(device, {}, stream);
+    StridedCopy c;
+    c.src = tile ? linear : tiled;
+    c.dst = tile ? tiled : linear;
+    c.size = plan.logical_bytes;
+    return CopyStridedOnDevice(device, {c}, stream);
+  }
+  std::vector<TiledJob> zero, jobs;
+  KVX_RETURN_IF_ERROR(AppendTiledJobs(plan, tiled, linear, 0, plan.logical_bytes, tile,
+                                      /*zero_pass=*/true, &zero, &jobs));
+  std::lock_guard<std::mutex> l(RingMutex());
+  DeviceGuard g(device);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  KVX_ASSIGN_OR_RETURN(ArgRing * ring, DeviceRing(device));
+  KVX_RETURN_IF_ERROR(LaunchTiledThroughRing(*ring, zero, stream));
+  KVX_RETURN_IF_ERROR(LaunchTiledThroughRing(*ring, jobs, stream));
   KVX_ASSIGN_OR_RETURN(hipEvent_t done, NewEvent());
   KVX_HIP_RETURN_IF_ERROR(hipEventRecord(done, stream));
   return CopyFuture::FromEvents({done}, {});

@@ -17,7 +17,14 @@
 // by the offset table (device-side contiguous staging), and CopyStrided runs
 // arbitrary strided push entries (column-split resharding) on the device;
 // StridedCopyPlan keeps such entries' device table for repeated runs.
-// TPU tiled layouts do not exist here, so there is no tile/detile step.
+//
+// A tensor may be stored in a tiled layout (TiledPlan). Its host copy is
+// then the row-major (linear) image, as the reference's D2hLayer / H2dLayer
+// produce by detiling / tiling on the host around a raw DMA of the tiled
+// bytes (weight_synchronizer_base.cc:357-389, 473-510). Here the tiled-copy
+// kernel does it in HBM: D2h detiles into the staging chunk the DMA reads,
+// H2d tiles out of the chunk the DMA wrote (padding cleared first). Chunk
+// boundaries inside a tiled tensor fall on its row groups.
 #ifndef KVX_HOST_WEIGHT_SYNCHRONIZER_H_
 #define KVX_HOST_WEIGHT_SYNCHRONIZER_H_
 
@@ -33,6 +40,7 @@
 #include "copy_future.h"
 #include "host_allocator.h"
 #include "status.h"
+#include "tiled_layout.h"
 
 namespace kvx {
 
@@ -42,6 +50,10 @@ struct WeightSyncConfig {
   int64_t num_shards = 1;
   std::vector<uint64_t> device_ptrs;  // [layer * num_shards + shard]
   std::vector<int64_t> device_bytes;
+  // Per tensor (empty: none): a tiled layout, or null for row-major bytes.
+  // A tiled tensor's device buffer holds at least plan->tiled_bytes and its
+  // host copy plan->logical_bytes.
+  std::vector<std::shared_ptr<const TiledPlan>> tiled;
   HostAllocKind host_alloc = HostAllocKind::kPinned;
   int64_t chunk_bytes = 256ll << 20;  // device staging chunk
   int staging_chunks = 2;
@@ -70,7 +82,8 @@ class WeightSynchronizer {
   int64_t num_shards() const { return cfg_.num_shards; }
   int64_t total_bytes() const { return total_; }
   int64_t offset(int64_t layer, int64_t shard) const { return off_[layer * cfg_.num_shards + shard]; }
-  int64_t size(int64_t layer, int64_t shard) const { return cfg_.device_bytes[layer * cfg_.num_shards + shard]; }
+  // Bytes of one tensor's host copy (the linear image of a tiled tensor).
+  int64_t size(int64_t layer, int64_t shard) const { return host_bytes_[layer * cfg_.num_shards + shard]; }
   uint8_t* host_base() const { return host_.ptr; }
   Status Synchronize();
   // Profiled pack (pack = true) or unpack kernel launches: count, summed
@@ -81,13 +94,28 @@ class WeightSynchronizer {
   explicit WeightSynchronizer(WeightSyncConfig cfg) : cfg_(std::move(cfg)) {}
   Status Init();
   StatusOr<CopyFuture> Chunked(bool d2h, hipStream_t dep);
+  // Chunks [range_lo, range_hi) of the packed image through the ring on the
+  // direction's stream (lock held, dependency already ordered).
+  Status ChunkRange(bool d2h, int64_t range_lo, int64_t range_hi);
+  // Largest cut point in (lo, x] of the packed image, or an error when a
+  // tiled tensor's row group does not fit between lo and x.
+  StatusOr<int64_t> CutBelow(int64_t lo, int64_t x) const;
   StatusOr<CopyFuture> WholeCopy(bool pack, uint64_t staging, int64_t bytes,
                                  hipStream_t stream);
   // Entries for packed range [lo, hi) with the image placed at `image`
   // (pack: tensors -> image; unpack: image -> tensors).
-  void RangeEntries(int64_t lo, int64_t hi, uint64_t image, bool pack,
-                    std::vector<StridedCopy>* out) const;
-  Status Launch(const std::vector<StridedCopy>& copies, bool pack, hipStream_t stream);
+  // Tiled tensors become tiled-copy jobs (*zero: padding cleared before
+  // *tiled runs); the rest strided entries.
+  Status RangeEntries(int64_t lo, int64_t hi, uint64_t image, bool pack,
+                      std::vector<StridedCopy>* out, std::vector<TiledJob>* zero,
+                      std::vector<TiledJob>* tiled) const;
+  Status Launch(const std::vector<StridedCopy>& copies, const std::vector<TiledJob>& zero,
+                const std::vector<TiledJob>& tiled, bool pack, hipStream_t stream);
+  // Tiled layout of tensor k, or null for row-major bytes.
+  const TiledPlan* plan(int64_t k) const {
+    if (cfg_.tiled.empty() || cfg_.tiled[k] == nullptr || !cfg_.tiled[k]->tiled) return nullptr;
+    return cfg_.tiled[k].get();
+  }
   Status WaitDep(hipStream_t dep, hipStream_t on);
 
   struct Sample {
@@ -99,6 +127,7 @@ class WeightSynchronizer {
 
   WeightSyncConfig cfg_;
   std::vector<int64_t> off_;
+  std::vector<int64_t> host_bytes_;
   int64_t total_ = 0;
   int numa_node_ = -1;
   HostBufferAllocation host_;
@@ -118,6 +147,12 @@ class WeightSynchronizer {
 // `stream` (no synchronizer needed); returns a future for the launch.
 StatusOr<CopyFuture> CopyStridedOnDevice(int device, const std::vector<StridedCopy>& copies,
                                          hipStream_t stream);
+
+// TileBuffer (tile = true: linear -> tiled, padding zero) or DetileBuffer
+// (tiling_utils.h:30-36) of one tensor between device buffers, on `stream`.
+// `tiled` holds plan.tiled_bytes, `linear` plan.logical_bytes.
+StatusOr<CopyFuture> TileOnDevice(int device, const TiledPlan& plan, uint64_t linear,
+                                  uint64_t tiled, bool tile, hipStream_t stream);
 
 // Strided entries whose device image (entry table + tile map) is built and
 // uploaded once, for callers that run the same entries again and again: a

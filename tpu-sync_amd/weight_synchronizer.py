@@ -17,6 +17,12 @@ and ``column_split_entries`` builds the entries of a column split whose
 bounds follow ``compute_nd_shard_slices`` (tpu_sync/kv_cache/
 nd_slice_math.py:23-70: equal tiles, remainder to the last shard).
 Networked pushes and their listener are not part of this package.
+
+A weight may be stored tiled on the device (``layouts``, one
+``tiling.TiledLayout`` or None per tensor): its host copy is then the
+row-major image, as the reference's D2hLayer / H2dLayer produce by detiling /
+tiling on the host (weight_synchronizer_base.cc:357-389, 473-510); here the
+detile / tile runs in HBM on the staging chunks.
 """
 import ctypes
 import itertools
@@ -160,7 +166,8 @@ class WeightSynchronizer:
                  bind_ip: Optional[str] = None, unsafe_skip_buffer_lock: bool = True,
                  auto_h2d: bool = False, *, host_alloc: str = "pinned",
                  chunk_bytes: int = 0, staging_chunks: int = 0,
-                 profile_kernels: bool = False, numa_local: bool = True):
+                 profile_kernels: bool = False, numa_local: bool = True,
+                 layouts: Optional[List[List[Any]]] = None):
         del local_port, parallelism, listener_port, bind_ip, unsafe_skip_buffer_lock, auto_h2d
         layers = [list(x) if isinstance(x, (list, tuple)) else [x] for x in device_tensors]
         num_shards = len(layers[0]) if layers else 1
@@ -192,6 +199,18 @@ class WeightSynchronizer:
         cfg.staging_chunks = staging_chunks
         cfg.profile_kernels = int(bool(profile_kernels))
         cfg.numa_off = 0 if numa_local else 1
+        self._layouts = None
+        if layouts is not None:
+            flat = [list(x) if isinstance(x, (list, tuple)) else [x] for x in layouts]
+            if len(flat) != len(layers) or any(len(s) != num_shards for s in flat):
+                raise RuntimeError("layouts must match device_tensors layer by layer")
+            self._layouts = flat
+            n = len(layers) * num_shards
+            self._layout_arr = (_capi.TiledLayoutC * max(n, 1))()
+            for k, lay in enumerate(x for shards in flat for x in shards):
+                if lay is not None:
+                    self._layout_arr[k] = lay.to_c()
+            cfg.layouts = self._layout_arr
         h = ctypes.c_void_p()
         _capi.check(_capi.load().kvx_weight_sync_create(ctypes.byref(cfg), ctypes.byref(h)),
                     "WeightSynchronizer create")
@@ -253,6 +272,13 @@ class WeightSynchronizer:
         ptr, nbytes, _ = self.host_buffer_info(layer_idx, shard_idx)
         t = self._tensors[layer_idx][shard_idx]
         buf = (ctypes.c_uint8 * nbytes).from_address(ptr)
+        lay = self._layouts[layer_idx][shard_idx] if self._layouts else None
+        if lay is not None and lay.tiles:
+            # The host copy of a tiled weight is its row-major image.
+            dtype = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[lay.itemsize]
+            if t.element_size() == lay.itemsize:
+                dtype = t.dtype
+            return torch.frombuffer(buf, dtype=torch.uint8).view(dtype).view(lay.dims)
         return torch.frombuffer(buf, dtype=torch.uint8).view(t.dtype).view(t.shape)
 
     def host_image(self):
