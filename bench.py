@@ -67,9 +67,9 @@ def parse_args():
                    help="skip the per-mode, one-direction and PCIe-peak measurements")
     p.add_argument("--mode", default="auto", choices=["auto", "staged", "zero_copy"],
                    help="transfer mode of the headline offload/reload loop")
-    p.add_argument("--configs", default="fp8,weights,pools,lanes,zipf",
+    p.add_argument("--configs", default="fp8,weights,tiled,pools,lanes,zipf",
                    help="comma list of extra workloads to measure after the headline "
-                        "(fp8, weights, pools, lanes, zipf; empty for none)")
+                        "(fp8, weights, tiled, pools, lanes, zipf; empty for none)")
     p.add_argument("--zipf-host-blocks", type=int, default=0,
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks (0: "
                         "the configured 256 GB budget, capped by free /dev/shm, available "
@@ -490,6 +490,77 @@ def bench_weight_sync(torch, pkg, dev, args):
     return out
 
 
+def bench_weight_sync_tiled(torch, pkg, dev, args):
+    """The Llama-3-8B parameter set stored tiled on the device, every tensor
+    in the bf16 {T(8,128)(2,1)} layout (1-D norms as (1, 4096), padded to whole
+    tiles): device detile + pack into one contiguous staging buffer, tile +
+    unpack back (padding cleared), and the pipelined D2H / H2D whose host
+    copies are the row-major images. Algorithmic bytes of a pack or unpack:
+    2 x the logical bytes (16.06 GB read + written)."""
+    shapes = llama3_8b_param_shapes()
+    layouts = [pkg.tiling.TiledLayout(2, sh, [(8, 128), (2, 1)]) for sh in shapes]
+    log("weights_tiled: allocating 291 tiled bf16 tensors")
+    params = [torch.empty(L.tiled_bytes // 2, dtype=torch.int16, device=dev).random_()
+              for L in layouts]
+    total = sum(L.logical_bytes for L in layouts)
+    ws = pkg.WeightSynchronizer([[t] for t in params], layouts=[[L] for L in layouts],
+                                profile_kernels=True)
+    staging = torch.empty(ws.total_bytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream(dev)
+    reps = max(3, args.sub_steps // 4)
+    ws.pack(staging, stream=s).Await()
+    ws.kernel_times(True, reset=True)
+    for f in [ws.pack(staging, stream=s) for _ in range(reps)]:
+        f.Await()
+    kt = ws.kernel_times(True, reset=True)
+    detile_ms = kt["total_ms"] / reps if kt["launches"] else None
+    for f in [ws.unpack(staging, stream=s) for _ in range(reps)]:
+        f.Await()
+    kt = ws.kernel_times(False, reset=True)
+    tile_ms = kt["total_ms"] / reps if kt["launches"] else None
+    ws.d2h().Await()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ws.d2h().Await()
+    d2h_gbps = reps * total / (time.perf_counter() - t0) / 1e9
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ws.h2d().Await()
+    h2d_gbps = reps * total / (time.perf_counter() - t0) / 1e9
+    ws.kernel_times(True, reset=True)
+    ws.kernel_times(False, reset=True)
+    # Host detile of one MLP weight with numpy (pad-free reshape / swap of
+    # axes, one thread), for scale: the reference detiles on the host.
+    import numpy as np
+    w = np.random.default_rng(0).integers(0, 1 << 16, 14336 * 4096, dtype=np.uint16)
+    tiled = np.ascontiguousarray(np.swapaxes(
+        np.moveaxis(w.reshape(1792, 8, 32, 128), 1, 2).reshape(1792, 32, 4, 2, 128), -1, -2))
+    t0 = time.perf_counter()
+    lin = np.ascontiguousarray(np.moveaxis(np.swapaxes(tiled, -1, -2).reshape(1792, 32, 8, 128),
+                                           1, 2)).reshape(-1)
+    host_s = time.perf_counter() - t0
+    assert np.array_equal(lin, w)
+    out = {"workload": "Llama-3-8B parameter set, 291 bf16 tensors in the T(8,128)(2,1) tiled "
+                       "layout, 16.06 GB logical",
+           "bytes": total, "tiled_bytes": sum(L.tiled_bytes for L in layouts),
+           "detile_pack_ms": round(detile_ms, 3) if detile_ms else None,
+           "detile_pack_gbps": round(2 * total / detile_ms / 1e6, 1) if detile_ms else None,
+           "detile_pack_frac_of_hbm_peak": round(2 * total / detile_ms / 1e6 / HBM_PEAK_GBPS, 4)
+           if detile_ms else None,
+           "tile_unpack_ms": round(tile_ms, 3) if tile_ms else None,
+           "tile_unpack_gbps": round(2 * total / tile_ms / 1e6, 1) if tile_ms else None,
+           "tile_unpack_frac_of_hbm_peak": round(2 * total / tile_ms / 1e6 / HBM_PEAK_GBPS, 4)
+           if tile_ms else None,
+           "d2h_gbps": round(d2h_gbps, 2), "h2d_gbps": round(h2d_gbps, 2),
+           "host_numpy_detile_gbps_one_thread": round(2 * w.nbytes / host_s / 1e9, 2),
+           "host_detile_sample": "one [14336, 4096] bf16 weight, numpy axis swaps, 1 thread"}
+    log(f"weights_tiled: {out}")
+    ws.close()
+    del params, staging
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_pools(torch, pkg, dev, args, rng):
     """Pool-addressed copies of a sparse (FA-like) pool: per block 4 head
     groups of 64 tokens x (K 256 B + V 256 B) packed at 70 KiB pitch inside a
@@ -843,6 +914,8 @@ def run_configs(torch, pkg, dev, args, rng, peaks):
         configs["fp8_kv_scales"] = bench_fp8_scales(torch, pkg, dev, args, rng)
     if "weights" in wanted:
         configs["weight_sync_pack"] = bench_weight_sync(torch, pkg, dev, args)
+    if "tiled" in wanted:
+        configs["weight_sync_tiled"] = bench_weight_sync_tiled(torch, pkg, dev, args)
     if "pools" in wanted:
         configs["sparse_pool_copies"] = bench_pools(torch, pkg, dev, args, rng)
     if "lanes" in wanted:

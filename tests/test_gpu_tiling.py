@@ -265,5 +265,5 @@ def test_weight_sync_rejects_small_tiled_buffers_and_chunks(kvx, cuda):
     with pytest.raises(kvx.KvxError, match="smaller than its tiled layout"):
         kvx.WeightSynchronizer([[small]], layouts=[[L]])
     ok = torch.zeros(L.tiled_bytes, dtype=torch.uint8, device=cuda)
-    with pytest.raises(kvx.KvxError, match="row group"):
+    with pytest.raises(kvx.KvxError, match="tile row"):
         kvx.WeightSynchronizer([[ok]], layouts=[[L]], chunk_bytes=2000)

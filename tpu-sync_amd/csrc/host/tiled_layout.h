@@ -65,8 +65,9 @@ struct TiledPlan {
   // General form: the final tiled shape's dimensions.
   std::vector<TiledGenDim> gen;
   // Largest byte offset <= x (from the start of the linear image) at which
-  // the linear image may be cut between two launches: whole row groups of a
-  // batch matrix in the standard form, whole elements in the general form.
+  // the linear image may be cut between two launches: whole tile rows (tH
+  // rows, or the end of a batch matrix) in the standard form, whole elements
+  // in the general form.
   int64_t CutAtOrBelow(int64_t x) const;
 };
 

@@ -87,13 +87,14 @@ Status WeightSynchronizer::Init() {
   KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueues({&ks_, &d2h_, &h2d_}));
   const int64_t chunk = std::min<int64_t>(cfg_.chunk_bytes, std::max<int64_t>(total_, 1));
   cfg_.chunk_bytes = chunk;
-  // A chunk must hold one row group of every tiled tensor.
+  // A chunk must hold one tile row of every tiled tensor.
   for (int64_t k = 0; k < n; ++k) {
     const TiledPlan* tp = plan(k);
     if (tp == nullptr || !tp->standard) continue;
-    const int64_t group = static_cast<int64_t>(tp->P * tp->W) * tp->layout.itemsize;
+    const int64_t group =
+        static_cast<int64_t>(std::min(tp->tH, tp->H) * tp->W) * tp->layout.itemsize;
     if (group > chunk) {
-      return InvalidArgumentError("tensor " + std::to_string(k) + ": a row group (" +
+      return InvalidArgumentError("tensor " + std::to_string(k) + ": a tile row (" +
                                   std::to_string(group) +
                                   " bytes) does not fit a staging chunk");
     }
@@ -258,7 +259,7 @@ StatusOr<int64_t> WeightSynchronizer::CutBelow(int64_t lo, int64_t x) const {
     if (cut <= lo) cut = x;
   }
   if (cut <= lo) {
-    return InternalError("staging chunk holds no whole row group of tensor " + std::to_string(k));
+    return InternalError("staging chunk holds no whole tile row of tensor " + std::to_string(k));
   }
   return cut;
 }

@@ -24,7 +24,7 @@
 // bytes (weight_synchronizer_base.cc:357-389, 473-510). Here the tiled-copy
 // kernel does it in HBM: D2h detiles into the staging chunk the DMA reads,
 // H2d tiles out of the chunk the DMA wrote (padding cleared first). Chunk
-// boundaries inside a tiled tensor fall on its row groups.
+// boundaries inside a tiled tensor fall on its tile rows.
 #ifndef KVX_HOST_WEIGHT_SYNCHRONIZER_H_
 #define KVX_HOST_WEIGHT_SYNCHRONIZER_H_
 
@@ -98,7 +98,7 @@ class WeightSynchronizer {
   // direction's stream (lock held, dependency already ordered).
   Status ChunkRange(bool d2h, int64_t range_lo, int64_t range_hi);
   // Largest cut point in (lo, x] of the packed image, or an error when a
-  // tiled tensor's row group does not fit between lo and x.
+  // tiled tensor's tile row does not fit between lo and x.
   StatusOr<int64_t> CutBelow(int64_t lo, int64_t x) const;
   StatusOr<CopyFuture> WholeCopy(bool pack, uint64_t staging, int64_t bytes,
                                  hipStream_t stream);

@@ -14,7 +14,12 @@
 //     one 2-D tile (tH, tW), optionally followed by a (P, 1) tile that packs
 //     P consecutive rows element by element, P in {2, 4} with P * itemsize =
 //     4). A unit is P rows x V bytes: V contiguous bytes of each of P linear
-//     rows and P * V contiguous bytes of the tiled buffer.
+//     rows and P * V contiguous bytes of the tiled buffer, moved by one lane
+//     or, for P = 2 at V = 16, by two lanes that exchange halves. Units are
+//     enumerated in linear order (row groups of the linear image, then column
+//     vectors) or in tiled order (unit u is bytes [u P V, (u + 1) P V) of the
+//     tiled buffer, padding included: rows past H and columns past W read as
+//     zero when tiling and are skipped when detiling).
 //   * kDetileGen / kTileGen: any other layout, element by element through the
 //     index map of the nested tiling.
 //   * kZero: clears a tiled buffer (V-byte vectors), launched before a tile
@@ -99,10 +104,21 @@ struct TiledJobDev {
   FastDivU32 ng;   // row groups per batch matrix = ceil(H / P)
   FastDivU32 th;   // tile rows
   FastDivU32 tw;   // tile columns
-  uint64_t H;
-  uint64_t W;
-  uint64_t nT0;  // tile rows per matrix = ceil(H / tH)
-  uint64_t nT1;  // tile columns per matrix = ceil(W / tW)
+  // Tiled order: u = ((T * GT + gi) * NCVT + cvt), T = (b * nT0 + tr) * nT1 + tc.
+  FastDivU32 t_ncv;  // column vectors per tile row group (NCVT = tW * itemsize / V)
+  FastDivU32 t_gpt;  // row groups per tile (GT = tH / P)
+  FastDivU32 t_nt1;  // tile columns per matrix (nT1)
+  FastDivU32 t_nt0;  // tile rows per matrix (nT0)
+  uint32_t torder;   // 0: linear order, 1: tiled order
+  uint32_t lanes_per_unit;  // packed units: 1, or 2 (P = 2 at 16-byte rows)
+  uint32_t pad0[2];
+  uint32_t h32;         // H (rows per batch matrix)
+  uint32_t w32;         // W (columns)
+  uint32_t nt0;         // tile rows per matrix = ceil(H / tH)
+  uint32_t nt1;         // tile columns per matrix = ceil(W / tW)
+  uint32_t tile_elems;  // tH * tW
+  uint32_t log2s;       // log2(itemsize)
+  uint32_t pad1[2];
   // General form.
   uint32_t rank;        // logical dimensions
   uint32_t ngen;        // dimensions of the final tiled shape
@@ -112,15 +128,31 @@ struct TiledJobDev {
 };
 static_assert(sizeof(TiledJobDev) % 16 == 0, "device layout");
 
-// Units (std), elements (gen) or vectors (zero) one workgroup moves.
-uint32_t TiledJobPerWorkgroup(const TiledJobDev& j);
+// What selects a kernel: every job of one launch shares it.
+struct TiledLaunchKey {
+  uint32_t mode;
+  uint32_t vec;       // standard and zero jobs: vector width
+  uint32_t P;         // standard jobs
+  uint32_t torder;    // standard jobs
+  uint32_t lanes;     // standard packed jobs: lanes per unit
+  uint32_t itemsize;  // general jobs
+  bool operator==(const TiledLaunchKey& o) const {
+    return mode == o.mode && vec == o.vec && P == o.P && torder == o.torder &&
+           lanes == o.lanes && itemsize == o.itemsize;
+  }
+};
 
-// Launches the jobs of a device-resident image: `n` TiledJobDev, then the
+// The key of a job whose launch uses vector width vec_bytes.
+TiledLaunchKey LaunchKeyOf(const TiledJobDev& j, int vec_bytes);
+
+// Units (std), elements (gen) or vectors (zero) one workgroup moves.
+uint32_t TiledPerWorkgroup(const TiledLaunchKey& k);
+
+// Launches the jobs of a device-resident image: the TiledJobDev array, the
 // general-path dimension arrays, then a workgroup -> job map of `grid`
-// uint32 at byte offset `map_offset`. Every standard and zero job of one
-// launch uses vector width `vec_bytes` (16, 8, 4, 2 or 1; P > 1 needs >= 4).
-hipError_t LaunchTiledCopy(const void* image_dev, uint32_t n, uint32_t map_offset,
-                           uint32_t grid, int vec_bytes, hipStream_t stream);
+// uint32 at byte offset `map_offset`. Every job of the image has `key`.
+hipError_t LaunchTiledCopy(const void* image_dev, uint32_t map_offset, uint32_t grid,
+                           const TiledLaunchKey& key, hipStream_t stream);
 
 }  // namespace kvx
 
