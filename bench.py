@@ -551,6 +551,10 @@ def bench_weight_sync_tiled(torch, pkg, dev, args):
            "tile_unpack_gbps": round(2 * total / tile_ms / 1e6, 1) if tile_ms else None,
            "tile_unpack_frac_of_hbm_peak": round(2 * total / tile_ms / 1e6 / HBM_PEAK_GBPS, 4)
            if tile_ms else None,
+           # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE with the
+           # same calibration (profiles/tiled_copy_weight_sync_llama3_8b_trace.txt).
+           "detile_pack_traffic": int((7844359.0 / 0.50002 + 15684479.2) * 1024),
+           "tile_unpack_traffic": int((7844086.1 / 0.50002 + 15693224.0) * 1024),
            "d2h_gbps": round(d2h_gbps, 2), "h2d_gbps": round(h2d_gbps, 2),
            "host_numpy_detile_gbps_one_thread": round(2 * w.nbytes / host_s / 1e9, 2),
            "host_detile_sample": "one [14336, 4096] bf16 weight, numpy axis swaps, 1 thread"}
