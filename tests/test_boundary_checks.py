@@ -158,3 +158,32 @@ def test_strided_plan_validates_entries_before_the_device(kvx):
     assert rc == 0 and p.value
     lib.kvx_strided_plan_destroy(p)
     assert lib.kvx_strided_plan_create(0, None, 0, None) == 3
+
+
+def test_tile_entry_points_reject_bad_tensors(kvx):
+    """tile_buffer / detile_buffer check both tensors (device, contiguity)
+    and their sizes against the layout before any library call."""
+    L = kvx.tiling.TiledLayout(2, (16, 256), [(8, 128), (2, 1)])
+    lin = FakeDeviceTensor(torch.empty(16 * 256, dtype=torch.int16))
+    til = FakeDeviceTensor(torch.empty(L.tiled_bytes // 2, dtype=torch.int16))
+    for fn in (kvx.tiling.tile_buffer, kvx.tiling.detile_buffer):
+        with pytest.raises(ValueError, match="HIP device"):
+            fn(L, torch.empty(16 * 256, dtype=torch.int16), til) if fn is kvx.tiling.tile_buffer \
+                else fn(L, til, torch.empty(16 * 256, dtype=torch.int16))
+        short = FakeDeviceTensor(torch.empty(16 * 256 - 1, dtype=torch.int16))
+        with pytest.raises(ValueError, match="linear buffer holds"):
+            fn(L, short, til) if fn is kvx.tiling.tile_buffer else fn(L, til, short)
+        with pytest.raises(ValueError, match="tiled buffer holds"):
+            fn(L, lin, short) if fn is kvx.tiling.tile_buffer else fn(L, short, lin)
+        with pytest.raises(ValueError, match="contiguous"):
+            bad = FakeDeviceTensor(torch.empty(256, 32, dtype=torch.int16).t())
+            fn(L, bad, til) if fn is kvx.tiling.tile_buffer else fn(L, til, bad)
+
+
+def test_weight_sync_layouts_must_match_the_tensors(kvx):
+    L = kvx.tiling.TiledLayout(2, (16, 256), [(8, 128), (2, 1)])
+    t = FakeDeviceTensor(torch.empty(L.tiled_bytes, dtype=torch.uint8))
+    with pytest.raises(RuntimeError, match="layouts must match"):
+        kvx.WeightSynchronizer([[t], [t]], layouts=[[L]])
+    with pytest.raises(RuntimeError, match="layouts must match"):
+        kvx.WeightSynchronizer([[t, t]], layouts=[[L]])
