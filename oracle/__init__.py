@@ -27,6 +27,9 @@ Parity status of each function (what pins it):
       an independent numpy formulation of 2-D tiling (pad, reshape, swap
       axes) and of the (P, 1) row packing, round trips, and brute-force
       bijection / padding checks (tests/test_tiling_oracle.py).
+  detile_std (the reference's threaded standard-form host detile, the timed
+  CPU baseline of tiled weight sync): against detile on every reference case
+  of the standard form and random standard layouts, 1-8 threads.
 """
 import ctypes
 import os
@@ -79,6 +82,10 @@ def lib():
         for fn in (l.oracle_tile, l.oracle_detile):
             fn.argtypes = [ctypes.c_int, ctypes.c_int, _i64p, _i32p, ctypes.c_int, _i32p,
                            _i64p, ctypes.c_void_p, ctypes.c_void_p]
+        l.oracle_detile_std.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_int]
         for fn in (l.oracle_extract, l.oracle_insert):
             fn.argtypes = [_u8pp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                            _i64p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
@@ -263,3 +270,15 @@ def detile(layout, tiled):
     if rc != 0:
         raise ValueError("oracle_detile failed: %d" % rc)
     return out
+
+
+def detile_std(itemsize, B, H, W, tH, tW, P, tiled, linear=None, nthreads=1):
+    """Standard-form detile with threads (bytes in, bytes out)."""
+    tiled = np.ascontiguousarray(np.asarray(tiled).view(np.uint8).reshape(-1))
+    if linear is None:
+        linear = np.zeros(B * H * W * itemsize, np.uint8)
+    rc = lib().oracle_detile_std(itemsize, B, H, W, tH, tW, P, tiled.ctypes.data,
+                                 linear.ctypes.data, nthreads)
+    if rc != 0:
+        raise ValueError("oracle_detile_std failed: %d" % rc)
+    return linear

@@ -27,6 +27,9 @@
  *                          tpu_sync/weight_sync/tiling_utils.cc:905-1036
  *                          (GetTiledBufferElements, TileBuffer, DetileBuffer:
  *                          XLA's nested tiling, element by element)
+ *   oracle_detile_std      tpu_sync/weight_sync/tiling_utils.cc:727-900
+ *                          (DetileBufferNDOptimized: the standard form, tile
+ *                          rows split over threads; the timed CPU baseline)
  * The reference C++ cannot be compiled here (Bazel, abseil, XLA/PJRT and
  * generated protos are absent), so there is no oracle/_ref build.
  */
@@ -440,4 +443,99 @@ int oracle_detile(int itemsize, int rank, const int64_t* dims, const int32_t* mt
                   const int32_t* tile_rank, const int64_t* tile_dims, const uint8_t* tiled,
                   uint8_t* linear) {
   return tiled_copy(0, itemsize, rank, dims, mtm, ntiles, tile_rank, tile_dims, tiled, linear);
+}
+
+/* ---------------------------------------------------------------------------
+ * Standard-form detile with threads, following the reference's host routine
+ * (DetileBufferNDOptimized, tiling_utils.cc:727-900): tasks are (batch
+ * matrix, tile row) pairs split into contiguous ranges over the threads
+ * (tiling_utils.cc:854-876); each tile row segment of a tile is copied with
+ * memcpy (P = 1) or its P interleaved rows are split element by element
+ * (P = 2 for 16-bit, P = 4 for 8-bit elements). Rows and columns past the
+ * matrix are skipped.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int itemsize, P;
+  int64_t B, H, W, tH, tW, nT0, nT1;
+  const uint8_t* tiled;
+  uint8_t* linear;
+  int64_t task_lo, task_hi;
+} detile_job;
+
+static void* detile_worker(void* arg) {
+  const detile_job* j = (const detile_job*)arg;
+  const int64_t s = j->itemsize, tile_bytes = j->tH * j->tW * s;
+  for (int64_t t = j->task_lo; t < j->task_hi; ++t) {
+    const int64_t b = t / j->nT0, tr = t % j->nT0;
+    const uint8_t* src_b = j->tiled + b * j->nT0 * j->nT1 * tile_bytes;
+    uint8_t* dst_b = j->linear + b * j->H * j->W * s;
+    for (int64_t tc = 0; tc < j->nT1; ++tc) {
+      const uint8_t* tile = src_b + (tr * j->nT1 + tc) * tile_bytes;
+      const int64_t c0 = tc * j->tW;
+      const int64_t cols = j->W - c0 < j->tW ? j->W - c0 : j->tW;
+      if (j->P == 1) {
+        for (int64_t r = 0; r < j->tH; ++r) {
+          const int64_t row = tr * j->tH + r;
+          if (row >= j->H) break;
+          memcpy(dst_b + (row * j->W + c0) * s, tile + r * j->tW * s, (size_t)(cols * s));
+        }
+        continue;
+      }
+      /* Row group g holds rows g P .. g P + P - 1 interleaved element by
+       * element; the typed loops below vectorise (the reference splits
+       * them with SIMD de-interleaving loads, tiling_utils.cc:300-420). */
+      for (int64_t g = 0; g < j->tH / j->P; ++g) {
+        const int64_t row = tr * j->tH + g * j->P;
+        if (row >= j->H) break;
+        const uint8_t* grp = tile + g * j->tW * j->P * s;
+        if (j->P == 2 && s == 2) {
+          const uint16_t* in = (const uint16_t*)grp;
+          uint16_t* d0 = (uint16_t*)(dst_b + (row * j->W + c0) * 2);
+          uint16_t* d1 = d0 + j->W;
+          const int two = row + 1 < j->H;
+          for (int64_t c = 0; c < cols; ++c) d0[c] = in[2 * c];
+          if (two) {
+            for (int64_t c = 0; c < cols; ++c) d1[c] = in[2 * c + 1];
+          }
+        } else if (j->P == 4 && s == 1) {
+          for (int k = 0; k < 4 && row + k < j->H; ++k) {
+            uint8_t* d = dst_b + (row + k) * j->W + c0;
+            for (int64_t c = 0; c < cols; ++c) d[c] = grp[4 * c + k];
+          }
+        } else {
+          for (int k = 0; k < j->P && row + k < j->H; ++k) {
+            uint8_t* d = dst_b + ((row + k) * j->W + c0) * s;
+            for (int64_t c = 0; c < cols; ++c) memcpy(d + c * s, grp + (c * j->P + k) * s, (size_t)s);
+          }
+        }
+      }
+    }
+  }
+  return NULL;
+}
+
+int oracle_detile_std(int itemsize, int64_t B, int64_t H, int64_t W, int64_t tH, int64_t tW,
+                      int P, const uint8_t* tiled, uint8_t* linear, int nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > 64) nthreads = 64;
+  detile_job jobs[64];
+  pthread_t th[64];
+  const int64_t nT0 = (H + tH - 1) / tH, nT1 = (W + tW - 1) / tW, tasks = B * nT0;
+  const int64_t chunk = (tasks + nthreads - 1) / nthreads;
+  int started = 0;
+  for (int i = 0; i < nthreads; ++i) {
+    detile_job* j = &jobs[i];
+    j->itemsize = itemsize;
+    j->P = P;
+    j->B = B; j->H = H; j->W = W; j->tH = tH; j->tW = tW; j->nT0 = nT0; j->nT1 = nT1;
+    j->tiled = tiled;
+    j->linear = linear;
+    j->task_lo = i * chunk;
+    j->task_hi = (i + 1) * chunk < tasks ? (i + 1) * chunk : tasks;
+    if (j->task_lo >= j->task_hi) break;
+    if (pthread_create(&th[i], NULL, detile_worker, j) != 0) return INVALID_ARGUMENT;
+    ++started;
+  }
+  for (int i = 0; i < started; ++i) pthread_join(th[i], NULL);
+  return OK;
 }

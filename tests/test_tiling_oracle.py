@@ -191,3 +191,53 @@ def test_fast_division_matches_integer_division(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120, env=env)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "fast div ok" in r.stdout
+
+
+def _standard(lay):
+    dims, tiles, mtm = lay["dims"], lay["tiles"], lay["minor_to_major"]
+    r = len(dims)
+    if any(mtm[i] != r - 1 - i for i in range(r)) or not tiles or len(tiles[0]) != 2:
+        return None
+    P = 1
+    if len(tiles) == 2:
+        if len(tiles[1]) != 2 or tiles[1][1] != 1 or tiles[1][0] not in (2, 4):
+            return None
+        P = tiles[1][0]
+        if P * lay["itemsize"] != 4 or tiles[0][0] % P:
+            return None
+    elif len(tiles) > 2:
+        return None
+    W = dims[-1]
+    H = 1 if r == 1 else dims[-2]
+    B = int(np.prod(dims)) // (W * H)
+    return B, H, W, tiles[0][0], tiles[0][1], P
+
+
+def test_threaded_standard_detile_matches_oracle(oracle):
+    """The timed CPU baseline (the reference's standard-form host detile,
+    tile rows over threads) against the element-by-element oracle."""
+    rng = np.random.default_rng(13)
+    lays = [_layout(c) for c in _cases()]
+    for _ in range(60):
+        s = int(rng.choice([1, 2, 4, 8]))
+        packed = s in (1, 2) and rng.random() < 0.5
+        P = 4 // s if packed else 1
+        tH = int(rng.choice([1, 2, 4, 8])) * P
+        tW = int(rng.choice([1, 3, 16, 128]))
+        dims = [int(rng.integers(1, 4)) for _ in range(int(rng.integers(0, 3)))]
+        dims += [int(rng.integers(1, 30)), int(rng.integers(1, 300))]
+        tiles = [[tH, tW]] + ([[P, 1]] if packed else [])
+        lays.append({"itemsize": s, "dims": dims,
+                     "minor_to_major": list(range(len(dims) - 1, -1, -1)), "tiles": tiles})
+    checked = 0
+    for lay in lays:
+        std = _standard(lay)
+        if std is None:
+            continue
+        y = rng.integers(0, 256, oracle.tiled_elements(lay) * lay["itemsize"], dtype=np.uint8)
+        want = oracle.detile(lay, y)
+        for nthreads in (1, 3, 8):
+            got = oracle.detile_std(lay["itemsize"], *std, y, nthreads=nthreads)
+            assert np.array_equal(got, want), (lay, nthreads)
+        checked += 1
+    assert checked >= 60
