@@ -83,9 +83,11 @@ struct TiledJob {
 // Jobs moving bytes [lo, hi) of the tensor's linear image (cut points from
 // CutAtOrBelow, or 0 / logical_bytes) between its tiled buffer `tiled` and
 // a linear image whose byte 0 is at `linear` (only [lo, hi) of it is
-// touched). tile = true: linear -> tiled; with zero_pass the whole tiled
-// buffer is first cleared when the layout has padding (the caller passes it
-// for the range that starts the tensor, and launches *zero before *jobs).
+// touched). tile = true: linear -> tiled. Standard-form tiling writes the
+// padding of the tile rows it covers; otherwise, with zero_pass, the whole
+// tiled buffer is first cleared when the layout has padding (the caller
+// passes zero_pass for the range that starts the tensor, and launches *zero
+// before *jobs).
 // Untiled layouts yield no jobs (callers copy their bytes).
 Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int64_t lo,
                        int64_t hi, bool tile, bool zero_pass, std::vector<TiledJob>* zero,

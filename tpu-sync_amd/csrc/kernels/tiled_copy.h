@@ -22,8 +22,9 @@
 //     zero when tiling and are skipped when detiling).
 //   * kDetileGen / kTileGen: any other layout, element by element through the
 //     index map of the nested tiling.
-//   * kZero: clears a tiled buffer (V-byte vectors), launched before a tile
-//     job writes its data so that padding reads as zero.
+//   * kZero: clears a tiled buffer (V-byte vectors), launched before a
+//     general-form tile job writes its data so that padding reads as zero
+//     (standard-form tiling writes its padding itself).
 #ifndef KVX_KERNELS_TILED_COPY_H_
 #define KVX_KERNELS_TILED_COPY_H_
 
