@@ -137,17 +137,36 @@ def test_random_general_layouts_match_oracle(kvx, oracle, cuda):
 
 def test_misaligned_buffers_match_oracle(kvx, oracle, cuda):
     """Buffers 1-8 bytes past a 256-byte boundary narrow the vectors (a packed
-    layout below 4-byte vectors goes element by element)."""
+    layout below 4-byte vectors goes element by element); buffers that are not
+    aligned to the element size are refused."""
     rng = np.random.default_rng(6)
     lays = [dict(itemsize=2, dims=[40, 384], minor_to_major=[1, 0], tiles=[[8, 128], [2, 1]]),
             dict(itemsize=1, dims=[40, 384], minor_to_major=[1, 0], tiles=[[8, 128], [4, 1]]),
             dict(itemsize=4, dims=[3, 20, 200], minor_to_major=[2, 1, 0], tiles=[[8, 128]])]
     for lay in lays:
         for lo, to in [(2, 0), (0, 2), (4, 8), (8, 4), (1, 0), (0, 1)]:
-            if lo % lay["itemsize"] or to % lay["itemsize"]:
-                continue
             print("tiling case misaligned", lay, lo, to, flush=True)
+            if lo % lay["itemsize"] or to % lay["itemsize"]:
+                # Below the element size: refused on the host before any launch.
+                check_misaligned_refused(kvx, cuda, lay, lo, to)
+                continue
             check_layout(kvx, oracle, cuda, lay, rng, lin_off=lo, tiled_off=to)
+
+
+def check_misaligned_refused(kvx, cuda, lay, lin_off, tiled_off):
+    """tile_buffer / detile_buffer with a buffer that is not aligned to the
+    element size return INVALID_ARGUMENT and leave both buffers untouched."""
+    L = as_layout(kvx, lay)
+    lin_all = torch.full((L.logical_bytes + lin_off,), 0x11, dtype=torch.uint8, device=cuda)
+    til_all = torch.full((L.tiled_bytes + tiled_off,), 0x22, dtype=torch.uint8, device=cuda)
+    lin = lin_all[lin_off:]
+    til = til_all[tiled_off:]
+    for fn, args in ((kvx.tiling.tile_buffer, (L, lin, til)),
+                     (kvx.tiling.detile_buffer, (L, til, lin))):
+        with pytest.raises(kvx.KvxError) as e:
+            fn(*args).Await()
+        assert e.value.code == 3, e.value
+    assert (u8(lin_all) == 0x11).all() and (u8(til_all) == 0x22).all()
 
 
 def numpy_tile_2d(x, tH, tW, P=1):
@@ -256,6 +275,47 @@ def test_weight_sync_tiled_tensors(kvx, oracle, cuda, chunk):
         assert np.array_equal(u8(tensors[k]), want), k
     # The host view of a tiled weight has its logical shape.
     assert tuple(ws.get_host_buffer(0, 0).shape) == (300, 1000)
+    ws.close()
+
+
+def test_weight_sync_odd_tile_row_cuts_keep_alignment(kvx, oracle, cuda):
+    """4 KiB staging chunks over an int8 weight whose tile rows are 301 bytes:
+    the chunk cuts fall on odd byte offsets (3913, 7826, 11739), and the
+    chunk starting at 11739 holds a whole f32 tiled weight (host offset
+    12288) and the head of a packed bf16 one. Each chunk sits in its staging
+    buffer at its start's offset modulo 256, so those weights stay 256-byte
+    aligned in staging; both directions match the oracle."""
+    rng = np.random.default_rng(11)
+    lays = [dict(itemsize=1, dims=[40, 301], minor_to_major=[1, 0], tiles=[[1, 128]]),
+            dict(itemsize=4, dims=[8, 64], minor_to_major=[1, 0], tiles=[[2, 64]]),
+            dict(itemsize=2, dims=[16, 128], minor_to_major=[1, 0], tiles=[[2, 128], [2, 1]]),
+            None]
+    tensors, layouts = [], []
+    for lay in lays:
+        L = as_layout(kvx, lay) if lay is not None else None
+        n = L.tiled_bytes if L is not None else 1000
+        tensors.append(torch.from_numpy(rng.integers(0, 256, n, dtype=np.uint8)).to(cuda))
+        layouts.append(L)
+    ws = kvx.WeightSynchronizer([[t] for t in tensors], layouts=[[l] for l in layouts],
+                                chunk_bytes=4096)
+    assert [ws.host_buffer_info(k, 0)[2] for k in range(4)] == [0, 12288, 14336, 18432]
+    dev0 = [u8(t) for t in tensors]
+    ws.d2h().Await()
+    img = ws.host_image()
+    for k in range(4):
+        _, n, off = ws.host_buffer_info(k, 0)
+        want = oracle.detile(lays[k], dev0[k]) if lays[k] is not None else dev0[k]
+        assert np.array_equal(img[off:off + n], want), k
+    new = {}
+    for k in range(4):
+        _, n, off = ws.host_buffer_info(k, 0)
+        new[k] = rng.integers(0, 256, n, dtype=np.uint8)
+        img[off:off + n] = new[k]
+        tensors[k].fill_(0xA5)
+    ws.h2d().Await()
+    for k in range(4):
+        want = oracle.tile(lays[k], new[k]) if lays[k] is not None else new[k]
+        assert np.array_equal(u8(tensors[k]), want), k
     ws.close()
 
 

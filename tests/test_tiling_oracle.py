@@ -193,6 +193,30 @@ def test_fast_division_matches_integer_division(tmp_path):
     assert "fast div ok" in r.stdout
 
 
+def test_tiled_job_builder_alignment_and_limits(tmp_path):
+    """The job builder of libkvx on the CPU (tests/tiled_jobs_check.cc):
+    buffers below the element size's alignment are refused for every form,
+    and the 32-bit unit limits are re-checked at the vector width the
+    buffers allow (an 8 GiB int8 tensor at 1- or 2-byte alignment is refused
+    instead of wrapping its unit indices)."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    libdir = os.path.join(ROOT, "tpu-sync_amd")
+    if cxx is None or not os.path.exists(os.path.join(libdir, "libkvx.so")):
+        pytest.skip("no C++ compiler or libkvx.so not built")
+    exe = tmp_path / "tiled_jobs_check"
+    env = {k: v for k, v in os.environ.items() if k != "LD_PRELOAD"}
+    r = subprocess.run([cxx, "-O1", "-std=c++17", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                        "-I/opt/rocm/include",
+                        "-I", os.path.join(ROOT, "tpu-sync_amd", "csrc", "host"),
+                        os.path.join(ROOT, "tests", "tiled_jobs_check.cc"), "-o", str(exe),
+                        "-L", libdir, "-lkvx", f"-Wl,-rpath,{libdir}"],
+                       capture_output=True, text=True, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all checks passed" in r.stdout
+
+
 def _standard(lay):
     dims, tiles, mtm = lay["dims"], lay["tiles"], lay["minor_to_major"]
     r = len(dims)

@@ -259,6 +259,30 @@ StatusOr<TiledPlan> PlanTiled(const TiledLayout& l) {
   return p;
 }
 
+// Whether the standard form's units at vector width v stay within the
+// kernels' 32-bit unit indices and FastDivU32 divisors: linear order counts
+// B * ceil(H / P) * (W * s / v) units, tiled order tiled_bytes / (P * v).
+static bool StdUnitsFit(const TiledPlan& p, int v, bool tile) {
+  if (v <= 0) return false;
+  const uint64_t s = static_cast<uint64_t>(p.layout.itemsize);
+  const uint64_t ng = (p.H + p.P - 1) / p.P;
+  const uint64_t ncv = p.W * s / static_cast<uint64_t>(v);
+  uint64_t units = 0;
+  if (ncv >= static_cast<uint64_t>(kDivLimit) || ng >= static_cast<uint64_t>(kDivLimit) ||
+      __builtin_mul_overflow(p.B * ng, ncv, &units) ||
+      units >= static_cast<uint64_t>(kU32Limit)) {
+    return false;
+  }
+  if (tile) {
+    const uint64_t ncvt = p.tW * s / static_cast<uint64_t>(v);
+    const uint64_t tunits = static_cast<uint64_t>(p.tiled_bytes) / (p.P * static_cast<uint64_t>(v));
+    if (ncvt >= static_cast<uint64_t>(kDivLimit) || tunits >= static_cast<uint64_t>(kU32Limit)) {
+      return false;
+    }
+  }
+  return true;
+}
+
 Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int64_t lo,
                        int64_t hi, bool tile, bool zero_pass, std::vector<TiledJob>* zero,
                        std::vector<TiledJob>* jobs) {
@@ -269,6 +293,12 @@ Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int6
   }
   if (tiled == 0) return InvalidArgumentError("tiled copy: null tiled buffer");
   const int64_t s = p.layout.itemsize;
+  // Both forms address whole elements: a buffer that is not aligned to the
+  // element size would give the vector form fewer bytes per vector than one
+  // element (no element per vector at all).
+  if (((tiled | linear) & static_cast<uint64_t>(s - 1)) != 0) {
+    return InvalidArgumentError("tiled copy: buffers not aligned to the element size");
+  }
   // Units need vectors aligned on both buffers; a packed layout whose
   // buffers allow less than 4 bytes goes element by element.
   int v = WidestVector(tiled | linear, p.vec);
@@ -288,7 +318,16 @@ Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int6
   } else if (p.P > 1) {
     v = std::min(v, 16 / static_cast<int>(p.P));
   }
-  const bool use_std = p.standard && (p.P == 1 || v >= 4);
+  // PlanTiled checked the 32-bit unit and divisor limits at the plan's widest
+  // vector; narrower buffers multiply the unit counts, so they are checked
+  // again at the width chosen here (the kernels index units in 32 bits).
+  bool use_std = p.standard && (p.P == 1 || v >= 4);
+  if (use_std && !StdUnitsFit(p, v, tile)) use_std = false;
+  if (!use_std && p.standard && p.gen.empty()) {
+    return UnimplementedError(
+        "tiled copy: this layout has more 32-bit-indexed units than one launch can address "
+        "at the buffers' alignment");
+  }
   const bool tiled_order = use_std && tile;
   // Tiled-order units write the padding themselves; otherwise it is cleared
   // first.
