@@ -100,8 +100,10 @@ Status WeightSynchronizer::Init() {
     }
   }
   for (int k = 0; k < cfg_.staging_chunks; ++k) {
+    // kTensorAlign spare bytes: a chunk sits at (lo mod kTensorAlign) in its
+    // buffer (ChunkRange), so every tensor keeps its host alignment there.
     void* p = nullptr;
-    KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, chunk));
+    KVX_HIP_RETURN_IF_ERROR(hipMalloc(&p, chunk + kTensorAlign));
     ring_.push_back(reinterpret_cast<uint64_t>(p));
     KVX_ASSIGN_OR_RETURN(hipEvent_t f, NewEvent());
     free_.push_back(f);
@@ -277,7 +279,13 @@ Status WeightSynchronizer::ChunkRange(bool d2h, int64_t range_lo, int64_t range_
     }
     const size_t k = next_;
     next_ = (next_ + 1) % ring_.size();
-    const uint64_t buf = ring_[k];
+    // The chunk starts at lo's offset within a kTensorAlign span of its
+    // buffer (hipMalloc returns kTensorAlign-aligned memory), so a tensor at
+    // a kTensorAlign-aligned host offset is kTensorAlign-aligned in staging
+    // too, wherever the previous cut fell (a tile row of an odd-width int8
+    // tensor, say): the vector kernels keep their widest vectors and no
+    // tensor origin drops below its element size.
+    const uint64_t buf = ring_[k] + static_cast<uint64_t>(lo % kTensorAlign);
     KVX_RETURN_IF_ERROR(RangeEntries(lo, hi, buf, /*pack=*/d2h, &entries, &zero, &tiled));
     // Both directions share the ring: a slot last used by the other
     // direction's stream is reused once that use has finished.
