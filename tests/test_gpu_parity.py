@@ -110,6 +110,12 @@ PATHS = {
     # A pinned mirror whose short runs also go through the bounce lanes.
     "lanes": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                   host_alloc="pinned", transfer_mode="lanes", host_copy_threads=3),
+    # One-slot rings: every chunk refills the slot the previous chunk's
+    # scatter (H2D) or host copy (D2H) still owns.
+    "bounce_1slot": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16,
+                         staging_chunks=1, host_alloc="malloc", host_copy_threads=3),
+    "lanes_1slot": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=1,
+                        host_alloc="pinned", transfer_mode="lanes", host_copy_threads=3),
     # Pageable mirror left to the runtime's per-run hipMemcpyAsync.
     "pageable": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                      host_alloc="malloc", host_copy_threads=-1),
@@ -122,7 +128,7 @@ MODES = ["staged", "zero_copy"]
 
 
 @pytest.mark.parametrize("path", ["direct", "staged", "zero_copy", "bounce", "bounce_hip",
-                                  "lanes", "pageable", "auto"])
+                                  "bounce_1slot", "lanes", "lanes_1slot", "pageable", "auto"])
 @pytest.mark.parametrize("bb", [32768, 61424, 12992, 1024, 48, 36, 3])
 def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
     if path == "bounce_hip":
@@ -147,10 +153,11 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
         assert mir.transfer(d2h, src, dst, sizes, layer, shard) == 0
         mir.check(mgr, dev)
     stats = mgr.engine_stats()
-    if path in ("staged", "bounce", "bounce_hip", "lanes", "pageable"):
+    if path in ("staged", "bounce", "bounce_hip", "bounce_1slot", "lanes", "lanes_1slot",
+                "pageable"):
         assert stats["direct_copies"] == 0 and stats["staged_copies"] == 12
         assert stats["chunks"] > 12 or bb < 1024
-        lanes = path.startswith("bounce") or path == "lanes"
+        lanes = path.startswith("bounce") or path.startswith("lanes")
         assert stats["bounce_copies"] == (12 if lanes else 0)
     elif path == "zero_copy":
         assert stats["zero_copy_copies"] == 12 and stats["memcpy_calls"] == 0
@@ -163,7 +170,7 @@ def test_random_d2h_h2d_match_oracle(kvx, oracle, cuda, monkeypatch, path, bb):
     else:
         assert stats["staged_copies"] == 0 and stats["zero_copy_copies"] == 0
     # The lanes' DMAs: one SDMA engine bit per direction, or hipMemcpyAsync.
-    if path in ("bounce", "lanes"):
+    if path in ("bounce", "bounce_1slot", "lanes", "lanes_1slot"):
         engines = mgr.lane_dma_engines
         assert engines is not None and all(e and e & (e - 1) == 0 for e in engines), engines
     elif path == "bounce_hip":

@@ -945,6 +945,13 @@ Status TransferEngine::PipelineBounceSdma(const LaneView& lane, Direction dir,
   for (const ChunkWork& ch : chunks) {
     const size_t k = ring.next;
     ring.next = (ring.next + 1) % ring.bufs.size();
+    if (prev != nullptr && prev_k == k) {
+      // A one-slot ring: the previous chunk still owns this slot, so its
+      // scatter goes first (after its DMA has landed), and the wait below
+      // then covers that scatter before the slot is refilled.
+      KVX_RETURN_IF_ERROR(scatter(*prev, prev_k));
+      prev = nullptr;
+    }
     // The slot's last scatter has read the staging buffer (its DMA landed
     // before that scatter was launched).
     if (ring.used[k]) KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(ring.free[k]));
