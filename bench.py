@@ -18,6 +18,22 @@ Printed as one JSON line, with the gather kernel's HBM roofline (HIP events
 on the kernel's stream over the timed region), measured pinned PCIe peaks
 per direction, and the CPU host pack/unpack baseline (the oracle's
 restatement of the reference's ReadBlockBytes/WriteBlockBytes loop).
+
+Every number comes from checked bytes. Before timing, one offload + reload
+with the headline manager is compared with a torch snapshot (the
+reference's perf gate, tpu_sync/benchmarks/perf_core.py:112-142); after
+each timed workload, outside its timed region, the bytes it moved are
+compared with torch indexing (the last duplex step's offload and reload,
+each isolated kernel's last launch, the extra configs' outputs). A mismatch
+raises and the benchmark exits non-zero; each workload that passed carries
+"verified": true.
+
+The kernels are also set against the box itself: box_copy is the library's
+strided copy over one contiguous buffer of the same bytes in this process,
+and every HBM kernel reports frac_of_box_copy beside its fraction of the
+8 TB/s peak. placement times the same kernels over the pool allocated the
+other way (one buffer sliced per storage, or one allocation per storage),
+alternating in this process.
 """
 import argparse
 import json
@@ -50,6 +66,24 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+POOL_ALLOC_TEXT = {
+    "single": "one device buffer sliced into one [pool_blocks, block_bytes] view per storage",
+    "per_storage": "one device allocation per storage",
+}
+
+
+def make_pool(torch, dev, gen, S, P, bb, how):
+    """S storages of [P, bb] random bytes: views of one buffer ("single", as
+    a serving engine that allocates its whole KV cache at once) or one
+    allocation each ("per_storage")."""
+    if how == "single":
+        buf = torch.randint(-2**31, 2**31 - 1, (S * P * bb // 4,), dtype=torch.int32, device=dev,
+                            generator=gen).view(torch.uint8)
+        return [buf[k * P * bb:(k + 1) * P * bb].view(P, bb) for k in range(S)]
+    return [torch.randint(-2**31, 2**31 - 1, (P, bb // 4), dtype=torch.int32, device=dev,
+                          generator=gen).view(torch.uint8) for _ in range(S)]
+
+
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -63,13 +97,19 @@ def parse_args():
     p.add_argument("--chunks", type=int, default=4)
     p.add_argument("--cpu-seconds", type=float, default=5.0,
                    help="minimum seconds per CPU-baseline leg (0 skips it)")
+    p.add_argument("--pool-alloc", default="single", choices=["single", "per_storage"],
+                   help="how the headline pool is allocated: one buffer sliced per storage "
+                        "(measured faster for the scatter) or one allocation per storage")
+    p.add_argument("--placement-rounds", type=int, default=3,
+                   help="rounds of the gather/scatter kernels over the headline pool and a "
+                        "pool allocated the other way, alternating in this process (0: skip)")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the per-mode, one-direction and PCIe-peak measurements")
     p.add_argument("--mode", default="auto", choices=["auto", "staged", "zero_copy"],
                    help="transfer mode of the headline offload/reload loop")
-    p.add_argument("--configs", default="fp8,weights,tiled,pools,lanes,zipf",
+    p.add_argument("--configs", default="scenarios,fp8,weights,tiled,pools,lanes,zipf",
                    help="comma list of extra workloads to measure after the headline "
-                        "(fp8, weights, tiled, pools, lanes, zipf; empty for none)")
+                        "(scenarios, fp8, weights, tiled, pools, lanes, zipf; empty for none)")
     p.add_argument("--zipf-host-blocks", type=int, default=0,
                    help="host tier of the Zipf churn, in 5 MiB Llama-3-70B blocks (0: "
                         "the configured 256 GB budget, capped by free /dev/shm, available "
@@ -317,17 +357,20 @@ def run_duplex(torch, mgr, batch, slots, steps, warmup):
     (offloaded at step k-2) into fresh free blocks. Step k waits only for the
     copies of step k-2, the last ones touching its slots, so step k-1's copies
     are still in flight when step k is issued: the steady state of a serving
-    loop, with no drain between steps. Returns the seconds the timed steps
-    took (all of them finished)."""
+    loop, with no drain between steps (batch() keeps consecutive steps'
+    blocks disjoint). Returns the seconds the timed steps took (all of them
+    finished) and the last step (k, offloaded ids, reload targets)."""
     for s in (2, 3):
         mgr.d2h(batch()[0], slots[s]).Await()  # the first reloads read real data
     inflight = {}
+    last = [None]
 
     def step(k):
         for f in inflight.pop(k - 2, []):
             f.Await()
         ids, free = batch()
         inflight[k] = [mgr.d2h(ids, slots[k % 4]), mgr.h2d(slots[(k + 2) % 4], free)]
+        last[0] = (k, ids, free)
 
     def drain():
         for fs in inflight.values():
@@ -346,10 +389,17 @@ def run_duplex(torch, mgr, batch, slots, steps, warmup):
     for k in range(steps):
         step(k)
     drain()
-    return time.perf_counter() - t0
+    return time.perf_counter() - t0, last[0]
 
 
 def one_direction(mgr, batch, slots, reps):
+    """Offload alone, then reload alone, one copy at a time, after two
+    untimed copies each way: the first D2H copies of a fresh manager, and
+    those right after the runtime has freed device memory, run 6-13 %
+    slower (measured 50.4 and 46.6 against 53.8 GB/s)."""
+    for _ in range(2):
+        mgr.d2h(batch()[0], slots[0]).Await()
+        mgr.h2d(slots[0], batch()[1]).Await()
     t0 = time.perf_counter()
     for _ in range(reps):
         mgr.d2h(batch()[0], slots[0]).Await()
@@ -368,11 +418,129 @@ def kernel_gbps(kt):
     return kt["bytes"] / (kt["total_ms"] / 1e3) / 1e9
 
 
+class Mismatch(AssertionError):
+    """Bytes a timed workload moved differ from what torch says they should
+    be; the benchmark exits non-zero (as the reference's perf gate does,
+    tpu_sync/benchmarks/perf_core.py:112-142)."""
+
+
+def check(ok, what):
+    if not ok:
+        raise Mismatch(f"verification failed: {what}")
+
+
+def rows_u8(t):
+    """A [major, ...] device tensor as [major, row bytes] uint8."""
+    import torch
+    return t.reshape(t.shape[0], -1).view(torch.uint8)
+
+
+def batch_source(rng, P, n):
+    """Per step, n random blocks to offload and n other random free blocks to
+    reload into, all 2n disjoint from the previous step's 2n. Consecutive
+    steps overlap in flight (step k waits only for step k-2), so a block the
+    previous step is still reloading into is never offloaded, and a block it
+    is still offloading is never reloaded into: every step's bytes are then
+    well defined and the last step can be checked."""
+    prev = np.empty(0, np.int64)
+
+    def batch():
+        nonlocal prev
+        perm = rng.permutation(P)
+        if prev.size:
+            perm = perm[~np.isin(perm, prev)]
+        sel = perm[:2 * n]
+        prev = sel
+        return sel[:n].tolist(), sel[n:].tolist()
+    return batch
+
+
+def host_rows(mgr, w, bb, first, count):
+    """Host mirror blocks [first, first + count) of storage w, as a uint8
+    numpy view [count, bb]."""
+    return mgr.host_view(w).reshape(-1, bb)[first:first + count]
+
+
+def verify_duplex(torch, mgr, storages, slots, last):
+    """After a duplex run has drained, the last step's copies are checked
+    against torch indexing: its offload left the bytes of its source blocks
+    in its host slot, and its reload left the bytes of the slot it read
+    (offloaded two steps before) in its free blocks."""
+    k, ids, free = last
+    dev = storages[0].device
+    ids_t = torch.tensor(ids, device=dev)
+    free_t = torch.tensor(free, device=dev)
+    s_off, s_rel = slots[k % 4], slots[(k + 2) % 4]
+    for w, t in enumerate(storages):
+        r = rows_u8(t)
+        bb = r.shape[1]
+        h_off = torch.from_numpy(host_rows(mgr, w, bb, s_off[0], len(s_off))).to(dev)
+        check(torch.equal(r[ids_t], h_off), f"offload of the last step, storage {w}")
+        h_rel = torch.from_numpy(host_rows(mgr, w, bb, s_rel[0], len(s_rel))).to(dev)
+        check(torch.equal(r[free_t], h_rel), f"reload of the last step, storage {w}")
+
+
+def verify_round_trip(torch, mgr, storages, src, host, dst):
+    """One offload + reload with the manager, outside any timed region (the
+    reference's verify_roundtrip, perf_core.py:112-142): the device blocks
+    dst must then hold the bytes src held before (a torch snapshot)."""
+    dev = storages[0].device
+    src_t = torch.tensor(src, device=dev)
+    dst_t = torch.tensor(dst, device=dev)
+    snap = [rows_u8(t)[src_t].clone() for t in storages]
+    mgr.d2h(src, host, [1] * len(src)).Await()
+    mgr.h2d(host, dst, [1] * len(dst)).Await()
+    torch.cuda.synchronize()
+    for w, t in enumerate(storages):
+        check(torch.equal(rows_u8(t)[dst_t], snap[w]), f"round trip, storage {w}")
+
+
+def box_copy(torch, pkg, src, dst, reps, stream):
+    """The box's streaming-copy yardstick: the library's strided kernel over
+    one contiguous entry (src -> dst, the same bytes as a gather launch),
+    timed by HIP events on the stream it runs on; read + write bytes per
+    second. The copy is checked against its source."""
+    plan = pkg.StridedPlan([pkg.StridedEntry(src.data_ptr(), dst.data_ptr(), src.numel())])
+    t = min(timed_events(torch, lambda: pkg.copy_strided(plan, stream=stream), reps, stream)
+            for _ in range(3))
+    torch.cuda.synchronize()
+    check(torch.equal(dst, src), "box copy")
+    plan.close()
+    return 2 * src.numel() / t / 1e9
+
+
+def frac_of_box(gbps, box_gbps):
+    return round(gbps / box_gbps, 4) if gbps and box_gbps else None
+
+
+def torch_detile(torch, tiled, H, W, tH=8, tW=128, P=2):
+    """The row-major [H, W] image of a 16-bit tensor stored in the
+    {T(tH,tW)(P,1)} layout, by torch reshapes (an independent formulation of
+    the nested tiling: pad to whole tiles, tiles row-major, P rows of a tile
+    interleaved element by element)."""
+    nT0, nT1 = -(-H // tH), -(-W // tW)
+    t = tiled.view(nT0, nT1, tH // P, tW, P).transpose(-1, -2)
+    t = t.reshape(nT0, nT1, tH, tW).permute(0, 2, 1, 3).reshape(nT0 * tH, nT1 * tW)
+    return t[:H, :W]
+
+
+def torch_tile(torch, x, tH=8, tW=128, P=2):
+    """The inverse of torch_detile, padding written as zero."""
+    H, W = x.shape
+    nT0, nT1 = -(-H // tH), -(-W // tW)
+    pad = torch.zeros(nT0 * tH, nT1 * tW, dtype=x.dtype, device=x.device)
+    pad[:H, :W] = x
+    t = pad.view(nT0, tH, nT1, tW).permute(0, 2, 1, 3).reshape(nT0, nT1, tH // P, P, tW)
+    return t.transpose(-1, -2).contiguous().reshape(-1)
+
+
 def bench_fp8_scales(torch, pkg, dev, args, rng):
     """fp8 KV (32 layers, 8 KV heads, head_dim 128, 16-token blocks, e4m3
     bytes) plus one fp32 scale per (layer, block, head): 512-block offload +
     reload at once, and the gather kernel moving payload and scales in one
-    launch."""
+    launch. Random payload bytes cover every e4m3 pattern (NaN, denormals);
+    every moved byte is checked against torch indexing outside the timed
+    regions."""
     L, P, H, n = 32, 16384, 8, 512
     bb = 16 * H * 128
     log(f"fp8: allocating {2 * L} x {P} x {bb} B pool + {L} scale tables")
@@ -380,34 +548,42 @@ def bench_fp8_scales(torch, pkg, dev, args, rng):
     kv = [torch.randint(0, 256, (P, bb), dtype=torch.uint8, device=dev, generator=gen)
           for _ in range(2 * L)]
     sc = [torch.randn(P, H, device=dev, generator=gen) for _ in range(L)]
+    storages = kv + sc
+    torch.cuda.synchronize()
     mgr = pkg.KVCacheManager(kv, host_blocks_to_allocate=4 * n, scale_tables=sc,
                              staging_chunk_bytes=args.chunk_mib << 20,
                              staging_chunks=args.chunks, profile_kernels=True)
     slots = [list(range(k * n, (k + 1) * n)) for k in range(4)]
-
-    def batch():
-        perm = rng.permutation(P)
-        return perm[:n].tolist(), perm[n:2 * n].tolist()
-
+    batch = batch_source(rng, P, n)
+    ids, free = batch()
+    verify_round_trip(torch, mgr, storages, ids, slots[0], free)
     step_bytes = 2 * n * (2 * L * bb + L * H * 4)
-    el = run_duplex(torch, mgr, batch, slots, args.sub_steps, args.warmup)
+    el, last = run_duplex(torch, mgr, batch, slots, args.sub_steps, args.warmup)
+    verify_duplex(torch, mgr, storages, slots, last)
     staging = torch.empty(n * (2 * L * bb + L * H * 4), dtype=torch.uint8, device=dev)
     s = torch.cuda.Stream(dev)
-    ids, _ = batch()
-    mgr.gather(ids, staging, stream=s).Await()
+    id_sets = [batch()[0] for _ in range(16)]
+    mgr.gather(id_sets[0], staging, stream=s).Await()
     mgr.kernel_times(True, reset=True)
-    for f in [mgr.gather(ids, staging, stream=s) for _ in range(args.sub_steps)]:
+    for f in [mgr.gather(id_sets[k % 16], staging, stream=s) for k in range(args.sub_steps)]:
         f.Await()
     g = kernel_gbps(mgr.kernel_times(True, reset=True))
+    # The last gather's staging: payload then scales, storage by storage.
+    last_ids = torch.tensor(id_sets[(args.sub_steps - 1) % 16], device=dev)
+    want = torch.cat([rows_u8(t)[last_ids].reshape(-1) for t in storages])
+    torch.cuda.synchronize()
+    check(torch.equal(staging, want), "fp8 payload + scales gather")
     out = {"workload": "fp8 e4m3 KV + fp32 scale per (layer, block, head), Llama-3-8B shape",
            "offload_reload_gbps": round(args.sub_steps * step_bytes / el / 1e9, 2),
            "blocks_per_s": round(args.sub_steps * 2 * n / el, 1),
            "gather_payload_and_scales_gbps": round(g, 1) if g else None,
            "gather_frac_of_hbm_peak": round(g / HBM_PEAK_GBPS, 4) if g else None,
-           "bytes_per_block": 2 * L * bb + L * H * 4}
+           "gather_frac_of_box_copy": frac_of_box(g, args.box_copy_gbps),
+           "bytes_per_block": 2 * L * bb + L * H * 4,
+           "verified": True}
     log(f"fp8: {out}")
     mgr.close()
-    del kv, sc, staging
+    del kv, sc, storages, staging
     torch.cuda.empty_cache()
     return out
 
@@ -420,15 +596,30 @@ def llama3_8b_param_shapes():
     return shapes + [(h,), (vocab, h)]
 
 
+def verify_weight_image(torch, ws, tensors_u8, staging, what):
+    """Every tensor's bytes at its offset-table position of `staging` (a
+    device buffer holding the packed image)."""
+    for k, t in enumerate(tensors_u8):
+        _, nbytes, off = ws.host_buffer_info(k, 0)
+        check(nbytes == t.numel() and torch.equal(staging[off:off + nbytes], t),
+              f"{what}, tensor {k}")
+
+
 def bench_weight_sync(torch, pkg, dev, args):
     """Llama-3-8B parameter set (291 bf16 tensors, 8.03e9 elements): device
     pack into one contiguous staging buffer via the offset table, pipelined
     pack + D2H to pinned host, H2D + unpack, and an 8-way column split of the
-    226 2-D weights."""
+    226 2-D weights. Each is checked against torch outside its timed region:
+    the packed image against the tensors, the host image against the packed
+    image, H2D and unpack against a device copy of the tensors, the split
+    chunks against torch column slices."""
     shapes = llama3_8b_param_shapes()
     log("weights: allocating 291 bf16 tensors (16.06 GB)")
     params = [torch.empty(s, dtype=torch.bfloat16, device=dev).normal_(0, 0.02)
               for s in shapes]
+    ref = [t.clone() for t in params]
+    as_u8 = [t.reshape(-1).view(torch.uint8) for t in params]
+    torch.cuda.synchronize()  # the pack runs on a stream of its own
     total = sum(t.numel() * 2 for t in params)
     t0 = time.perf_counter()
     ws = pkg.WeightSynchronizer([[t] for t in params], profile_kernels=True)
@@ -442,19 +633,35 @@ def bench_weight_sync(torch, pkg, dev, args):
         f.Await()
     pack_gbps = kernel_gbps(ws.kernel_times(True, reset=True))  # read+write counted once
     pack_gbps = pack_gbps * 2 if pack_gbps else None
+    torch.cuda.synchronize()
+    verify_weight_image(torch, ws, as_u8, staging, "pack")
     ws.d2h().Await()
     ws.kernel_times(True, reset=True)
     t0 = time.perf_counter()
     for _ in range(reps):
         ws.d2h().Await()
     d2h_gbps = reps * total / (time.perf_counter() - t0) / 1e9
+    check(torch.equal(torch.from_numpy(ws.host_image()).to(dev), staging), "d2h host image")
     t0 = time.perf_counter()
     for _ in range(reps):
         ws.h2d().Await()
     h2d_gbps = reps * total / (time.perf_counter() - t0) / 1e9
     ws.kernel_times(True, reset=True)
     ws.kernel_times(False, reset=True)
-    del staging
+    # H2D and unpack must restore tensors that were overwritten.
+    for t in params:
+        t.fill_(7)
+    torch.cuda.synchronize()
+    ws.h2d().Await()
+    torch.cuda.synchronize()
+    check(all(torch.equal(a, b) for a, b in zip(params, ref)), "h2d")
+    for t in params:
+        t.fill_(9)
+    torch.cuda.synchronize()  # the unpack runs on s, which does not wait for the fill
+    ws.unpack(staging, stream=s).Await()
+    torch.cuda.synchronize()
+    check(all(torch.equal(a, b) for a, b in zip(params, ref)), "unpack")
+    del staging, ref
     # Column split: one launch over every 2-D weight.
     mats = [t for t in params if t.dim() == 2]
     entries, outs = [], []
@@ -474,15 +681,23 @@ def bench_weight_sync(torch, pkg, dev, args):
     ev1.record(s)
     ev1.synchronize()
     split_s = ev0.elapsed_time(ev1) / 1e3 / reps
+    for m, chunk in zip(mats, outs):
+        c0 = 0
+        for c in chunk:
+            check(torch.equal(c, m[:, c0:c0 + c.shape[1]]), "column split")
+            c0 += c.shape[1]
+    split_gbps = 2 * split_bytes / split_s / 1e9
     out = {"workload": "Llama-3-8B parameter set, 291 bf16 tensors, 16.06 GB",
            "bytes": total, "pinned_host_setup_s": round(setup_s, 2),
            "pack_kernel_gbps": round(pack_gbps, 1) if pack_gbps else None,
            "pack_frac_of_hbm_peak": round(pack_gbps / HBM_PEAK_GBPS, 4) if pack_gbps else None,
+           "pack_frac_of_box_copy": frac_of_box(pack_gbps, args.box_copy_gbps),
            "d2h_gbps": round(d2h_gbps, 2), "h2d_gbps": round(h2d_gbps, 2),
-           "column_split_gbps": round(2 * split_bytes / split_s / 1e9, 1),
-           "column_split_frac_of_hbm_peak": round(2 * split_bytes / split_s / 1e9
-                                                  / HBM_PEAK_GBPS, 4),
-           "column_split_entries": len(entries)}
+           "column_split_gbps": round(split_gbps, 1),
+           "column_split_frac_of_hbm_peak": round(split_gbps / HBM_PEAK_GBPS, 4),
+           "column_split_frac_of_box_copy": frac_of_box(split_gbps, args.box_copy_gbps),
+           "column_split_entries": len(entries),
+           "verified": True}
     log(f"weights: {out}")
     ws.close()
     del params, outs, mats
@@ -502,33 +717,55 @@ def bench_weight_sync_tiled(torch, pkg, dev, args):
     log("weights_tiled: allocating 291 tiled bf16 tensors")
     params = [torch.empty(L.tiled_bytes // 2, dtype=torch.int16, device=dev).random_()
               for L in layouts]
+    torch.cuda.synchronize()  # the detile + pack runs on a stream of its own
     total = sum(L.logical_bytes for L in layouts)
     ws = pkg.WeightSynchronizer([[t] for t in params], layouts=[[L] for L in layouts],
                                 profile_kernels=True)
     staging = torch.empty(ws.total_bytes, dtype=torch.uint8, device=dev)
     s = torch.cuda.Stream(dev)
     reps = max(3, args.sub_steps // 4)
+    hw = [(1, sh[0]) if len(sh) == 1 else sh for sh in shapes]  # rank 1 tiles as (1, d0)
+
+    def image(k):  # tensor k's row-major image in the packed staging buffer
+        _, nbytes, off = ws.host_buffer_info(k, 0)
+        return staging[off:off + nbytes].view(torch.int16).view(hw[k])
+
     ws.pack(staging, stream=s).Await()
     ws.kernel_times(True, reset=True)
     for f in [ws.pack(staging, stream=s) for _ in range(reps)]:
         f.Await()
     kt = ws.kernel_times(True, reset=True)
     detile_ms = kt["total_ms"] / reps if kt["launches"] else None
+    torch.cuda.synchronize()
+    for k, t in enumerate(params):
+        check(torch.equal(image(k), torch_detile(torch, t, *hw[k])), f"detile + pack, tensor {k}")
     for f in [ws.unpack(staging, stream=s) for _ in range(reps)]:
         f.Await()
     kt = ws.kernel_times(False, reset=True)
     tile_ms = kt["total_ms"] / reps if kt["launches"] else None
+    torch.cuda.synchronize()
+    tiled_want = [torch_tile(torch, image(k)) for k in range(len(params))]
+    for k, t in enumerate(params):
+        check(torch.equal(t, tiled_want[k]), f"tile + unpack (padding zero), tensor {k}")
     ws.d2h().Await()
     t0 = time.perf_counter()
     for _ in range(reps):
         ws.d2h().Await()
     d2h_gbps = reps * total / (time.perf_counter() - t0) / 1e9
+    check(torch.equal(torch.from_numpy(ws.host_image()).to(dev), staging), "tiled d2h host image")
     t0 = time.perf_counter()
     for _ in range(reps):
         ws.h2d().Await()
     h2d_gbps = reps * total / (time.perf_counter() - t0) / 1e9
     ws.kernel_times(True, reset=True)
     ws.kernel_times(False, reset=True)
+    for t in params:
+        t.fill_(3)
+    torch.cuda.synchronize()
+    ws.h2d().Await()
+    torch.cuda.synchronize()
+    check(all(torch.equal(t, w) for t, w in zip(params, tiled_want)), "tiled h2d")
+    del tiled_want
     # The reference detiles on the host after the raw DMA (DetileBufferNDOptimized,
     # 4 threads): its restatement in the oracle, timed on one MLP weight.
     import numpy as np
@@ -552,10 +789,15 @@ def bench_weight_sync_tiled(torch, pkg, dev, args):
            "detile_pack_gbps": round(2 * total / detile_ms / 1e6, 1) if detile_ms else None,
            "detile_pack_frac_of_hbm_peak": round(2 * total / detile_ms / 1e6 / HBM_PEAK_GBPS, 4)
            if detile_ms else None,
+           "detile_pack_frac_of_box_copy": frac_of_box(2 * total / detile_ms / 1e6, args.box_copy_gbps)
+           if detile_ms else None,
            "tile_unpack_ms": round(tile_ms, 3) if tile_ms else None,
            "tile_unpack_gbps": round(2 * total / tile_ms / 1e6, 1) if tile_ms else None,
            "tile_unpack_frac_of_hbm_peak": round(2 * total / tile_ms / 1e6 / HBM_PEAK_GBPS, 4)
            if tile_ms else None,
+           "tile_unpack_frac_of_box_copy": frac_of_box(2 * total / tile_ms / 1e6, args.box_copy_gbps)
+           if tile_ms else None,
+           "verified": True,
            # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE with the
            # same calibration (profiles/tiled_copy_weight_sync_llama3_8b_trace.txt).
            "detile_pack_traffic": int((7844359.0 / 0.50002 + 15684479.2) * 1024),
@@ -591,6 +833,7 @@ def bench_pools(torch, pkg, dev, args, rng):
     pools = [torch.empty(NB, stride, dtype=torch.uint8, device=dev) for _ in range(L)]
     for p in pools:
         p.random_(0, 256)
+    torch.cuda.synchronize()
     mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=NB,
                              host_alloc=args.pools_host_alloc)
     specs = [pkg.PoolSpec("fa", l, 0, stride, NB, regions) for l in range(L)]
@@ -618,6 +861,37 @@ def bench_pools(torch, pkg, dev, args, rng):
     t_d2h = timed(lambda: pool_copy(True), reps)
     t_h2d = timed(lambda: pool_copy(False), reps)
     t_dense = timed(lambda: mgr.d2h(ids, ids).Await(), reps)
+    # Live bytes by the regions' definition: unit u of a region covers
+    # [offset + u * stride, offset + u * stride + units_per_stride * unit).
+    mask_np = np.zeros(stride, bool)
+    for r in regions:
+        for u in range(r.num_units):
+            a = r.offset_bytes + u * r.stride_bytes
+            mask_np[a:a + r.units_per_stride * r.unit_bytes] = True
+    mask = torch.from_numpy(mask_np).to(dev)
+    ids_t = torch.tensor(ids, device=dev)
+    # D2H onto zeroed host blocks: the live bytes arrive, the padding stays 0.
+    for l in range(L):
+        host_rows(mgr, l, stride, 0, NB)[ids] = 0
+    pool_copy(True)
+    for l in range(L):
+        h = torch.from_numpy(host_rows(mgr, l, stride, 0, NB)[ids]).to(dev)
+        d = pools[l][ids_t]
+        check(torch.equal(h[:, mask], d[:, mask]) and not h[:, ~mask].any(),
+              f"pool d2h, storage {l}")
+    # H2D of new host bytes: live bytes land, the device padding is untouched.
+    for l in range(L):
+        hr = host_rows(mgr, l, stride, 0, NB)
+        hr[ids] = rng.integers(0, 256, (n, stride), dtype=np.uint8)
+    before = [pools[l][ids_t].clone() for l in range(L)]
+    pool_copy(False)
+    torch.cuda.synchronize()
+    for l in range(L):
+        h = torch.from_numpy(host_rows(mgr, l, stride, 0, NB)[ids]).to(dev)
+        d = pools[l][ids_t]
+        check(torch.equal(d[:, mask], h[:, mask]) and torch.equal(d[:, ~mask], before[l][:, ~mask]),
+              f"pool h2d, storage {l}")
+    del before
     live_bytes = L * n * live
     out = {"workload": "FA-like sparse pool (4 head groups x 32 KiB live per 320 KiB block), "
                        f"{L} storages x {NB} blocks, {n} random blocks per copy",
@@ -627,7 +901,8 @@ def bench_pools(torch, pkg, dev, args, rng):
            "pool_h2d_live_gbps": round(live_bytes / t_h2d / 1e9, 2),
            "pool_d2h_ms": round(t_d2h * 1e3, 3),
            "whole_block_d2h_ms": round(t_dense * 1e3, 3),
-           "speedup_vs_whole_blocks": round(t_dense / t_d2h, 2)}
+           "speedup_vs_whole_blocks": round(t_dense / t_d2h, 2),
+           "verified": True}
     log(f"pools: {out}")
     mgr.close()
     del pools
@@ -689,6 +964,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     pools = [torch.empty(P, bb, dtype=torch.uint8, device=dev) for _ in range(S)]
     for p in pools:
         p.random_(0, 256)
+    torch.cuda.synchronize()
     store = pkg.KVCacheStore(capacity=host_blocks, num_shards=1, store_server_ip="127.0.0.1",
                              metadata_shm_key="")
     tier = {}
@@ -849,6 +1125,12 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                                [t for nb, t in latency if nb < 128])}
                           if latency else None),
            "requests_64_to_127_blocks_vs_pcie_bound": small_vs_bound}
+    # One offload + reload through the same manager and host tier after the
+    # churn (its lanes, chunking and /dev/shm tier), checked against torch.
+    perm = rng.permutation(P)
+    verify_round_trip(torch, mgr, pools, perm[:512].tolist(),
+                      rng.permutation(host_blocks)[:512].tolist(), perm[512:1024].tolist())
+    out["verified"] = True
     log(f"zipf: {out}")
     mgr.close()
     store.close()
@@ -874,6 +1156,7 @@ def bench_lanes(torch, pkg, dev, args, rng):
     pools = [torch.empty(P, bb, dtype=torch.uint8, device=dev) for _ in range(S)]
     for p in pools:
         p.random_(0, 256)
+    torch.cuda.synchronize()
     key = f"kvx_lanes_{os.getpid()}"
     mgr = pkg.KVCacheManager(pools, host_blocks_to_allocate=HB, staging_chunk_bytes=32 << 20,
                              staging_chunks=4, host_alloc="shm", shm_key=key)
@@ -912,6 +1195,10 @@ def bench_lanes(torch, pkg, dev, args, rng):
         out[f"requests_of_{nb}_blocks"] = res
         log(f"lanes {nb} blocks: {res}")
     out["lane_dma_engines"] = mgr.lane_dma_engines
+    perm = rng.permutation(P)
+    verify_round_trip(torch, mgr, pools, perm[:512].tolist(),
+                      rng.permutation(HB)[:512].tolist(), perm[512:1024].tolist())
+    out["verified"] = True
     mgr.close()
     seg = f"/dev/shm/{key}_dev_{dev.index or 0}"
     if os.path.exists(seg):
@@ -921,9 +1208,97 @@ def bench_lanes(torch, pkg, dev, args, rng):
     return out
 
 
+# The reference's published raw-transfer figures on Ironwood (8 chips, 256
+# layers, 32 blocks), aggregate over the 8 chips: (H2D, D2H) GB/s per dtype
+# (examples/microbenchmarks/RAW_TRANSFER.md, "Benchmark Results").
+REFERENCE_SCENARIO_GBPS = {
+    "A": {"fp8": (78.50, 78.95), "bf16": (154.67, 148.79), "f32": (189.27, 184.97),
+          "int32": (190.62, 186.07)},
+    "B": {"fp8": (176.75, 173.43), "bf16": (183.38, 182.56), "f32": (192.88, 188.24),
+          "int32": (193.89, 189.00)},
+}
+
+
+def bench_reference_scenarios(torch, pkg, dev, args, peaks):
+    """The reference's raw-transfer microbenchmark at one device's share
+    (tpu_sync/core/kv_cache_manager_perf_test.cc:146-185, 336-366): 32 layers
+    x 32 blocks of [128 tokens, 8 heads, K/V, 128]. Scenario A: one array per
+    layer, [32, 128, 8, 2, 128]; Scenario B: one block-major array
+    [32, 32, 128, 8, 2, 128]. D2H copies the 16 odd blocks to the same host
+    blocks and H2D the 16 odd host blocks to the even device blocks, each as
+    one KVCacheManager.d2h / h2d call; afterwards every even device block
+    must equal its odd neighbour (the reference's own check). GB/s = bytes
+    moved / mean call time (the reference reports the mean), beside the
+    published figure per chip (the 8-chip aggregate / 8)."""
+    dtypes = {"fp8": torch.float8_e4m3fn, "bf16": torch.bfloat16, "f32": torch.float32,
+              "int32": torch.int32}
+    odd, even, ones = list(range(1, 32, 2)), list(range(0, 32, 2)), [1] * 16
+    iters, warm = max(5, args.sub_steps), 3
+    out = {"workload": "reference raw-transfer scenarios, one device's share: 32 layers x "
+                       "32 blocks of [128, 8, 2, 128]; odd blocks D2H, then H2D into the "
+                       "even blocks",
+           "iterations": iters}
+    for sc in ("A", "B"):
+        res = {}
+        for name, dt in dtypes.items():
+            if sc == "A":
+                tensors = [torch.empty((32, 128, 8, 2, 128), dtype=dt, device=dev)
+                           for _ in range(32)]
+            else:
+                tensors = [torch.empty((32, 32, 128, 8, 2, 128), dtype=dt, device=dev)]
+            for t in tensors:
+                rows_u8(t).random_(0, 256)
+            torch.cuda.synchronize()
+            mgr = pkg.KVCacheManager(tensors, host_blocks_to_allocate=32)
+            bb = rows_u8(tensors[0]).shape[1]
+            moved = 16 * bb * len(tensors)
+            for _ in range(warm):
+                mgr.d2h(odd, odd, ones).Await()
+                mgr.h2d(odd, even, ones).Await()
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                mgr.d2h(odd, odd, ones).Await()
+            t_d2h = (time.perf_counter() - t0) / iters
+            ev, od = torch.tensor(even, device=dev), torch.tensor(odd, device=dev)
+            for t in tensors:  # the timed H2D copies must rewrite the even blocks
+                rows_u8(t)[ev] = 0
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                mgr.h2d(odd, even, ones).Await()
+            t_h2d = (time.perf_counter() - t0) / iters
+            torch.cuda.synchronize()
+            for w, t in enumerate(tensors):
+                r = rows_u8(t)
+                check(torch.equal(r[ev], r[od]), f"scenario {sc} {name}: even == odd, layer {w}")
+                h = torch.from_numpy(host_rows(mgr, w, bb, 0, 32)[odd]).to(dev)
+                check(torch.equal(h, r[od]), f"scenario {sc} {name}: host odd blocks, layer {w}")
+            st = mgr.engine_stats()
+            path = "+".join(k for k in ("direct", "staged", "zero_copy")
+                            if st.get(f"{k}_copies", 0)) or "none"
+            pub_h2d, pub_d2h = REFERENCE_SCENARIO_GBPS[sc][name]
+            r = {"bytes_per_copy": moved, "d2h_gbps": round(moved / t_d2h / 1e9, 2),
+                 "h2d_gbps": round(moved / t_h2d / 1e9, 2), "path": path,
+                 "reference_per_chip_d2h_gbps": round(pub_d2h / 8, 2),
+                 "reference_per_chip_h2d_gbps": round(pub_h2d / 8, 2)}
+            if peaks:
+                r["d2h_frac_of_pcie_d2h"] = round(moved / t_d2h / 1e9 / peaks["pcie_d2h_gbps"], 4)
+                r["h2d_frac_of_pcie_h2d"] = round(moved / t_h2d / 1e9 / peaks["pcie_h2d_gbps"], 4)
+            res[name] = r
+            log(f"scenario {sc} {name}: {r}")
+            mgr.close()
+            del tensors
+        out[f"scenario_{sc}"] = res
+    out["verified"] = True
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_configs(torch, pkg, dev, args, rng, peaks):
     configs = {}
     wanted = [c for c in args.configs.split(",") if c]
+    if "scenarios" in wanted:
+        configs["reference_scenarios"] = bench_reference_scenarios(torch, pkg, dev, args, peaks)
     if "fp8" in wanted:
         configs["fp8_kv_scales"] = bench_fp8_scales(torch, pkg, dev, args, rng)
     if "weights" in wanted:
@@ -943,6 +1318,7 @@ def run_configs(torch, pkg, dev, args, rng, peaks):
 def main():
     args = parse_args()
     args.sub_steps = max(1, min(args.steps, 20))
+    args.box_copy_gbps = None  # set once the box copy has been measured
     if args.rocpd_summary:
         rocpd_summary(args.rocpd_summary)
         return
@@ -971,14 +1347,13 @@ def main():
     S = 2 * L
     bb = w["block_tokens"] * w["kv_heads"] * w["head_dim"] * w["dtype_bytes"]
     dev = torch.device("cuda:0")
-    log(f"allocating {S} x {P} x {bb} B pool ({S * P * bb / 2**30:.1f} GiB)")
     gen = torch.Generator(device=dev).manual_seed(0)
-    pools = [torch.randint(-2**31, 2**31 - 1, (P, bb // 4), dtype=torch.int32, device=dev,
-                           generator=gen).view(torch.uint8) for _ in range(S)]
+    log(f"allocating {S} x {P} x {bb} B pool ({S * P * bb / 2**30:.1f} GiB, {args.pool_alloc})")
+    pools = make_pool(torch, dev, gen, S, P, bb, args.pool_alloc)
     torch.cuda.synchronize()
 
-    def make_mgr(mode):
-        return pkg.KVCacheManager(pools, host_blocks_to_allocate=4 * n,
+    def make_mgr(mode, storages=pools, host_blocks=4 * n):
+        return pkg.KVCacheManager(storages, host_blocks_to_allocate=host_blocks,
                                   staging_chunk_bytes=args.chunk_mib << 20,
                                   staging_chunks=args.chunks, profile_kernels=True,
                                   transfer_mode=mode)
@@ -992,18 +1367,21 @@ def main():
     log(f"manager ready (mode {args.mode})")
     rng = np.random.default_rng(0)
     slots = [list(range(k * n, (k + 1) * n)) for k in range(4)]
+    batch = batch_source(rng, P, n)
 
-    def batch():
-        perm = rng.permutation(P)
-        return perm[:n].tolist(), perm[n:2 * n].tolist()
-
+    # The reference's gate: one offload + reload with the same manager,
+    # checked before anything is timed.
+    ids0, free0 = batch()
+    verify_round_trip(torch, mgr, pools, ids0, slots[0], free0)
     step_bytes = 2 * n * S * bb
     log(f"timing {args.steps} offload+reload steps")
-    elapsed = run_duplex(torch, mgr, batch, slots, args.steps, args.warmup)
+    elapsed, last = run_duplex(torch, mgr, batch, slots, args.steps, args.warmup)
     value = args.steps * step_bytes / elapsed / 1e9
     stats = mgr.engine_stats()
     log(f"offload+reload: {value:.2f} GB/s, {elapsed / args.steps * 1e3:.2f} ms/step "
         f"({stats})")
+    verify_duplex(torch, mgr, pools, slots, last)
+    log("last step's offload and reload verified")
     # What the headline copies actually did (the auto mode decides per copy).
     kinds = {"staged": stats["staged_copies"], "zero_copy": stats["zero_copy_copies"],
              "direct": stats["direct_copies"]}
@@ -1033,41 +1411,106 @@ def main():
     # launches are reported separately.
     log("timing the gather/scatter kernels alone")
     staging = torch.empty(n * S * bb, dtype=torch.uint8, device=dev)
+    copy_dst = torch.empty_like(staging)
     ks_stream = torch.cuda.Stream(dev)
+    # The box's streaming-copy yardstick, same bytes per launch.
+    staging.random_(0, 256)
+    torch.cuda.synchronize()
+    args.box_copy_gbps = box_copy(torch, pkg, staging, copy_dst, max(5, args.sub_steps),
+                                  ks_stream)
+    log(f"box copy (strided kernel, one contiguous {staging.numel() >> 20} MiB entry): "
+        f"{args.box_copy_gbps:.0f} GB/s")
     # A fresh batch of random ids for each launch (16 in rotation): repeating
     # one batch keeps its pages' translations warm (gather +0.7 points).
     id_sets = [batch()[0] for _ in range(16)]
-    iso = {}
-    for name, fn in (("gather", mgr.gather), ("scatter", mgr.scatter)):
+    gen_c = np.random.default_rng(5)
+    contig_sets = [list(range(s0, s0 + n)) for s0 in gen_c.integers(0, P - n, 16)]
+
+    def time_kernel(m, gather, idsets, launches):
+        fn = m.gather if gather else m.scatter
         for _ in range(2):
-            fn(id_sets[0], staging, stream=ks_stream).Await()
+            fn(idsets[0], staging, stream=ks_stream).Await()
         # The engine brackets each launch with HIP events on ks_stream (the
         # stream the kernel runs on); the id-table upload before it is not
         # inside the bracket.
-        mgr.kernel_times(name == "gather", reset=True)
-        futs = [fn(id_sets[k % 16], staging, stream=ks_stream) for k in range(args.steps)]
+        m.kernel_times(gather, reset=True)
+        futs = [fn(idsets[k % len(idsets)], staging, stream=ks_stream) for k in range(launches)]
         for f in futs:
             f.Await()
-        kt = mgr.kernel_times(name == "gather", reset=True)
-        avg_s = kt["total_ms"] / kt["launches"] / 1e3
-        per_launch = kt["bytes"] / kt["launches"]
-        assert per_launch == 2 * n * S * bb
+        kt = m.kernel_times(gather, reset=True)
+        check(kt["bytes"] / kt["launches"] == 2 * n * S * bb, "bytes per launch")
+        return kt["total_ms"] / kt["launches"] / 1e3, idsets[(launches - 1) % len(idsets)]
+
+    def verify_kernel(storages, gather, ids):
+        torch.cuda.synchronize()
+        ids_t = torch.tensor(ids, device=dev)
+        stg = staging.view(S, n, bb)
+        for w_, t in enumerate(storages):
+            check(torch.equal(t[ids_t], stg[w_]), f"{'gather' if gather else 'scatter'}, "
+                                                   f"storage {w_}")
+
+    iso = {}
+    for name, idsets in (("gather", id_sets), ("scatter", id_sets),
+                         ("scatter_contiguous", contig_sets)):
+        gather = name == "gather"
+        avg_s, last_ids = time_kernel(mgr, gather, idsets, args.steps)
+        verify_kernel(pools, gather, last_ids)
+        per_launch = 2 * n * S * bb
         ach = per_launch / avg_s / 1e9
+        what = ("a fresh contiguous run of ids per launch" if name == "scatter_contiguous"
+                else "a fresh random id batch per launch")
         iso[name] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                     "frac_of_box_copy": frac_of_box(ach, args.box_copy_gbps),
                      "traffic": MEASURED_TRAFFIC.get((name, per_launch)),
-                     "kernel": f"block_copy_fast_kernel ({name}), {n} random ids x {S} storages "
-                               "per launch, a fresh id batch per launch",
-                     "launches": kt["launches"], "avg_launch_us": round(avg_s * 1e6, 2),
-                     "bytes_per_launch": int(per_launch)}
-        log(f"{name} alone: {ach:.0f} GB/s ({ach / HBM_PEAK_GBPS:.1%} of HBM peak)")
-    # A plain device copy of the same byte count: the measured copy ceiling,
-    # and the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters.
-    copy_dst = torch.empty_like(staging)
+                     "kernel": f"block_copy_fast_kernel ({name.split('_')[0]}), {n} ids x {S} "
+                               f"storages per launch, {what}",
+                     "launches": args.steps, "avg_launch_us": round(avg_s * 1e6, 2),
+                     "bytes_per_launch": int(per_launch), "verified": True}
+        log(f"{name} alone: {ach:.0f} GB/s ({ach / HBM_PEAK_GBPS:.1%} of HBM peak, "
+            f"{ach / args.box_copy_gbps:.1%} of the box copy)")
+    # A plain runtime device copy of the same byte count (the runtime's blit
+    # kernel), and the calibration kernel for the FETCH_SIZE / WRITE_SIZE
+    # counters.
     t_copy = timed_events(torch, lambda: copy_dst.copy_(staging), max(3, args.sub_steps // 4),
                           ks_stream)
     hbm_copy_gbps = 2 * staging.numel() / t_copy / 1e9
-    log(f"plain device copy of {staging.numel() >> 20} MiB: {hbm_copy_gbps:.0f} GB/s")
+    log(f"runtime device copy of {staging.numel() >> 20} MiB: {hbm_copy_gbps:.0f} GB/s")
+
+    # Placement: the same kernels over a pool allocated the other way (one
+    # buffer sliced per storage, or one allocation per storage), alternating
+    # with the headline pool in this process.
+    placement = None
+    if args.placement_rounds > 0:
+        other = "per_storage" if args.pool_alloc == "single" else "single"
+        log(f"placement: allocating the pool as {other}")
+        pools2 = make_pool(torch, dev, gen, S, P, bb, other)
+        mgr2 = make_mgr(args.mode, storages=pools2, host_blocks=8)
+        pm = {args.pool_alloc: (mgr, pools), other: (mgr2, pools2)}
+        res = {k: {"gather": [], "scatter": [], "scatter_contiguous": []} for k in pm}
+        for r in range(args.placement_rounds):
+            for k in (list(pm) if r % 2 == 0 else list(pm)[::-1]):
+                m, st = pm[k]
+                for name, idsets in (("gather", id_sets), ("scatter", id_sets),
+                                     ("scatter_contiguous", contig_sets)):
+                    avg_s, last_ids = time_kernel(m, name == "gather", idsets, args.sub_steps)
+                    res[k][name].append(avg_s)
+                    if r == 0:
+                        verify_kernel(st, name == "gather", last_ids)
+        placement = {"rounds": args.placement_rounds, "launches_per_round": args.sub_steps,
+                     "note": "median launch time per kernel, rounds alternating between the "
+                             "two pools in one process"}
+        for k, kinds_ in res.items():
+            placement[k] = {}
+            for name, xs in kinds_.items():
+                med = float(np.median(xs))
+                g_ = 2 * n * S * bb / med / 1e9
+                placement[k][name] = {"avg_launch_us": round(med * 1e6, 2),
+                                      "frac": round(g_ / HBM_PEAK_GBPS, 4),
+                                      "frac_of_box_copy": frac_of_box(g_, args.box_copy_gbps)}
+        log(f"placement: {placement}")
+        mgr2.close()
+        del pools2, mgr2, pm
     del staging, copy_dst
     mgr.kernel_times(True, reset=True)
     mgr.kernel_times(False, reset=True)
@@ -1082,8 +1525,11 @@ def main():
             m = mgr if mode == args.mode else make_mgr(mode)
             t_off, t_rel = one_direction(m, batch, slots, reps)
             el_steps = args.steps if m is mgr else args.sub_steps
-            el = elapsed if m is mgr else run_duplex(torch, m, batch, slots, el_steps,
-                                                      args.warmup)
+            if m is mgr:
+                el = elapsed
+            else:
+                el, last_m = run_duplex(torch, m, batch, slots, el_steps, args.warmup)
+                verify_duplex(torch, m, pools, slots, last_m)
             modes[mode] = {"duplex_gbps": round(el_steps * step_bytes / el / 1e9, 2),
                            "offload_gbps": round(half / t_off / 1e9, 2),
                            "reload_gbps": round(half / t_rel / 1e9, 2)}
@@ -1139,15 +1585,22 @@ def main():
             "block_tokens": w["block_tokens"], "kv_dtype": w["dtype"], "storages": S,
             "block_bytes": bb, "pool_blocks": P, "batch_blocks": n,
             "transfer_mode": args.mode, "staging_chunk_mib": args.chunk_mib,
+            "pool_allocation": POOL_ALLOC_TEXT[args.pool_alloc],
         },
         "blocks_per_s": round(args.steps * 2 * n / elapsed, 1),
+        "verified": True,
         "headline_path": headline_path,
         "roofline": iso["gather"],
         "scatter_roofline": iso["scatter"],
+        "scatter_contiguous": iso["scatter_contiguous"],
+        "box_copy": {"kernel": "strided_copy_kernel over one contiguous entry of the same "
+                               "bytes (2 workgroups per CU), HIP events on its stream",
+                     "achieved": round(args.box_copy_gbps, 1),
+                     "frac": round(args.box_copy_gbps / HBM_PEAK_GBPS, 4), "verified": True},
+        "placement": placement,
         "loop_gather": loop_gather,
         "loop_scatter": loop_scatter,
         "hbm_copy_same_bytes_gbps": round(hbm_copy_gbps, 1),
-        "gather_frac_of_measured_copy": round(iso["gather"]["achieved"] / hbm_copy_gbps, 4),
         "cpu_baseline": cpu,
         "host": host_info,
         **extras,
