@@ -8,6 +8,7 @@
 #include <string>
 #include <vector>
 
+#include "../host/device_memory.h"
 #include "../host/hip_util.h"
 #include "../host/kv_cache_store.h"
 #include "../host/numa.h"
@@ -184,6 +185,15 @@ int kvx_manager_create(const kvx_manager_config* cfg, kvx_manager** out) {
   }
   const bool device_backed = cfg->device_ptrs != nullptr;
   const int device = c.device;
+  // Every storage must be device memory of cfg->device covering its bytes
+  // (checked before anything is allocated or issued).
+  kvx::DeviceRangeChecker ranges(device);
+  for (size_t k = 0; k < c.device_ptrs.size(); ++k) {
+    if (c.device_bytes[k] < 0) return Fail(KVX_INVALID_ARGUMENT, "negative device_bytes");
+    kvx::Status st = ranges.Check(c.device_ptrs[k], static_cast<uint64_t>(c.device_bytes[k]),
+                                  ("device_ptrs[" + std::to_string(k) + "]").c_str());
+    if (!st.ok()) return Fail(st);
+  }
   auto r = kvx::KVCacheManager::Create(std::move(c));
   if (!r.ok()) return Fail(r.status());
   if (device_backed) {
@@ -320,6 +330,10 @@ static int DeviceCopy(bool gather, kvx_manager* m, const int64_t* ids,
   if (order != KVX_LAYER_MAJOR && order != KVX_BLOCK_MAJOR) {
     return Fail(KVX_INVALID_ARGUMENT, "unknown staging order");
   }
+  if (staging_bytes < 0) return Fail(KVX_INVALID_ARGUMENT, "negative staging_bytes");
+  kvx::Status chk = kvx::CheckDeviceRange(m->impl->device(), staging,
+                                          static_cast<uint64_t>(staging_bytes), "staging");
+  if (!chk.ok()) return Fail(chk);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto v = Vec(ids, n);
   auto r = gather ? m->impl->Gather(v, staging, staging_bytes, order == KVX_BLOCK_MAJOR,
@@ -656,6 +670,19 @@ static int RawCopy(bool gather, uint64_t storage_table, int64_t num_storages,
       static_cast<uint64_t>(num_storages) > UINT32_MAX / static_cast<uint64_t>(n)) {
     return Fail(KVX_INVALID_ARGUMENT, "too many blocks for one launch");
   }
+  // Every table and buffer on one device (the storage bases inside the
+  // table are device data the host does not read).
+  kvx::DeviceRangeChecker ranges(-1);
+  const uint64_t W = static_cast<uint64_t>(num_storages), N = static_cast<uint64_t>(n);
+  uint64_t staging_bytes = 0;
+  if (__builtin_mul_overflow(W * N, static_cast<uint64_t>(block_bytes), &staging_bytes)) {
+    return Fail(KVX_INVALID_ARGUMENT, "staging size overflows");
+  }
+  kvx::Status chk = ranges.Check(storage_table, W * 8, "storage_table");
+  if (chk.ok()) chk = ranges.Check(ids, N * 8, "ids");
+  if (chk.ok()) chk = ranges.Check(staging, staging_bytes, "staging");
+  if (chk.ok()) chk = ranges.Check(error, error != 0 ? 4 : 0, "error");
+  if (!chk.ok()) return Fail(chk);
   kvx::CopyLaunch l;
   l.npieces = 1;
   l.ids = reinterpret_cast<const int64_t*>(ids);

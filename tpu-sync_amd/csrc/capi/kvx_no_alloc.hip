@@ -24,6 +24,7 @@
 #include <mutex>
 #include <string>
 
+#include "../host/device_memory.h"
 #include "../host/hip_util.h"
 #include "../kernels/block_copy.h"
 #include "capi_internal.h"
@@ -217,6 +218,10 @@ extern "C" int kvx_manager_gather_no_alloc(kvx_manager* m, const int64_t* ids, i
   if (order == KVX_BLOCK_MAJOR && ngroups != 1) {
     return Fail(KVX_INVALID_ARGUMENT, "block-major staging needs one block size");
   }
+  // The bytes this gather writes must be device memory of the manager's
+  // device (a runtime lookup: it allocates nothing).
+  Status chk = CheckDeviceRange(device, staging, static_cast<uint64_t>(need), "staging");
+  if (!chk.ok()) return Fail(chk);
 
   DeviceGuard dg(device);
   if (!dg.ok()) return Fail(KVX_INTERNAL, "hipSetDevice failed");

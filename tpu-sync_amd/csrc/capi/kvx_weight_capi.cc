@@ -1,7 +1,10 @@
 // extern "C" layer over the weight synchronizer and the strided-entry copy.
+#include <algorithm>
 #include <memory>
+#include <string>
 #include <vector>
 
+#include "../host/device_memory.h"
 #include "../host/weight_synchronizer.h"
 #include "capi_internal.h"
 
@@ -25,9 +28,12 @@ int Emit(kvx::StatusOr<kvx::CopyFuture> r, kvx_future** out) {
   return KVX_OK;
 }
 
-// Validates the C entries and converts them (offsets folded into addresses).
-int ToCopies(const kvx_strided_entry* entries, int64_t n, std::vector<kvx::StridedCopy>* out) {
+// Validates the C entries and converts them (offsets folded into addresses):
+// every row an entry reads or writes must lie in device memory of `device`.
+int ToCopies(int32_t device, const kvx_strided_entry* entries, int64_t n,
+             std::vector<kvx::StridedCopy>* out) {
   if (BadArray(entries, n)) return Fail(KVX_INVALID_ARGUMENT, "bad arguments");
+  kvx::DeviceRangeChecker ranges(device);
   out->assign(static_cast<size_t>(n), kvx::StridedCopy{});
   for (int64_t i = 0; i < n; ++i) {
     const kvx_strided_entry& e = entries[i];
@@ -46,6 +52,16 @@ int ToCopies(const kvx_strided_entry* entries, int64_t n, std::vector<kvx::Strid
     c.count = count;
     c.src_stride = e.src_stride_bytes;
     c.dst_stride = e.dst_stride_bytes;
+    uint64_t src_bytes = 0, dst_bytes = 0;
+    if (!kvx::StridedExtent(c.size, count, c.src_stride, &src_bytes) ||
+        !kvx::StridedExtent(c.size, count, c.dst_stride, &dst_bytes)) {
+      return Fail(KVX_INVALID_ARGUMENT, "entry extent overflows");
+    }
+    kvx::Status st = ranges.Check(c.src, src_bytes, "strided entry source");
+    if (st.ok()) st = ranges.Check(c.dst, dst_bytes, "strided entry destination");
+    if (!st.ok()) {
+      return Fail(kvx::InvalidArgumentError("entry " + std::to_string(i) + ": " + st.message()));
+    }
   }
   return KVX_OK;
 }
@@ -71,6 +87,16 @@ int ToLayout(const kvx_tiled_layout* l, kvx::TiledLayout* out) {
   return KVX_OK;
 }
 
+// The packed image a Pack writes / an Unpack reads must be device memory of
+// the synchronizer's device.
+int CheckStaging(const kvx::WeightSynchronizer& w, uint64_t staging, int64_t staging_bytes) {
+  if (staging_bytes < 0) return Fail(KVX_INVALID_ARGUMENT, "negative staging_bytes");
+  const int64_t used = std::min<int64_t>(staging_bytes, w.total_bytes());
+  kvx::Status st = kvx::CheckDeviceRange(w.device(), staging, static_cast<uint64_t>(used),
+                                         "staging");
+  return st.ok() ? KVX_OK : Fail(st);
+}
+
 int TileCall(int32_t device, const kvx_tiled_layout* layout, uint64_t linear, uint64_t tiled,
              bool tile, void* stream, kvx_future** out) {
   if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
@@ -79,6 +105,16 @@ int TileCall(int32_t device, const kvx_tiled_layout* layout, uint64_t linear, ui
   if (rc != KVX_OK) return rc;
   auto plan = kvx::PlanTiled(l);
   if (!plan.ok()) return Fail(plan.status());
+  // Both buffers are device memory (the reference's TileBuffer / DetileBuffer
+  // take host buffers; these run in HBM).
+  kvx::DeviceRangeChecker ranges(device);
+  kvx::Status st = ranges.Check(linear, static_cast<uint64_t>(plan->logical_bytes),
+                                tile ? "src_linear" : "dst_linear");
+  if (st.ok()) {
+    st = ranges.Check(tiled, static_cast<uint64_t>(plan->tiled_bytes),
+                      tile ? "dst_tiled" : "src_tiled");
+  }
+  if (!st.ok()) return Fail(st);
   return Emit(kvx::TileOnDevice(device, plan.value(), linear, tiled, tile,
                                 static_cast<hipStream_t>(stream)),
               out);
@@ -125,6 +161,13 @@ int kvx_weight_sync_create(const kvx_weight_sync_config* cfg, kvx_weight_sync** 
   c.num_shards = cfg->num_shards;
   c.device_ptrs.assign(cfg->device_ptrs, cfg->device_ptrs + n);
   c.device_bytes.assign(cfg->device_bytes, cfg->device_bytes + n);
+  kvx::DeviceRangeChecker ranges(cfg->device);
+  for (int64_t k = 0; k < n; ++k) {
+    if (c.device_bytes[k] < 0) return Fail(KVX_INVALID_ARGUMENT, "negative device_bytes");
+    kvx::Status st = ranges.Check(c.device_ptrs[k], static_cast<uint64_t>(c.device_bytes[k]),
+                                  ("device_ptrs[" + std::to_string(k) + "]").c_str());
+    if (!st.ok()) return Fail(st);
+  }
   if (cfg->host_alloc != KVX_HOST_PINNED && cfg->host_alloc != KVX_HOST_MALLOC) {
     return Fail(KVX_INVALID_ARGUMENT, "weight sync host memory must be pinned or malloc");
   }
@@ -179,12 +222,14 @@ int kvx_weight_sync_h2d_layer(kvx_weight_sync* w, int64_t layer, void* stream,
 int kvx_weight_sync_pack(kvx_weight_sync* w, uint64_t staging, int64_t staging_bytes,
                          void* stream, kvx_future** out) {
   if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  if (const int rc = CheckStaging(*w->impl, staging, staging_bytes); rc != KVX_OK) return rc;
   return Emit(w->impl->Pack(staging, staging_bytes, static_cast<hipStream_t>(stream)), out);
 }
 
 int kvx_weight_sync_unpack(kvx_weight_sync* w, uint64_t staging, int64_t staging_bytes,
                            void* stream, kvx_future** out) {
   if (w == nullptr || out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  if (const int rc = CheckStaging(*w->impl, staging, staging_bytes); rc != KVX_OK) return rc;
   return Emit(w->impl->Unpack(staging, staging_bytes, static_cast<hipStream_t>(stream)), out);
 }
 
@@ -228,7 +273,7 @@ int kvx_copy_strided(int32_t device, const kvx_strided_entry* entries, int64_t n
                      void* stream, kvx_future** out) {
   if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "bad arguments");
   std::vector<kvx::StridedCopy> copies;
-  const int rc = ToCopies(entries, n, &copies);
+  const int rc = ToCopies(device, entries, n, &copies);
   if (rc != KVX_OK) return rc;
   return Emit(kvx::CopyStridedOnDevice(device, copies, static_cast<hipStream_t>(stream)), out);
 }
@@ -238,7 +283,7 @@ int kvx_strided_plan_create(int32_t device, const kvx_strided_entry* entries, in
   if (out == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
   *out = nullptr;
   std::vector<kvx::StridedCopy> copies;
-  const int rc = ToCopies(entries, n, &copies);
+  const int rc = ToCopies(device, entries, n, &copies);
   if (rc != KVX_OK) return rc;
   auto p = kvx::StridedCopyPlan::Create(device, copies);
   if (!p.ok()) return Fail(p.status());

@@ -81,6 +81,7 @@ class WeightSynchronizer {
   int64_t num_layers() const { return cfg_.num_layers; }
   int64_t num_shards() const { return cfg_.num_shards; }
   int64_t total_bytes() const { return total_; }
+  int device() const { return cfg_.device; }
   int64_t offset(int64_t layer, int64_t shard) const { return off_[layer * cfg_.num_shards + shard]; }
   // Bytes of one tensor's host copy (the linear image of a tiled tensor).
   int64_t size(int64_t layer, int64_t shard) const { return host_bytes_[layer * cfg_.num_shards + shard]; }
