@@ -14,6 +14,11 @@ through candidates and the LRU tail (kv_cache_store.cc:1743-1781,
 lru_cache.h:260); hashes demoted to candidates and requested again are
 saved again.
 
+The test runs on a pinned tier and on a /dev/shm tier, the second with the
+benchmark's 32 MiB staging chunks, so its copies take the pageable bounce
+lanes (host threads between the segment and pinned bounce buffers, SDMA
+between those and device staging) that the benchmark's churn measures.
+
 Checks, against device-side copies taken with torch (not the library):
   * every block a load places equals, in all 160 storages, the bytes its
     hash had on the device when it was saved;
@@ -22,6 +27,8 @@ Checks, against device-side copies taken with torch (not the library):
     (storage, block), taken before the run) or the bytes of the last hash
     loaded into it.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -54,7 +61,8 @@ def _poll(fn, want, what):
     raise AssertionError(f"{what}: {len(got)} of {want} done")
 
 
-def test_llama70b_prefix_cache_churn_bytes(kvx, cuda):
+@pytest.mark.parametrize("host_alloc", ["pinned", "shm"])
+def test_llama70b_prefix_cache_churn_bytes(kvx, cuda, host_alloc):
     rng = np.random.default_rng(2024)
     gen = torch.Generator(device=cuda).manual_seed(7)
     print(f"allocating {S} x {P} x {BB} B pool", flush=True)
@@ -65,9 +73,14 @@ def test_llama70b_prefix_cache_churn_bytes(kvx, cuda):
     initial = _fingerprints(pools, weights)
     store = kvx.KVCacheStore(capacity=HOST_BLOCKS, num_shards=1, store_server_ip="127.0.0.1",
                              metadata_shm_key="")
+    tier = {}
+    if host_alloc == "shm":
+        tier = dict(host_alloc="shm", shm_key=f"kvx_test_churn_{os.getpid()}",
+                    staging_chunk_bytes=32 << 20, staging_chunks=4)
     mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=HOST_BLOCKS,
-                             raiden_controller_address=store.raiden_controller_address)
-    assert mgr.host_alloc == "pinned"
+                             raiden_controller_address=store.raiden_controller_address,
+                             **tier)
+    assert mgr.host_alloc == host_alloc
     rid = store.raiden_id
     on_host = (kvx.BlockStatus.HOST, kvx.BlockStatus.HOST_AND_HBM)
     w = 1.0 / np.arange(1, DOCS + 1) ** 1.1
@@ -153,7 +166,15 @@ def test_llama70b_prefix_cache_churn_bytes(kvx, cuda):
         check(blocks, [last_loaded[d] for d in blocks], "final state")
     print(f"saves {saves}, loads {loads}, evicted {evicted}, candidates re-saved "
           f"{recycled}, blocks loaded into {len(last_loaded)}", flush=True)
+    if host_alloc == "shm":
+        # Every copy of the shm tier went through the bounce lanes.
+        st = mgr.engine_stats()
+        assert st["bounce_copies"] > 0 and st["bounce_copies"] == st["staged_copies"], st
     mgr.close()
     store.close()
+    if tier:
+        seg = f"/dev/shm/{tier['shm_key']}_dev_{cuda.index or 0}"
+        if os.path.exists(seg):
+            os.unlink(seg)
     del snaps, pools
     torch.cuda.empty_cache()
