@@ -222,8 +222,12 @@ int kvx_manager_scatter(kvx_manager* m, const int64_t* ids, int64_t n,
  * (KVX_NO_ALLOC_MAX_IDS + 32 + KVX_NO_ALLOC_MAX_STORAGES) x 8 bytes
  * (160.25 KiB) instead of the library's argument ring; larger calls are
  * rejected with KVX_INVALID_ARGUMENT. The host ids are consumed before the
- * call returns. Every call on one GPU shares that array: calls that overlap
- * on one GPU (different streams or unordered threads) race.
+ * call returns. Every call on one GPU shares that array, so calls on one GPU
+ * are ordered: a call on another stream than the previous call's first makes
+ * its stream wait (on the GPU, through a per-device event created at set-up)
+ * until the previous call's gather has read the array; calls from several
+ * host threads are issued one at a time. Calls on one stream wait for
+ * nothing beyond the stream's order.
  */
 #define KVX_NO_ALLOC_MAX_IDS 16384
 #define KVX_NO_ALLOC_MAX_STORAGES 4096

@@ -2,10 +2,13 @@
 no allocation) against kvx_manager_gather (tables in the library's argument
 ring) through the C-ABI: identical staging bytes for the same ids, two calls
 in a row on one stream (the second smaller, so it reuses the array the first
-one filled), every staging order and restriction, two block sizes in one
-launch (fp8 payload + scales), the size limits and the id checks.
+one filled), calls back to back on two streams and from two host threads
+(ordered on the GPU through the per-device event), every staging order and
+restriction, two block sizes in one launch (fp8 payload + scales), the size
+limits and the id checks.
 """
 import ctypes
+import threading
 
 import numpy as np
 import pytest
@@ -76,6 +79,55 @@ def test_no_alloc_matches_gather_two_calls(kvx, cuda, order, layer, shard):
     g2 = _bytes(got2)
     assert np.array_equal(g2[:want2.numel()], _bytes(want2))
     assert (g2[want2.numel():] == 0x5A).all()
+    mgr.close()
+
+
+def test_no_alloc_two_streams_and_threads_are_ordered(kvx, cuda):
+    """Calls alternating between two streams with no host wait, then two host
+    threads issuing on their own streams at once: each gather moves 2 GiB, so
+    a later call's fills would overwrite the shared array while an earlier
+    gather still reads it unless the calls are ordered. Every output must
+    equal kvx_manager_gather's for its ids."""
+    gen = torch.Generator(device=cuda).manual_seed(90)
+    W, blocks, bb, n = 16, 8192, 32768, 4096
+    pools = [torch.randint(0, 256, (blocks, bb), dtype=torch.uint8, device=cuda, generator=gen)
+             for _ in range(W)]
+    mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=4)
+    streams = [torch.cuda.Stream(cuda) for _ in range(2)]
+    rng = np.random.default_rng(91)
+    id_sets = [rng.choice(blocks, n, replace=False) for _ in range(4)]
+    want = []
+    for ids in id_sets:
+        w = torch.zeros(W * n * bb, dtype=torch.uint8, device=cuda)
+        _existing(kvx, mgr, ids, w, 0, -1, -1, streams[0])
+        want.append(w)
+    got = [torch.full((W * n * bb,), 0x5A, dtype=torch.uint8, device=cuda) for _ in range(4)]
+    torch.cuda.synchronize()
+    print("no-alloc: 4 calls alternating between 2 streams", flush=True)
+    for k in range(4):
+        assert _no_alloc(kvx, mgr, id_sets[k], got[k], 0, -1, -1, streams[k % 2]) == 0
+    torch.cuda.synchronize()
+    for k in range(4):
+        assert torch.equal(got[k], want[k]), k
+    print("no-alloc: 2 host threads, 2 calls each", flush=True)
+    for g in got:
+        g.fill_(0x5A)
+    torch.cuda.synchronize()
+    rcs = []
+
+    def issue(t):
+        for k in (t, t + 2):
+            rcs.append(_no_alloc(kvx, mgr, id_sets[k], got[k], 0, -1, -1, streams[t]))
+
+    threads = [threading.Thread(target=issue, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert rcs == [0, 0, 0, 0]
+    for k in range(4):
+        assert torch.equal(got[k], want[k]), k
     mgr.close()
 
 

@@ -12,10 +12,15 @@
 // returns. Every launch goes on the caller's stream, in order.
 //
 // `scratch` is one array per GPU, shared by every call on that GPU, and it
-// keeps the last call's contents. Calls that overlap on one GPU (different
-// streams, or different host threads with no ordering between them) race on
-// it. Every word a call reads is written by the same call first, so nothing
-// needs clearing.
+// keeps the last call's contents. Every word a call reads is written by the
+// same call first, so nothing needs clearing. Calls on one GPU are ordered:
+// each records a per-device event after its last launch, and a call on
+// another stream first makes its stream wait for that event, so its fills
+// overwrite `scratch` only after the previous call's gather has read it
+// (the event is created at set-up: a call allocates nothing). A per-device
+// mutex keeps one call's wait, fills, launches and record together when
+// host threads call at once. Calls on one stream are ordered by the stream
+// and wait for nothing else.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -57,6 +62,17 @@ __global__ __launch_bounds__(kFillWords) void scratch_fill_kernel(FillArgs a, ui
 // Device address of `scratch` per device ordinal (0 = not looked up yet).
 std::atomic<uint64_t> g_scratch_addr[kMaxDevices];
 std::mutex g_scratch_mu;
+
+// Per device: the event recorded after each call's last launch and the
+// stream it was recorded on (the event lives as long as the process, like
+// `scratch`).
+struct CallOrder {
+  std::mutex mu;
+  hipEvent_t last = nullptr;
+  hipStream_t stream = nullptr;
+  bool recorded = false;
+};
+CallOrder g_order[kMaxDevices];
 
 // Streams words into scratch[first..) through fill launches on `stream`.
 class ScratchWriter {
@@ -101,6 +117,13 @@ Status InitNoAllocScratch(int device) {
   }
   std::lock_guard<std::mutex> l(g_scratch_mu);
   if (g_scratch_addr[device].load(std::memory_order_acquire) != 0) return OkStatus();
+  {
+    std::lock_guard<std::mutex> o(g_order[device].mu);
+    if (g_order[device].last == nullptr) {
+      KVX_HIP_RETURN_IF_ERROR(
+          hipEventCreateWithFlags(&g_order[device].last, hipEventDisableTiming));
+    }
+  }
   void* ptr = nullptr;
   KVX_HIP_RETURN_IF_ERROR(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
   if (ptr == nullptr) return InternalError("hipGetSymbolAddress(scratch) returned null");
@@ -226,8 +249,28 @@ extern "C" int kvx_manager_gather_no_alloc(kvx_manager* m, const int64_t* ids, i
   DeviceGuard dg(device);
   if (!dg.ok()) return Fail(KVX_INTERNAL, "hipSetDevice failed");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  ScratchWriter wr(scratch_addr, st);
+  CallOrder& ord = g_order[device];
+  std::lock_guard<std::mutex> order_lock(ord.mu);
+  if (ord.last == nullptr) return Fail(KVX_INTERNAL, "no-alloc ordering event was not set up");
   hipError_t e = hipSuccess;
+  if (ord.recorded && ord.stream != st) e = hipStreamWaitEvent(st, ord.last, 0);
+  if (e != hipSuccess) {
+    return Fail(KVX_INTERNAL, (std::string("stream wait failed: ") +
+                               hipGetErrorString(e)).c_str());
+  }
+  // Whatever this call launches, the next call on another stream waits for
+  // it (also after a failed launch, whose fills may have run).
+  struct RecordOnExit {
+    CallOrder& o;
+    hipStream_t s;
+    ~RecordOnExit() {
+      if (hipEventRecord(o.last, s) == hipSuccess) {
+        o.stream = s;
+        o.recorded = true;
+      }
+    }
+  } record_on_exit{ord, st};
+  ScratchWriter wr(scratch_addr, st);
   for (int64_t i = 0; i < n && e == hipSuccess; ++i) e = wr.Push(static_cast<uint64_t>(ids[i]));
   const uint64_t table0 = (static_cast<uint64_t>(n) + 31) / 32 * 32;
   if (e == hipSuccess) e = wr.SkipTo(table0);
