@@ -743,6 +743,60 @@ def test_bounce_lanes_overlap_and_drain(kvx, oracle, cuda, threads, alloc):
                 os.unlink(os.path.join("/dev/shm", name))
 
 
+def test_auto_duplex_short_runs_take_the_lanes(kvx, oracle, cuda):
+    """Auto mode on a pinned mirror with single-block host runs: a lone copy
+    goes zero-copy; a save issued while a load is in flight goes through the
+    lanes, and so do both copies of the next load + save inside the duplex
+    window; after an idle pause longer than the window a lone copy is
+    zero-copy again. Every step's bytes against the oracle."""
+    import time
+    rng = np.random.default_rng(77)
+    layers, blocks, hb, bb, n = 4, 512, 1024, 32768, 256
+    host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
+    mgr = make_mgr(kvx, dev, hb, staging_chunk_bytes=1 << 20, staging_chunks=4,
+                   host_copy_threads=3)
+    mir = Mirror(host, hb)
+
+    def pick():
+        d = rng.permutation(blocks)
+        h = rng.permutation(hb)
+        return d[:n].tolist(), d[n:2 * n].tolist(), h[:n].tolist(), h[n:2 * n].tolist()
+
+    def kinds():
+        st = mgr.engine_stats()
+        return st["zero_copy_copies"], st["bounce_copies"]
+
+    ones = [1] * n
+    d0, _, h0, _ = pick()
+    print("lone offload", flush=True)
+    mgr.d2h(d0, h0, ones).Await()
+    assert mir.transfer(True, d0, h0, ones) == 0
+    assert kinds() == (1, 0)
+    # A load of 32 MiB keeps its kernel busy while the save is issued.
+    for step in range(2):
+        d_load, d_save, h_load, h_save = pick()
+        h_load = h0 if step == 0 else h_load  # the first load reads real bytes
+        print(f"load + save {step}", flush=True)
+        f1 = mgr.h2d(h_load, d_load, ones)
+        f2 = mgr.d2h(d_save, h_save, ones)
+        f1.Await()
+        f2.Await()
+        assert mir.transfer(False, h_load, d_load, ones) == 0
+        assert mir.transfer(True, d_save, h_save, ones) == 0
+        mir.check(mgr, dev)
+    zc, lanes = kinds()
+    # The first load was lone (zero-copy); its save and the second pair rode the lanes.
+    assert zc == 2 and lanes == 3, (zc, lanes)
+    time.sleep(0.4)
+    d1, _, h1, _ = pick()
+    print("lone offload after a pause", flush=True)
+    mgr.d2h(d1, h1, ones).Await()
+    assert mir.transfer(True, d1, h1, ones) == 0
+    mir.check(mgr, dev)
+    assert kinds() == (3, 3)
+    mgr.close()
+
+
 def test_zero_copy_needs_pinned_host(kvx, cuda):
     t = torch.zeros(4, 256, dtype=torch.uint8, device=cuda)
     with pytest.raises(kvx.KvxError) as e:

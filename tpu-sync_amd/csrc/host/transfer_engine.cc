@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <cstring>
 #include <numeric>
@@ -465,10 +466,53 @@ Status TransferEngine::WaitDep(hipStream_t dep, hipStream_t on) {
   return st;
 }
 
+namespace {
+
+int64_t NowUs() {
+  return std::chrono::duration_cast<std::chrono::microseconds>(
+             std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+
+}  // namespace
+
+bool TransferEngine::DuplexNow(Direction dir) {
+  if (opts_.auto_duplex_window_us <= 0) return false;
+  std::lock_guard<std::mutex> l(duplex_mu_);
+  std::deque<CopyFuture>& other = recent_[1 - static_cast<int>(dir)];
+  while (!other.empty() && other.front().IsReady()) other.pop_front();
+  const int64_t now = NowUs();
+  if (!other.empty()) last_duplex_us_ = now;
+  return now - last_duplex_us_ < opts_.auto_duplex_window_us;
+}
+
+void TransferEngine::NoteIssued(Direction dir, const CopyFuture& f) {
+  if (opts_.auto_duplex_window_us <= 0) return;
+  std::lock_guard<std::mutex> l(duplex_mu_);
+  std::deque<CopyFuture>& q = recent_[static_cast<int>(dir)];
+  while (!q.empty() && q.front().IsReady()) q.pop_front();
+  q.push_back(f);
+  constexpr size_t kMaxRemembered = 256;
+  if (q.size() > kMaxRemembered) q.pop_front();
+}
+
 StatusOr<CopyFuture> TransferEngine::Copy(
     Direction dir, const std::vector<StorageView>& storages,
     const std::vector<int64_t>& src, const std::vector<int64_t>& dst,
     const std::vector<int64_t>& sizes, hipStream_t dep) {
+  if (opts_.mode != TransferMode::kAuto) {
+    return CopyPath(dir, storages, src, dst, sizes, dep, /*duplex=*/false);
+  }
+  const bool duplex = DuplexNow(dir);
+  StatusOr<CopyFuture> r = CopyPath(dir, storages, src, dst, sizes, dep, duplex);
+  if (r.ok()) NoteIssued(dir, r.value());
+  return r;
+}
+
+StatusOr<CopyFuture> TransferEngine::CopyPath(
+    Direction dir, const std::vector<StorageView>& storages,
+    const std::vector<int64_t>& src, const std::vector<int64_t>& dst,
+    const std::vector<int64_t>& sizes, hipStream_t dep, bool duplex) {
   if (src.size() != dst.size() || src.size() != sizes.size()) {
     return InvalidArgumentError("src, dst and sizes must have the same length");
   }
@@ -528,6 +572,9 @@ StatusOr<CopyFuture> TransferEngine::Copy(
     const int64_t n = static_cast<int64_t>(cdev.size());
     const int64_t chunk = opts_.staging_chunk_bytes;
     bool lanes = per_block > 0 && n > opts_.auto_lanes_min_chunks * chunk / per_block;
+    // Short runs while both directions are at work: the lanes, in both
+    // directions (see EngineOptions::auto_duplex_window_us).
+    if (!lanes && zero_copy && duplex) lanes = true;
     if (!lanes && !zero_copy) {
       const int64_t own = (n * per_block + chunk - 1) / chunk;
       std::lock_guard<std::mutex> l(mu_);

@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <climits>
 #include <cstdint>
 #include <deque>
 #include <functional>
@@ -68,9 +69,10 @@ struct ByteExtent {
 //          storage at least auto_staged_min_run_bytes); zero-copy otherwise;
 //          a copy of more than auto_lanes_min_chunks staging chunks, or a
 //          staged one that would leave more than that many staged chunks of
-//          its direction in flight, goes through the lanes (as kLanes). Host
-//          memory the GPU cannot map always goes staged (through the
-//          pageable lanes).
+//          its direction in flight, goes through the lanes (as kLanes); so
+//          does a short-run copy while the engine sees both directions at
+//          work (auto_duplex_window_us). Host memory the GPU cannot map
+//          always goes staged (through the pageable lanes).
 //   kLanes: pinned host memory too goes through the pageable lanes (host
 //          threads move the host side, whole chunks cross on SDMA): a load
 //          and a save at once reach the link's duplex rate, where zero-copy
@@ -120,6 +122,16 @@ struct EngineOptions {
   // zero-copy paths are as fast or faster (a lone 64-block copy: zero-copy
   // 6.1 ms, lanes 6.5).
   int64_t auto_lanes_min_chunks = 32;
+  // kAuto moves a short-run copy (one that would go zero-copy) through the
+  // lanes, when host_copy_threads > 0, while a copy of the other direction
+  // is in flight or was within this many microseconds of such an overlap
+  // (0: never). Zero-copy kernels in both directions interfere (load + save
+  // of 512 Llama-3-70B blocks each way on a pinned tier: 63-64 ms, against
+  // 56.9 ms through the lanes), while a lone short copy is fastest
+  // zero-copy (64 blocks: 6.05 against 6.5 ms). The window keeps both
+  // directions of a load + save pattern on the same path: a zero-copy save
+  // next to lane loads is the slowest mix of all (94 ms).
+  int64_t auto_duplex_window_us = 250000;
   // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
   // bounce buffers that this many host threads fill and drain, one lane per
   // direction with its own streams, staging ring and SDMA engine (0: leave
@@ -378,6 +390,23 @@ class TransferEngine {
   // Chunks of the direction's staged copies not yet finished (drops the
   // finished ones). Needs mu_.
   int64_t StagedChunksInFlightLocked(Direction dir);
+  // Auto mode's view of both directions (under duplex_mu_): the futures of
+  // its recent copies per direction, finished ones dropped from the front,
+  // and when a copy last found the other direction in flight.
+  std::mutex duplex_mu_;
+  std::deque<CopyFuture> recent_[2];  // by Direction
+  int64_t last_duplex_us_ = INT64_MIN / 2;
+  // Copy() after auto mode's duplex check: picks the path and issues.
+  StatusOr<CopyFuture> CopyPath(Direction dir, const std::vector<StorageView>& storages,
+                                const std::vector<int64_t>& src,
+                                const std::vector<int64_t>& dst,
+                                const std::vector<int64_t>& sizes, hipStream_t dep,
+                                bool duplex);
+  // Whether a copy of `dir` issued now takes the duplex path (and records
+  // an overlap when the other direction is in flight).
+  bool DuplexNow(Direction dir);
+  // Remembers an issued auto-mode copy of `dir`.
+  void NoteIssued(Direction dir, const CopyFuture& f);
 };
 
 }  // namespace kvx
