@@ -303,18 +303,22 @@ Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int6
   // buffers allow less than 4 bytes goes element by element.
   int v = WidestVector(tiled | linear, p.vec);
   // Packed units: one lane per unit with units of one 16-byte tiled vector
-  // (v = 16 / P), except that detiling pairs (P = 2) at 16-byte rows go two
-  // lanes per unit. Measured on the Llama-3-8B set (bf16, P = 2), one
+  // (v = 16 / P), except that detiling at 16-byte rows goes two lanes per
+  // unit for pairs (P = 2) and four for quads (P = 4). Measured on the Llama-3-8B set (bf16, P = 2), one
   // process, one launch each: tiling 79.2 % of HBM peak at v = 8 against
   // 76.7 % with two lanes per 16-byte unit and 67.8 % with one lane per
   // 16-byte unit (each 16-byte tiled store of a wave then leaves 16-byte
   // holes); detiling 77.0 % with two lanes against 75.7 % at v = 8. For
-  // int8 (P = 4) one lane per 16-byte tiled vector: tiling 63.8 %, detiling
-  // 53.7 %, against 38.8 / 39.9 % for four lanes per unit (a 4 x 4 word
-  // transpose through ds_bpermute).
-  bool two_lanes = false;
+  // int8 (P = 4) at 16-byte rows, detiling: four lanes per 64-byte unit
+  // exchanging through LDS (each wave then writes 1 KiB of one row per
+  // store) 71.6 % against 61.8 % for one lane per 16-byte tiled vector;
+  // tiling keeps one lane per tiled vector (72.3 % against 67.0 % through
+  // LDS).
+  bool two_lanes = false, four_lanes = false;
   if (p.P == 2 && !tile && v == 16) {
     two_lanes = true;
+  } else if (p.P == 4 && !tile && v == 16) {
+    four_lanes = true;
   } else if (p.P > 1) {
     v = std::min(v, 16 / static_cast<int>(p.P));
   }
@@ -358,7 +362,7 @@ Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int6
     };
     j.vec = v;
     j.dev.mode = tile ? kTileStd : kDetileStd;
-    j.dev.lanes_per_unit = two_lanes ? 2 : 1;
+    j.dev.lanes_per_unit = two_lanes ? 2 : four_lanes ? 4 : 1;
     if (tiled_order) {
       // Whole tile rows (cuts fall on them): units of tile rows [t_lo, t_hi).
       auto tile_row = [&](int64_t x) -> uint64_t {
