@@ -851,7 +851,58 @@ def bench_weight_sync_tiled(torch, pkg, dev, args):
                                       "on the host by the oracle's restatement of the reference's "
                                       "threaded routine (4 threads, as the reference), GB/s counted "
                                       "as 2 x bytes like the kernel"}}
+    ws.close()
+    del params, staging
+    torch.cuda.empty_cache()
+    out["int8_quads"] = bench_tiled_int8(torch, pkg, dev, args)
     log(f"weights_tiled: {out}")
+    return out
+
+
+def bench_tiled_int8(torch, pkg, dev, args):
+    """Weights packed four 8-bit elements to a word: 8 int8 [14336, 8192]
+    matrices (0.94 GB) in T(8,128)(4,1), detile + pack and tile + unpack
+    through the weight synchronizer's device pack / unpack, each checked
+    against the torch formulation of the tiling."""
+    H, W, n = 14336, 8192, 8
+    lay = pkg.tiling.TiledLayout(1, (H, W), [(8, 128), (4, 1)])
+    params = [torch.empty(lay.tiled_bytes, dtype=torch.uint8, device=dev).random_(0, 256)
+              for _ in range(n)]
+    torch.cuda.synchronize()
+    total = n * lay.logical_bytes
+    ws = pkg.WeightSynchronizer([[t] for t in params], layouts=[[lay]] * n, profile_kernels=True)
+    staging = torch.empty(ws.total_bytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.Stream(dev)
+    reps = max(3, args.sub_steps // 2)
+
+    def image(k):
+        _, nbytes, off = ws.host_buffer_info(k, 0)
+        return staging[off:off + nbytes].view(H, W)
+
+    out = {"workload": f"{n} int8 [{H}, {W}] matrices in T(8,128)(4,1), {total / 1e9:.2f} GB"}
+    ws.pack(staging, stream=s).Await()
+    ws.kernel_times(True, reset=True)
+    for f in [ws.pack(staging, stream=s) for _ in range(reps)]:
+        f.Await()
+    kt = ws.kernel_times(True, reset=True)
+    torch.cuda.synchronize()
+    for k, t in enumerate(params):
+        check(torch.equal(image(k), torch_detile(torch, t, H, W, 8, 128, 4)),
+              f"int8 detile + pack, tensor {k}")
+    for f in [ws.unpack(staging, stream=s) for _ in range(reps)]:
+        f.Await()
+    kt2 = ws.kernel_times(False, reset=True)
+    torch.cuda.synchronize()
+    for k, t in enumerate(params):
+        check(torch.equal(t, torch_tile(torch, image(k), 8, 128, 4)),
+              f"int8 tile + unpack, tensor {k}")
+    for name, kt_ in (("detile_pack", kt), ("tile_unpack", kt2)):
+        ms = kt_["total_ms"] / reps
+        g = 2 * total / ms / 1e6
+        out[f"{name}_gbps"] = round(g, 1)
+        out[f"{name}_frac_of_hbm_peak"] = round(g / HBM_PEAK_GBPS, 4)
+        out[f"{name}_frac_of_box_copy"] = frac_of_box(g, args.box_copy_gbps)
+    out["verified"] = True
     ws.close()
     del params, staging
     torch.cuda.empty_cache()
