@@ -20,9 +20,11 @@ numpy restatement of the weight-sync byte movement:
 Parity status: expand_entries / nd_shard_slices are pinned by known answers
 derived from the definitions and by closed forms (a column split equals
 numpy column slicing; pack then unpack is the identity). offset_table /
-pack: parity unpinned -- the packed host layout has no reference
-counterpart (the reference keeps one host buffer per tensor), so only its
-definition and the byte identity of every tensor's copy check it.
+pack have no reference counterpart (the reference keeps one host buffer per
+tensor): the packed host layout is this build's own format, so its
+definition is what fixes it, and it is pinned by known answers derived from
+that definition (offsets of hand-picked tensor sizes) and by the byte
+identity of every tensor's copy.
 """
 import itertools
 

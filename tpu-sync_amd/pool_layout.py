@@ -4,7 +4,8 @@ The reference's Python descriptors (tpu_sync/api/torch/pool_layout.py:30-199):
 a *storage* is one wrapped allocation (a KVCacheManager block array, index =
 layer); a *pool* is an array of equally strided blocks inside one storage;
 *regions* describe the live bytes of one block. ``tag`` and ``dtype_tag`` are
-opaque: stored, filtered and echoed, never parsed.
+labels for the caller: kept with the pool, usable to select pools by tag and
+returned by ``to_dict``, but this package gives them no meaning.
 
 The geometry functions below (copy extents, live segments, compact-live copy
 translation) run the library's native restatement of
@@ -76,7 +77,8 @@ class PoolSpec:
 
     @property
     def storage_extent_end_bytes(self) -> int:
-        """Absolute end of the last declared live byte in the storage."""
+        """Byte offset, from the start of the storage, just past the live
+        bytes of the pool's last block (its furthest-reaching region)."""
         live_end = max((r.extent_end_bytes for r in self.regions), default=0)
         return self.base_offset_bytes + (self.num_blocks - 1) * self.block_stride_bytes + live_end
 
