@@ -49,11 +49,11 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and, in a
 # second run, WRITE_SIZE (KiB per dispatch), each divided by the factor the
 # same counter reads for a plain 1 GiB device copy in the same runs (FETCH
-# 0.50002, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
+# 0.50001, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
 # (kernel, algorithmic bytes per launch).
 MEASURED_TRAFFIC = {
-    ("gather", 2 * 512 * 64 * 32768): int((524450.1 / 0.50002 + 1048615.4 / 1.0) * 1024),
-    ("scatter", 2 * 512 * 64 * 32768): int((524337.8 / 0.50002 + 1048598.7 / 1.0) * 1024),
+    ("gather", 2 * 512 * 64 * 32768): int((524448.5 / 0.50001 + 1048635.9 / 1.0) * 1024),
+    ("scatter", 2 * 512 * 64 * 32768): int((524337.2 / 0.50001 + 1048594.5 / 1.0) * 1024),
 }
 
 WORKLOADS = {
@@ -840,9 +840,9 @@ def bench_weight_sync_tiled(torch, pkg, dev, args):
            if tile_ms else None,
            "verified": True,
            # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE with the
-           # same calibration (profiles/tiled_copy_weight_sync_llama3_8b_trace.txt).
-           "detile_pack_traffic": int((7844359.0 / 0.50002 + 15684479.2) * 1024),
-           "tile_unpack_traffic": int((7844086.1 / 0.50002 + 15693224.0) * 1024),
+           # same calibration (profiles/tiled_copy_weight_sync_trace.txt).
+           "detile_pack_traffic": int((7844359.0 / 0.50001 + 15684509.8) * 1024),
+           "tile_unpack_traffic": int((7844089.8 / 0.50001 + 15691940.2) * 1024),
            "d2h_gbps": round(d2h_gbps, 2), "h2d_gbps": round(h2d_gbps, 2),
            "cpu_baseline": {"value": round(cpu[4], 2), "unit": "GB/s", "cores": 4, "kind": "port",
                             "all_threads_gbps": round(cpu[max(cpu)], 2), "all_threads": max(cpu),
@@ -902,6 +902,10 @@ def bench_tiled_int8(torch, pkg, dev, args):
         out[f"{name}_gbps"] = round(g, 1)
         out[f"{name}_frac_of_hbm_peak"] = round(g / HBM_PEAK_GBPS, 4)
         out[f"{name}_frac_of_box_copy"] = frac_of_box(g, args.box_copy_gbps)
+    # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE with the
+    # same calibration (profiles/tiled_copy_weight_sync_trace.txt).
+    out["detile_pack_traffic"] = int((458921.0 / 0.50001 + 918186.6) * 1024)
+    out["tile_unpack_traffic"] = int((458925.3 / 0.50001 + 917620.5) * 1024)
     out["verified"] = True
     ws.close()
     del params, staging
