@@ -86,6 +86,41 @@ def test_fp8_payload_and_scales_round_trip_match_oracle(kvx, oracle, cuda, mode)
     mgr.close()
 
 
+def test_fp8_chunk_with_partial_payload_and_scales_matches_oracle(kvx, oracle, cuda):
+    """1.5 MiB staging chunks over 8 payload storages x 40 ids of 16 KiB:
+    three chunks of payload alone, then a chunk holding the last 32 payload
+    blocks (starting inside a storage) together with every scale block, so
+    one launch carries a payload piece that does not start at a storage
+    boundary beside the scale piece, in both directions."""
+    rng = np.random.default_rng(43)
+    layers, blocks, host_blocks, n = 4, 96, 64, 40
+    kv_np, sc_np, kv, sc, bb = build(rng, cuda, layers, blocks)
+    mgr = kvx.KVCacheManager(kv, host_blocks_to_allocate=host_blocks, scale_tables=sc,
+                             transfer_mode="staged", staging_chunk_bytes=96 * bb,
+                             staging_chunks=2)
+    dev = [u8(a).copy() for a in kv_np + sc_np]
+    host = [np.zeros(host_blocks * (bb if k < 2 * layers else 32), np.uint8)
+            for k in range(3 * layers)]
+    bbs = [bb] * (2 * layers) + [32] * layers
+    ids = rng.choice(blocks, n, replace=False).tolist()
+    slot = rng.permutation(host_blocks)[:n].tolist()
+    before = mgr.engine_stats()["kernel_launches"]
+    mgr.d2h(ids, slot).Await()
+    assert mgr.engine_stats()["kernel_launches"] - before == 4
+    assert oracle.transfer(True, dev, host, bbs, [d.nbytes for d in dev], ids, slot,
+                           [1] * n) == 0
+    for k in range(3 * layers):
+        assert np.array_equal(mgr.host_view(k), host[k]), k
+    back = rng.choice(blocks, n, replace=False).tolist()
+    mgr.h2d(slot, back).Await()
+    assert oracle.transfer(False, dev, host, bbs, [d.nbytes for d in dev], slot, back,
+                           [1] * n) == 0
+    torch.cuda.synchronize()
+    for k, t in enumerate(kv + sc):
+        assert np.array_equal(u8(t.cpu().numpy()), dev[k]), k
+    mgr.close()
+
+
 def test_fp8_device_gather_moves_scales_in_the_same_launch(kvx, oracle, cuda):
     rng = np.random.default_rng(41)
     layers, blocks = 3, 64

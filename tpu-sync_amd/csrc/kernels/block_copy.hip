@@ -131,6 +131,55 @@ __device__ __forceinline__ bool bad_id(int64_t id, int64_t limit) {
   return static_cast<uint64_t>(id) >= static_cast<uint64_t>(limit);
 }
 
+// Many small blocks per workgroup (side tables such as fp8 scales). The
+// workgroup first resolves its blocks -- id, table entries, bounds check --
+// with one pass of independent, coalesced loads, one block per lane, and
+// stages each block's source and destination address in LDS (0 for a bad
+// id). Then lane e moves vector (e % elems) of block (e / elems) with both
+// addresses read from LDS, so no lane waits on a chain of dependent table
+// loads before its data load. b0: the workgroup's first block of the piece.
+template <typename V, bool kGather>
+__device__ __forceinline__ void copy_small_blocks(const KPiece& p, const int64_t* ids,
+                                                  const int64_t* ids2, int32_t* error,
+                                                  uint32_t n, uint32_t b0) {
+  __shared__ uint64_t s_src[kSmallMaxBlocks];
+  __shared__ uint64_t s_dst[kSmallMaxBlocks];
+  const uint32_t left = p.nblocks - b0;
+  const uint32_t nb = left < p.bpw ? left : p.bpw;
+  const uint64_t block_bytes = static_cast<uint64_t>(p.elems) * sizeof(V);
+  for (uint32_t b = threadIdx.x; b < nb; b += kThreads) {
+    const uint32_t f = p.f0 + b0 + b;
+    const uint32_t w = f / n;
+    const uint32_t i = f - w * n;
+    const int64_t id = gptr<const int64_t>(reinterpret_cast<uint64_t>(ids))[i];
+    const uint64_t base = gptr<const uint64_t>(p.storages)[w];
+    bool bad = bad_id(id, p.pool_blocks);
+    uint64_t other;
+    if (p.others != 0) {
+      const int64_t id2 = gptr<const int64_t>(reinterpret_cast<uint64_t>(ids2))[i];
+      const uint64_t obase = gptr<const uint64_t>(p.others)[w];
+      bad = bad || bad_id(id2, p.other_blocks);
+      other = obase + static_cast<uint64_t>(id2) * block_bytes;
+    } else {
+      other = p.staging + w * static_cast<uint64_t>(p.stride_w) +
+              i * static_cast<uint64_t>(p.stride_i);
+    }
+    const uint64_t pool = base + static_cast<uint64_t>(id) * block_bytes;
+    if (bad && error != nullptr) atomicOr(error, 1);
+    s_src[b] = bad ? 0 : (kGather ? pool : other);
+    s_dst[b] = bad ? 0 : (kGather ? other : pool);
+  }
+  __syncthreads();
+  const uint32_t total = nb * p.elems;
+  for (uint32_t e = threadIdx.x; e < total; e += kThreads) {
+    const uint32_t b = e / p.elems;
+    const uint32_t sub = e - b * p.elems;
+    const uint64_t src = s_src[b];
+    if (src == 0) continue;
+    st_nt(ld_nt(gptr<const V>(src) + sub), gptr<V>(s_dst[b]) + sub);
+  }
+}
+
 template <typename V, bool kGather, int kUnroll>
 __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
   const uint32_t wg = blockIdx.x;
@@ -175,49 +224,7 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(KParams P) {
     return;
   }
 
-  // Many small blocks per workgroup (side tables such as fp8 scales). The
-  // workgroup first resolves its blocks -- id, table entries, bounds check --
-  // with one pass of independent, coalesced loads, one block per lane, and
-  // stages each block's source and destination address in LDS (0 for a bad
-  // id). Then lane e moves vector (e % elems) of block (e / elems) with both
-  // addresses read from LDS, so no lane waits on a chain of dependent table
-  // loads before its data load.
-  __shared__ uint64_t s_src[kSmallMaxBlocks];
-  __shared__ uint64_t s_dst[kSmallMaxBlocks];
-  const uint32_t left = p.nblocks - b0;
-  const uint32_t nb = left < p.bpw ? left : p.bpw;
-  const uint64_t block_bytes = static_cast<uint64_t>(p.elems) * sizeof(V);
-  for (uint32_t b = threadIdx.x; b < nb; b += kThreads) {
-    const uint32_t f = p.f0 + b0 + b;
-    const uint32_t w = f / n;
-    const uint32_t i = f - w * n;
-    const int64_t id = gptr<const int64_t>(reinterpret_cast<uint64_t>(P.ids))[i];
-    const uint64_t base = gptr<const uint64_t>(p.storages)[w];
-    bool bad = bad_id(id, p.pool_blocks);
-    uint64_t other;
-    if (p.others != 0) {
-      const int64_t id2 = gptr<const int64_t>(reinterpret_cast<uint64_t>(P.ids2))[i];
-      const uint64_t obase = gptr<const uint64_t>(p.others)[w];
-      bad = bad || bad_id(id2, p.other_blocks);
-      other = obase + static_cast<uint64_t>(id2) * block_bytes;
-    } else {
-      other = p.staging + w * static_cast<uint64_t>(p.stride_w) +
-              i * static_cast<uint64_t>(p.stride_i);
-    }
-    const uint64_t pool = base + static_cast<uint64_t>(id) * block_bytes;
-    if (bad && P.error != nullptr) atomicOr(P.error, 1);
-    s_src[b] = bad ? 0 : (kGather ? pool : other);
-    s_dst[b] = bad ? 0 : (kGather ? other : pool);
-  }
-  __syncthreads();
-  const uint32_t total = nb * p.elems;
-  for (uint32_t e = threadIdx.x; e < total; e += kThreads) {
-    const uint32_t b = e / p.elems;
-    const uint32_t sub = e - b * p.elems;
-    const uint64_t src = s_src[b];
-    if (src == 0) continue;
-    st_nt(ld_nt(gptr<const V>(src) + sub), gptr<V>(s_dst[b]) + sub);
-  }
+  copy_small_blocks<V, kGather>(p, P.ids, P.ids2, P.error, n, b0);
 }
 
 // The common launch (one piece of large blocks, no second paged side, one
@@ -248,9 +255,9 @@ struct FastParams {
 
 enum FastOrder : int { kStorageMajor = 0, kStoragePairs = 1, kAllStorages = 2 };
 
+// Block g of a fast launch (one workgroup, one whole block).
 template <typename V, bool kGather, int kUnroll, int kOrder>
-__global__ __launch_bounds__(kThreads) void block_copy_fast_kernel(FastParams P) {
-  const uint32_t g = blockIdx.x;
+__device__ __forceinline__ void fast_block(const FastParams& P, uint32_t g) {
   uint32_t w, i;
   if (kOrder == kAllStorages) {
     i = g / P.wstorages;
@@ -284,6 +291,25 @@ __global__ __launch_bounds__(kThreads) void block_copy_fast_kernel(FastParams P)
     copy_whole_block<V, kUnroll>(stg, pool, elems);
   }
   if (bad && threadIdx.x == 0 && P.error != nullptr) atomicOr(P.error, 1);
+}
+
+template <typename V, bool kGather, int kUnroll, int kOrder>
+__global__ __launch_bounds__(kThreads) void block_copy_fast_kernel(FastParams P) {
+  fast_block<V, kGather, kUnroll, kOrder>(P, blockIdx.x);
+}
+
+// The fast launch behind one leading small-block piece: the fp8 payload and
+// its scale side table in one launch. The first side_wgs workgroups move the
+// side piece (many blocks each, as in the general kernel), the rest take the
+// payload blocks in the fast kernel's order.
+template <typename V, bool kGather, int kUnroll, int kOrder>
+__global__ __launch_bounds__(kThreads) void block_copy_fast_side_kernel(FastParams P, KPiece side,
+                                                                        uint32_t side_wgs) {
+  if (blockIdx.x < side_wgs) {
+    copy_small_blocks<V, kGather>(side, P.ids, nullptr, P.error, P.n, blockIdx.x * side.bpw);
+    return;
+  }
+  fast_block<V, kGather, kUnroll, kOrder>(P, blockIdx.x - side_wgs);
 }
 
 // Blocks per workgroup: one for blocks of >= 2 vectors per lane, otherwise
@@ -400,6 +426,21 @@ bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, int* order) {
   return true;
 }
 
+// The fast-with-side-piece parameters when the launch is one small-block
+// piece (no second paged side; BuildParams puts it first) followed by one
+// whole-block piece that qualifies for the fast kernel.
+bool BuildFastSideParams(const KParams& K, CopyDir dir, FastParams* F, KPiece* side,
+                         uint32_t* side_wgs, int* order) {
+  if (K.npieces != 2 || K.p[0].whole || K.p[0].others != 0) return false;
+  KParams one = K;
+  one.npieces = 1;
+  one.p[0] = K.p[1];
+  if (!BuildFastParams(one, dir, F, order)) return false;
+  *side = K.p[0];
+  *side_wgs = K.p[1].wg_begin;
+  return true;
+}
+
 // LDS of one CU on gfx950.
 constexpr uint32_t kLdsPerCu = 160u << 10;
 
@@ -429,12 +470,31 @@ hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, int wg_per_cu,
     }
     return hipGetLastError();
   }
+  // HBM-bound gathers (not the capped grids of zero-copy copies) on the
+  // kernels with the small-block path take the same cap, minus that path's
+  // own 4 KiB of address tables.
+  const uint32_t glds = wg_per_cu > 0 && !capped_grid
+                            ? kLdsPerCu / static_cast<uint32_t>(wg_per_cu) - kStaticLds
+                            : 0;
+  KPiece side;
+  uint32_t side_wgs = 0;
+  if (BuildFastSideParams(P, dir, &F, &side, &side_wgs, &order)) {
+    if (dir == CopyDir::kGather && order == kStoragePairs) {
+      hipLaunchKernelGGL((block_copy_fast_side_kernel<V, true, kUnroll, kStoragePairs>),
+                         dim3(grid), dim3(kThreads), glds, stream, F, side, side_wgs);
+    } else if (dir == CopyDir::kGather) {
+      hipLaunchKernelGGL((block_copy_fast_side_kernel<V, true, kUnroll, kStorageMajor>),
+                         dim3(grid), dim3(kThreads), glds, stream, F, side, side_wgs);
+    } else if (order == kAllStorages) {
+      hipLaunchKernelGGL((block_copy_fast_side_kernel<V, false, kUnroll, kAllStorages>),
+                         dim3(grid), dim3(kThreads), 0, stream, F, side, side_wgs);
+    } else {
+      hipLaunchKernelGGL((block_copy_fast_side_kernel<V, false, kUnroll, kStorageMajor>),
+                         dim3(grid), dim3(kThreads), 0, stream, F, side, side_wgs);
+    }
+    return hipGetLastError();
+  }
   if (dir == CopyDir::kGather) {
-    // HBM-bound gathers (not the capped grids of zero-copy copies) take the
-    // same cap, minus the kernel's own 4 KiB of address tables.
-    const uint32_t glds = wg_per_cu > 0 && !capped_grid
-                              ? kLdsPerCu / static_cast<uint32_t>(wg_per_cu) - kStaticLds
-                              : 0;
     hipLaunchKernelGGL((block_copy_kernel<V, true, kUnroll>), dim3(grid),
                        dim3(kThreads), glds, stream, P);
   } else {
