@@ -133,6 +133,9 @@ def parse_args():
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
                         "request's load and save finish before the next is issued)")
+    p.add_argument("--zipf-more-inflight", type=int, default=2,
+                   help="then continue the churn on the warm tier with this many "
+                        "requests in flight (0 or 1: skip)")
     p.add_argument("--configs-only", action="store_true",
                    help="measure only the --configs workloads (no headline, no CPU "
                         "baseline) and print them; for profiling one of them")
@@ -1050,7 +1053,8 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     have copies in flight (the next request is looked up and issued while the
     previous one's copies run), as in a server with several requests in
     progress. With one request in flight, each request's latency (lookup to
-    both copies polled done) is recorded."""
+    both copies polled done) is recorded. Then the same request stream
+    continues on the warm tier with --zipf-more-inflight requests in flight."""
     L, P, bb = 80, 12000, 32768
     S = 2 * L
     host_blocks, tier_limit = zipf_host_blocks(args, S * bb)
@@ -1099,68 +1103,82 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                     raise RuntimeError(f"store save failed: {len(failed)} blocks")
                 done_s += len(done)
 
-    saved = loaded = hits = asked = skipped = device_hits = replaced = 0
-    inflight = max(1, args.zipf_inflight)
-    window = []  # (loads, saves) of the requests possibly still in flight
-    latency = []  # (blocks, seconds) per request, one request in flight
-    per_request = []  # (blocks loaded, blocks saved) per request
-    t0 = time.perf_counter()
-    for step in range(args.zipf_batches):
-        t_req = time.perf_counter()
-        doc = int(np.searchsorted(cdf, rng.random()))
-        nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
-        chain = [b"d%03d:%05d" % (doc, i) for i in range(nb)]
-        dev_ids = rng.permutation(P)[:nb].tolist()
-        found = store.lookup(chain, pin_found=True)
-        k = len(found)
-        rest = chain[k:]
-        # Host-resident hits are loaded; an HBM-only entry (inserted by a
-        # request whose save could not get host blocks, or whose save is
-        # still in flight) names a device block the caller owns: a hit with
-        # nothing to move.
-        # A block another request in flight is loading arrives with that
-        # load: also a hit with nothing to move.
-        on_host = (pkg.BlockStatus.HOST, pkg.BlockStatus.HOST_AND_HBM)
-        to_load = [b.status in on_host and h not in loading for h, b in found]
-        load_h = [h for (h, _), t in zip(found, to_load) if t]
-        load_d = [dev_ids[i] for i, t in enumerate(to_load) if t]
-        in_hbm = [h for (h, _), t in zip(found, to_load) if not t]
-        if in_hbm:
-            store.release(in_hbm)
-            device_hits += len(in_hbm)
-        if load_h and not store.load(load_h, load_d):
-            raise RuntimeError(f"store load of {len(load_h)} blocks failed: {store.last_error()}")
-        loading.update(load_h)
-        n_save = 0
-        if rest:
-            # Chain blocks past the cached prefix that are still on the host
-            # (their prefix was evicted first) cannot be reached through a
-            # prefix lookup any more; the request's fresh copies replace them.
-            replaced += store.evict(rest)
-            sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
-            if store.insert(rest, sl, on_host=False):
-                if store.save(rest):
-                    n_save = len(rest)
-                else:  # no host blocks to spare, or a block pinned by another request
-                    store.release(rest)
+    def run(inflight, batches):
+        """batches requests with up to `inflight` in flight; returns the
+        phase's counters, per-request latencies (one in flight) and sizes."""
+        nonlocal done_l, done_s
+        done_l = done_s = 0
+        saved = loaded = hits = asked = skipped = device_hits = replaced = 0
+        window = []  # (loads, saves) of the requests possibly still in flight
+        latency = []  # (blocks, seconds) per request, one request in flight
+        per_request = []  # (blocks loaded, blocks saved) per request
+        t0 = time.perf_counter()
+        for step in range(batches):
+            t_req = time.perf_counter()
+            doc = int(np.searchsorted(cdf, rng.random()))
+            nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
+            chain = [b"d%03d:%05d" % (doc, i) for i in range(nb)]
+            dev_ids = rng.permutation(P)[:nb].tolist()
+            found = store.lookup(chain, pin_found=True)
+            k = len(found)
+            rest = chain[k:]
+            # Host-resident hits are loaded; an HBM-only entry (inserted by a
+            # request whose save could not get host blocks, or whose save is
+            # still in flight) names a device block the caller owns: a hit
+            # with nothing to move. A block another request in flight is
+            # loading arrives with that load: also a hit with nothing to move.
+            on_host = (pkg.BlockStatus.HOST, pkg.BlockStatus.HOST_AND_HBM)
+            to_load = [b.status in on_host and h not in loading for h, b in found]
+            load_h = [h for (h, _), t in zip(found, to_load) if t]
+            load_d = [dev_ids[i] for i, t in enumerate(to_load) if t]
+            in_hbm = [h for (h, _), t in zip(found, to_load) if not t]
+            if in_hbm:
+                store.release(in_hbm)
+                device_hits += len(in_hbm)
+            if load_h and not store.load(load_h, load_d):
+                raise RuntimeError(f"store load of {len(load_h)} blocks failed: "
+                                   f"{store.last_error()}")
+            loading.update(load_h)
+            n_save = 0
+            if rest:
+                # Chain blocks past the cached prefix that are still on the
+                # host (their prefix was evicted first) cannot be reached
+                # through a prefix lookup any more; the request's fresh
+                # copies replace them.
+                replaced += store.evict(rest)
+                sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
+                if store.insert(rest, sl, on_host=False):
+                    if store.save(rest):
+                        n_save = len(rest)
+                    else:  # no host blocks to spare, or a block pinned by another request
+                        store.release(rest)
+                        skipped += len(rest)
+                else:  # another request in flight inserted some of them
                     skipped += len(rest)
-            else:  # another request in flight inserted some of them
-                skipped += len(rest)
-        loaded += len(load_h)
-        saved += n_save
-        hits += k
-        asked += nb
-        window.append((len(load_h), n_save))
-        # Keep at most `inflight` requests in flight: wait until every copy
-        # but those of the newest inflight - 1 requests has landed.
-        keep = window[len(window) - (inflight - 1):] if inflight > 1 else []
-        poll_until(loaded - sum(x[0] for x in keep), saved - sum(x[1] for x in keep))
-        window = keep
-        if inflight == 1:
-            latency.append((nb, time.perf_counter() - t_req))
-        per_request.append((len(load_h), n_save))
-    poll_until(loaded, saved)
-    t_run = time.perf_counter() - t0
+            loaded += len(load_h)
+            saved += n_save
+            hits += k
+            asked += nb
+            window.append((len(load_h), n_save))
+            # Keep at most `inflight` requests in flight: wait until every
+            # copy but those of the newest inflight - 1 requests has landed.
+            keep = window[len(window) - (inflight - 1):] if inflight > 1 else []
+            poll_until(loaded - sum(x[0] for x in keep), saved - sum(x[1] for x in keep))
+            window = keep
+            if inflight == 1:
+                latency.append((nb, time.perf_counter() - t_req))
+            per_request.append((len(load_h), n_save))
+        poll_until(loaded, saved)
+        t_run = time.perf_counter() - t0
+        return dict(saved=saved, loaded=loaded, hits=hits, asked=asked, skipped=skipped,
+                    device_hits=device_hits, replaced=replaced, t_run=t_run,
+                    latency=latency, per_request=per_request)
+
+    inflight = max(1, args.zipf_inflight)
+    r = run(inflight, args.zipf_batches)
+    saved, loaded, hits, asked = r["saved"], r["loaded"], r["hits"], r["asked"]
+    skipped, device_hits, replaced = r["skipped"], r["device_hits"], r["replaced"]
+    latency, per_request, t_run = r["latency"], r["per_request"], r["t_run"]
     moved = (saved + loaded) * S * bb
     # PCIe bound of this request stream: a request's load (H2D) and save (D2H)
     # run at once, each at most at its direction's measured pinned peak and
@@ -1221,6 +1239,19 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                                [t for nb, t in latency if nb < 128])}
                           if latency else None),
            "requests_64_to_127_blocks_vs_pcie_bound": small_vs_bound}
+    if args.zipf_more_inflight > 1:
+        # The same request stream continued on the warm tier with more
+        # requests in flight, as a server with several requests in progress;
+        # it has no per-request PCIe bound (requests overlap).
+        r2 = run(args.zipf_more_inflight, args.zipf_batches)
+        moved2 = (r2["saved"] + r2["loaded"]) * S * bb
+        out["more_in_flight"] = {
+            "requests_in_flight": args.zipf_more_inflight, "batches": args.zipf_batches,
+            "blocks_saved": r2["saved"], "blocks_loaded": r2["loaded"],
+            "blocks_skipped": r2["skipped"], "device_hits": r2["device_hits"],
+            "hit_rate": round(r2["hits"] / max(r2["asked"], 1), 4),
+            "gbps": round(moved2 / r2["t_run"] / 1e9, 2),
+            "blocks_per_s": round((r2["saved"] + r2["loaded"]) / r2["t_run"], 1)}
     # One offload + reload through the same manager and host tier after the
     # churn (its lanes, chunking and /dev/shm tier), checked against torch.
     perm = rng.permutation(P)
