@@ -1528,7 +1528,10 @@ def main():
     kinds = {"staged": stats["staged_copies"], "zero_copy": stats["zero_copy_copies"],
              "direct": stats["direct_copies"]}
     headline_path = {"mode": args.mode, **{f"{k}_copies": v for k, v in kinds.items()},
-                     "path": "+".join(k for k, v in kinds.items() if v) or "none"}
+                     "path": "+".join(k for k, v in kinds.items() if v) or "none",
+                     # Gather, D2H, H2D and scatter streams: pairs probed on
+                     # one hardware queue at creation (0: all apart).
+                     "stream_placement": mgr.stream_placement}
     kg = mgr.kernel_times(True, reset=True)
     ks = mgr.kernel_times(False, reset=True)
 

@@ -304,6 +304,20 @@ int kvx_manager_engine_stats(kvx_manager* m, int64_t* out8);
  * lane has run, or when the lanes use hipMemcpyAsync (KVX_LANE_DMA=hip, or
  * no engine available); -1 for a null or CPU-only manager. */
 int32_t kvx_manager_lane_dma_engines(kvx_manager* m);
+/* Hardware-queue placement of the transfer engine's four streams (no
+ * reference counterpart: PJRT has no streams). At creation one short probe
+ * kernel per stream runs at once with the others; two streams whose probes
+ * ran one after the other share a hardware queue, which serializes their
+ * work (an offload's DMA behind a reload's), and the set is created again
+ * behind more spacer streams, up to 3 times. out2[0] = pairs still sharing a
+ * queue (0: every stream on its own queue; -1: the probe could not run),
+ * out2[1] = stream sets created. */
+int kvx_manager_stream_placement(kvx_manager* m, int32_t* out2);
+/* The same probe over a caller's streams (hipStream_t values, n <= 64) of the
+ * current device (no reference counterpart): *pairs_out = pairs that ran one
+ * after the other, i.e. share a hardware queue. For a framework that wants
+ * its own streams off the library's queues. */
+int kvx_probe_stream_queues(const uint64_t* streams, int32_t n, int32_t* pairs_out);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the
  * gather (gather = 1) or scatter (gather = 0) kernels so far. Waits for the

@@ -12,6 +12,7 @@
 #include "../host/hip_util.h"
 #include "../host/kv_cache_store.h"
 #include "../host/numa.h"
+#include "../host/queue_check.h"
 #include "../host/raiden_env.h"
 #include "../kernels/block_copy.h"
 #include "capi_internal.h"
@@ -526,6 +527,28 @@ int kvx_manager_engine_stats(kvx_manager* m, int64_t* out8) {
 int32_t kvx_manager_lane_dma_engines(kvx_manager* m) {
   if (m == nullptr || m->impl->engine() == nullptr) return -1;
   return static_cast<int32_t>(m->impl->engine()->LaneDmaEngines());
+}
+int kvx_manager_stream_placement(kvx_manager* m, int32_t* out2) {
+  if (m == nullptr || out2 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null manager or output");
+  if (m->impl->engine() == nullptr) {
+    return Fail(KVX_FAILED_PRECONDITION, "CPU-only manager has no transfer engine");
+  }
+  const kvx::StreamPlacement p = m->impl->engine()->placement();
+  out2[0] = p.serialized_pairs;
+  out2[1] = p.attempts;
+  return KVX_OK;
+}
+int kvx_probe_stream_queues(const uint64_t* streams, int32_t n, int32_t* pairs_out) {
+  if (pairs_out == nullptr || (streams == nullptr && n > 0)) {
+    return Fail(KVX_INVALID_ARGUMENT, "null streams or output");
+  }
+  if (n < 0 || n > 64) return Fail(KVX_INVALID_ARGUMENT, "stream probe takes 0..64 streams");
+  std::vector<hipStream_t> ss(static_cast<size_t>(n));
+  for (int32_t i = 0; i < n; ++i) ss[i] = reinterpret_cast<hipStream_t>(streams[i]);
+  auto pairs = kvx::SerializedStreamPairs(ss);
+  if (!pairs.ok()) return Fail(pairs.status());
+  *pairs_out = static_cast<int32_t>(pairs->size());
+  return KVX_OK;
 }
 
 int kvx_manager_kernel_times(kvx_manager* m, int32_t gather, int32_t reset,

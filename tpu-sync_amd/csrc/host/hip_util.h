@@ -69,20 +69,28 @@ inline int HwQueuesPerProcess() {
 // hardware queue, created first, fills the pool and evens out counts that
 // differ by at most one, so the streams created next each join a different
 // queue. Counts that differ by more (many streams created elsewhere on one
-// queue) can still put two of them on one queue.
-inline Status CreateStreamsOnDistinctQueues(std::initializer_list<hipStream_t*> out) {
-  std::vector<hipStream_t> spacers(static_cast<size_t>(HwQueuesPerProcess()), nullptr);
+// queue) can still put two of them on one queue; more spacers (`spacers`,
+// default one per hardware queue) even out larger differences.
+// CreateStreamsOnDistinctQueuesChecked (queue_check.h) checks the result.
+inline Status CreateStreamsOnDistinctQueues(const std::vector<hipStream_t*>& out,
+                                            int spacers = 0) {
+  std::vector<hipStream_t> sp(static_cast<size_t>(spacers > 0 ? spacers : HwQueuesPerProcess()),
+                              nullptr);
   Status st = OkStatus();
-  for (hipStream_t& s : spacers) {
+  for (hipStream_t& s : sp) {
     if (st.ok()) st = HipStatus(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "spacer stream");
   }
   for (hipStream_t* s : out) {
     if (st.ok()) st = HipStatus(hipStreamCreateWithFlags(s, hipStreamNonBlocking), "stream");
   }
-  for (hipStream_t s : spacers) {
+  for (hipStream_t s : sp) {
     if (s != nullptr) (void)hipStreamDestroy(s);
   }
   return st;
+}
+
+inline Status CreateStreamsOnDistinctQueues(std::initializer_list<hipStream_t*> out) {
+  return CreateStreamsOnDistinctQueues(std::vector<hipStream_t*>(out));
 }
 
 }  // namespace kvx

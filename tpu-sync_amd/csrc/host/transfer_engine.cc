@@ -224,8 +224,8 @@ StatusOr<std::unique_ptr<TransferEngine>> TransferEngine::Create(
 Status TransferEngine::Init() {
   DeviceGuard g(opts_.device);
   if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
-  KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueues(
-      {&gather_stream_, &d2h_stream_, &h2d_stream_, &scatter_stream_}));
+  KVX_RETURN_IF_ERROR(CreateStreamsOnDistinctQueuesChecked(
+      {&gather_stream_, &d2h_stream_, &h2d_stream_, &scatter_stream_}, &placement_));
   return GrowArgRing(opts_.arg_ring_bytes);
 }
 

@@ -31,6 +31,7 @@
 #include "../kernels/block_copy.h"
 #include "arg_ring.h"
 #include "copy_future.h"
+#include "queue_check.h"
 #include "sdma_engines.h"
 #include "status.h"
 
@@ -227,6 +228,9 @@ class TransferEngine {
   // The occupancy cap the engine's device gathers launch with.
   int gather_workgroups_per_cu() const { return opts_.gather_workgroups_per_cu; }
   EngineStats stats() const;
+  // How the four streams landed on hardware queues at creation (probed: a
+  // set with two streams on one queue is created again, up to 3 times).
+  StreamPlacement placement() const { return placement_; }
   // SDMA engine bits of the pageable lanes' DMAs, (device-to-host << 16) |
   // host-to-device; 0 while no lane exists or when the lanes use
   // hipMemcpyAsync.
@@ -364,6 +368,7 @@ class TransferEngine {
   hipStream_t d2h_stream_ = nullptr;      // D2H: DMA
   hipStream_t h2d_stream_ = nullptr;      // H2D: DMA
   hipStream_t scatter_stream_ = nullptr;  // H2D: kernels
+  StreamPlacement placement_;
   Ring out_ring_;
   Ring in_ring_;
   uint8_t* arg_host_ = nullptr;

@@ -97,6 +97,17 @@ def _flatten_caches(kv_caches) -> Tuple[List[List[Any]], int]:
     return layers, num_shards
 
 
+def probe_stream_queues(streams) -> int:
+    """Pairs of `streams` (torch.cuda.Stream objects or raw hipStream_t
+    values of the current device, at most 64) whose short probe kernels ran
+    one after the other, i.e. that share a hardware queue."""
+    vals = [int(getattr(s, "cuda_stream", s)) for s in streams]
+    arr = (ctypes.c_uint64 * max(len(vals), 1))(*vals)
+    out = ctypes.c_int32()
+    _capi.check(_capi.load().kvx_probe_stream_queues(arr, len(vals), ctypes.byref(out)))
+    return int(out.value)
+
+
 class LogicalBlockManager:
     """Host block allocator (tpu_sync/kv_cache/logical_block_manager.h:35-93)."""
 
@@ -757,6 +768,18 @@ class KVCacheManager:
         keys = ("direct_copies", "staged_copies", "memcpy_calls", "kernel_launches",
                 "chunks", "zero_copy_copies", "extent_kernel_copies", "bounce_copies")
         return dict(zip(keys, list(out)))
+
+    @property
+    def stream_placement(self) -> dict:
+        """How the transfer engine's four streams landed on hardware queues:
+        a probe at creation (one short kernel per stream, all at once) finds
+        pairs that ran one after the other, i.e. share a queue, and such a
+        set is created again, up to 3 times. serialized_pairs: pairs left on
+        one queue (0: each on its own; -1: the probe could not run);
+        attempts: stream sets created."""
+        out = (ctypes.c_int32 * 2)()
+        _capi.check(_capi.load().kvx_manager_stream_placement(self._h, out))
+        return {"serialized_pairs": int(out[0]), "attempts": int(out[1])}
 
     @property
     def lane_dma_engines(self) -> Optional[Tuple[int, int]]:
