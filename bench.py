@@ -1111,14 +1111,19 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
         saved = loaded = hits = asked = skipped = device_hits = replaced = 0
         window = []  # (loads, saves) of the requests possibly still in flight
         latency = []  # (blocks, seconds) per request, one request in flight
+        # Per request, seconds from its lookup until both copies are issued,
+        # and of that the store's load and save calls.
+        issue = []
         per_request = []  # (blocks loaded, blocks saved) per request
         t0 = time.perf_counter()
         for step in range(batches):
-            t_req = time.perf_counter()
             doc = int(np.searchsorted(cdf, rng.random()))
             nb = int(np.exp(rng.uniform(np.log(64), np.log(2048))))
             chain = [b"d%03d:%05d" % (doc, i) for i in range(nb)]
             dev_ids = rng.permutation(P)[:nb].tolist()
+            # A request's latency runs from its lookup (the request itself is
+            # drawn above) until both of its copies are polled done.
+            t_req = time.perf_counter()
             found = store.lookup(chain, pin_found=True)
             k = len(found)
             rest = chain[k:]
@@ -1135,11 +1140,14 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
             if in_hbm:
                 store.release(in_hbm)
                 device_hits += len(in_hbm)
+            t_call = time.perf_counter()
             if load_h and not store.load(load_h, load_d):
                 raise RuntimeError(f"store load of {len(load_h)} blocks failed: "
                                    f"{store.last_error()}")
+            t_load_call = time.perf_counter() - t_call
             loading.update(load_h)
             n_save = 0
+            t_save_call = 0.0
             if rest:
                 # Chain blocks past the cached prefix that are still on the
                 # host (their prefix was evicted first) cannot be reached
@@ -1148,7 +1156,10 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                 replaced += store.evict(rest)
                 sl = [pkg.RaidenBlockId(rid, -1, d, pkg.BlockStatus.HBM) for d in dev_ids[k:]]
                 if store.insert(rest, sl, on_host=False):
-                    if store.save(rest):
+                    t_call = time.perf_counter()
+                    saved_ok = store.save(rest)
+                    t_save_call = time.perf_counter() - t_call
+                    if saved_ok:
                         n_save = len(rest)
                     else:  # no host blocks to spare, or a block pinned by another request
                         store.release(rest)
@@ -1160,6 +1171,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
             hits += k
             asked += nb
             window.append((len(load_h), n_save))
+            issue.append((time.perf_counter() - t_req, t_load_call, t_save_call))
             # Keep at most `inflight` requests in flight: wait until every
             # copy but those of the newest inflight - 1 requests has landed.
             keep = window[len(window) - (inflight - 1):] if inflight > 1 else []
@@ -1172,13 +1184,14 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
         t_run = time.perf_counter() - t0
         return dict(saved=saved, loaded=loaded, hits=hits, asked=asked, skipped=skipped,
                     device_hits=device_hits, replaced=replaced, t_run=t_run,
-                    latency=latency, per_request=per_request)
+                    latency=latency, issue=issue, per_request=per_request)
 
     inflight = max(1, args.zipf_inflight)
     r = run(inflight, args.zipf_batches)
     saved, loaded, hits, asked = r["saved"], r["loaded"], r["hits"], r["asked"]
     skipped, device_hits, replaced = r["skipped"], r["device_hits"], r["replaced"]
     latency, per_request, t_run = r["latency"], r["per_request"], r["t_run"]
+    issue = r["issue"]
     moved = (saved + loaded) * S * bb
     # PCIe bound of this request stream: a request's load (H2D) and save (D2H)
     # run at once, each at most at its direction's measured pinned peak and
@@ -1202,17 +1215,24 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
             pcie_bound_dir = moved / t_dir / 1e9
         # Small requests (64-127 blocks): latency against the request's own
         # PCIe time, which separates per-request overhead from bytes moved.
-        small = [(t, b, l + sv) for (nb, t), b, (l, sv) in zip(latency, req_bound, per_request)
-                 if nb < 128 and b > 0]
+        small = [(t, b, l + sv, ti) for (nb, t), b, (l, sv), ti
+                 in zip(latency, req_bound, per_request, issue) if nb < 128 and b > 0]
         if small:
-            ratios = sorted(t / b for t, b, _ in small)
-            over_ms = sorted((t - b) * 1e3 for t, b, _ in small)
+            ratios = sorted(t / b for t, b, _, _ in small)
+            over_ms = sorted((t - b) * 1e3 for t, b, _, _ in small)
             small_vs_bound = {
                 "count": len(small),
-                "median_blocks_moved": int(np.median([m for _, _, m in small])),
-                "median_pcie_bound_ms": round(float(np.median([b for _, b, _ in small])) * 1e3, 2),
+                "median_blocks_moved": int(np.median([m for _, _, m, _ in small])),
+                "median_pcie_bound_ms": round(float(np.median([b for _, b, _, _ in small])) * 1e3, 2),
                 "median_latency_over_bound": round(ratios[len(ratios) // 2], 3),
-                "median_ms_above_bound": round(over_ms[len(over_ms) // 2], 2)}
+                "median_ms_above_bound": round(over_ms[len(over_ms) // 2], 2),
+                # Host time from the lookup until the load and save are
+                # issued (store lookup / release / evict / insert / save /
+                # load calls), part of the time above the bound; and of it
+                # the load and save calls (which plan and enqueue the copies).
+                "median_issue_ms": round(float(np.median([ti[0] for *_, ti in small])) * 1e3, 2),
+                "median_load_call_ms": round(float(np.median([ti[1] for *_, ti in small])) * 1e3, 2),
+                "median_save_call_ms": round(float(np.median([ti[2] for *_, ti in small])) * 1e3, 2)}
     out = {"workload": "Llama-3-70B-shaped KV (80 layers, 12000-block pool), prefix-cache "
                        "churn through the KV store: requests are prefixes (64-2048 blocks) of "
                        f"{docs} documents' hash chains, document drawn Zipf(1.1)",
