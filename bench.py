@@ -1272,6 +1272,17 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
             "hit_rate": round(r2["hits"] / max(r2["asked"], 1), 4),
             "gbps": round(moved2 / r2["t_run"] / 1e9, 2),
             "blocks_per_s": round((r2["saved"] + r2["loaded"]) / r2["t_run"], 1)}
+        if peaks:
+            # With requests overlapping freely the stream can do no better
+            # than all loads on H2D, all saves on D2H and everything on the
+            # bidirectional peak at once.
+            t_lo = max(r2["loaded"] * S * bb / (peaks["pcie_h2d_gbps"] * 1e9),
+                       r2["saved"] * S * bb / (peaks["pcie_d2h_gbps"] * 1e9),
+                       moved2 / (peaks["pcie_bidir_gbps"] * 1e9))
+            if t_lo > 0:
+                out["more_in_flight"]["pcie_bound_overlapped_gbps"] = round(moved2 / t_lo / 1e9, 2)
+                out["more_in_flight"]["frac_of_overlapped_bound"] = round(
+                    moved2 / r2["t_run"] / (moved2 / t_lo), 4)
     # One offload + reload through the same manager and host tier after the
     # churn (its lanes, chunking and /dev/shm tier), checked against torch.
     perm = rng.permutation(P)
