@@ -241,6 +241,26 @@ def timed_events(torch, fn, reps, stream):
     return start.elapsed_time(stop) / 1e3 / reps
 
 
+def timed_each(torch, fn, reps, stream):
+    """Mean duration of one launch of fn on `stream`, with an event pair
+    around each launch (the way the library's profiled kernel launches are
+    timed), so a yardstick and the kernels it is compared with carry the same
+    per-launch event overhead."""
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.synchronize()
+        pairs = []
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            pairs.append((a, b))
+    pairs[-1][1].synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / 1e3 / reps
+
+
 def pcie_peaks(torch, dev, nbytes=1 << 30, reps=5):
     """Large pinned hipMemcpyAsync per direction, and both at once, on random
     bytes like the workload's."""
@@ -542,10 +562,11 @@ def verify_round_trip(torch, mgr, storages, src, host, dst):
 def box_copy(torch, pkg, src, dst, reps, stream):
     """The box's streaming-copy yardstick: the library's strided kernel over
     one contiguous entry (src -> dst, the same bytes as a gather launch),
-    timed by HIP events on the stream it runs on; read + write bytes per
-    second. The copy is checked against its source."""
+    timed by HIP events around each launch on the stream it runs on, as the
+    block-copy launches are; read + write bytes per second. The copy is
+    checked against its source."""
     plan = pkg.StridedPlan([pkg.StridedEntry(src.data_ptr(), dst.data_ptr(), src.numel())])
-    t = min(timed_events(torch, lambda: pkg.copy_strided(plan, stream=stream), reps, stream)
+    t = min(timed_each(torch, lambda: pkg.copy_strided(plan, stream=stream), reps, stream)
             for _ in range(3))
     torch.cuda.synchronize()
     check(torch.equal(dst, src), "box copy")
@@ -1648,7 +1669,7 @@ def main():
     # A plain runtime device copy of the same byte count (the runtime's blit
     # kernel), and the calibration kernel for the FETCH_SIZE / WRITE_SIZE
     # counters.
-    t_copy = timed_events(torch, lambda: copy_dst.copy_(staging), max(3, args.sub_steps // 4),
+    t_copy = timed_each(torch, lambda: copy_dst.copy_(staging), max(3, args.sub_steps // 4),
                           ks_stream)
     hbm_copy_gbps = 2 * staging.numel() / t_copy / 1e9
     log(f"runtime device copy of {staging.numel() >> 20} MiB: {hbm_copy_gbps:.0f} GB/s")
