@@ -74,3 +74,31 @@ def test_pin_current_thread(kvx):
     t.join()
     assert got["cpus"] == want & os.sched_getaffinity(0) or got["cpus"] == want
     assert got["bad"] == 5  # NOT_FOUND: no such node
+
+
+def test_topology_lookups_on_a_two_node_tree(tmp_path):
+    """The GPU-node and CPU-list lookups of libkvx (tests/numa_topology_check.cc)
+    against a made-up sysfs tree of a two-node machine: this machine may have
+    one node, so the two-node cases are checked on the lookups themselves."""
+    import shutil
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    cxx = shutil.which("g++") or shutil.which("c++")
+    libdir = os.path.join(root, "tpu-sync_amd")
+    if cxx is None or not os.path.exists(os.path.join(libdir, "libkvx.so")):
+        pytest.skip("no C++ compiler or libkvx.so not built")
+    exe = tmp_path / "numa_topology_check"
+    env = {k: v for k, v in os.environ.items() if k != "LD_PRELOAD"}
+    r = subprocess.run([cxx, "-O1", "-std=c++17", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                        "-I/opt/rocm/include",
+                        "-I", os.path.join(root, "tpu-sync_amd", "csrc", "host"),
+                        os.path.join(root, "tests", "numa_topology_check.cc"), "-o", str(exe),
+                        "-L", libdir, "-lkvx", f"-Wl,-rpath,{libdir}"],
+                       capture_output=True, text=True, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    tree = tmp_path / "sys"
+    tree.mkdir()
+    r = subprocess.run([str(exe), str(tree)], capture_output=True, text=True, timeout=60, env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all checks passed" in r.stdout
+
