@@ -149,6 +149,41 @@ def test_fp8_device_gather_moves_scales_in_the_same_launch(kvx, oracle, cuda):
     mgr.close()
 
 
+@pytest.mark.parametrize("heads", [1, 5, 8])
+def test_fp8_scale_rows_of_any_width(kvx, oracle, cuda, heads):
+    """Scale rows of 4, 20 and 32 bytes: the launch's vector width follows
+    the narrowest row (4-byte vectors for 4 and 20), payload included, and
+    the scale piece still moves in the payload's launch."""
+    rng = np.random.default_rng(44 + heads)
+    layers, blocks, n = 2, 48, 17
+    kv_np, sc_np, kv, sc, bb = build(rng, cuda, layers, blocks, heads=heads)
+    mgr = kvx.KVCacheManager(kv, host_blocks_to_allocate=32, scale_tables=sc)
+    assert mgr.block_bytes(2 * layers) == 4 * heads
+    ids = rng.choice(blocks, n, replace=False).tolist()
+    staging = torch.zeros(2 * layers * n * bb + layers * n * 4 * heads, dtype=torch.uint8,
+                          device=cuda)
+    before = mgr.engine_stats()["kernel_launches"]
+    mgr.gather(ids, staging).Await()
+    assert mgr.engine_stats()["kernel_launches"] - before == 1
+    rc, want_kv = oracle.extract(kv_np, bb, ids)
+    assert rc == 0
+    rc, want_sc = oracle.extract([u8(a) for a in sc_np], 4 * heads, ids)
+    assert rc == 0
+    got = staging.cpu().numpy()
+    assert np.array_equal(got[:want_kv.size], want_kv)
+    assert np.array_equal(got[want_kv.size:], want_sc)
+    dst = [i for i in range(blocks) if i not in ids][:n]
+    mgr.scatter(dst, staging).Await()
+    torch.cuda.synchronize()
+    for k, a in enumerate(kv_np + sc_np):
+        assert np.array_equal(u8((kv + sc)[k].cpu().numpy()[dst]), u8(a[ids])), k
+    # Untouched blocks keep their bytes.
+    rest = [i for i in range(blocks) if i not in dst]
+    for k, a in enumerate(kv_np + sc_np):
+        assert np.array_equal(u8((kv + sc)[k].cpu().numpy()[rest]), u8(a[rest])), k
+    mgr.close()
+
+
 def test_fp8_llama3_8b_pool_full_size_round_trip(kvx, cuda):
     """32 layers x 16384 blocks of fp8 KV (16 GiB) plus 32 scale tables: a
     512-block offload into a host slot and a reload into 512 other random
