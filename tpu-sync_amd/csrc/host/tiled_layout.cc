@@ -304,16 +304,17 @@ Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int6
   int v = WidestVector(tiled | linear, p.vec);
   // Packed units: one lane per unit with units of one 16-byte tiled vector
   // (v = 16 / P), except that detiling at 16-byte rows goes two lanes per
-  // unit for pairs (P = 2) and four for quads (P = 4). Measured on the Llama-3-8B set (bf16, P = 2), one
-  // process, one launch each: tiling 79.2 % of HBM peak at v = 8 against
-  // 76.7 % with two lanes per 16-byte unit and 67.8 % with one lane per
-  // 16-byte unit (each 16-byte tiled store of a wave then leaves 16-byte
-  // holes); detiling 77.0 % with two lanes against 75.7 % at v = 8. For
-  // int8 (P = 4) at 16-byte rows, detiling: four lanes per 64-byte unit
-  // exchanging through LDS (each wave then writes 1 KiB of one row per
-  // store) 71.6 % against 61.8 % for one lane per 16-byte tiled vector;
-  // tiling keeps one lane per tiled vector (72.3 % against 67.0 % through
-  // LDS).
+  // unit for pairs (P = 2) and four for quads (P = 4), exchanging through
+  // LDS so that each wave writes 1 KiB of one row per store. Measured on the
+  // Llama-3-8B set (bf16, P = 2), one process, one launch each: tiling
+  // 79.2 % of HBM peak at v = 8 against 76.7 % with two lanes per 16-byte
+  // unit and 67.8 % with one lane per 16-byte unit (each 16-byte tiled store
+  // of a wave then leaves 16-byte holes); detiling 77.0 % with two lanes
+  // (exchanging within the lane pair) against 75.7 % at v = 8, and 79.6
+  // against 78.4 % for the LDS exchange over the lane-pair one. For int8
+  // (P = 4) at 16-byte rows, detiling: 71.6 % through LDS against 61.8 % for
+  // one lane per 16-byte tiled vector; tiling keeps one lane per tiled
+  // vector (72.3 % against 67.0 % through LDS).
   bool two_lanes = false, four_lanes = false;
   if (p.P == 2 && !tile && v == 16) {
     two_lanes = true;
