@@ -562,16 +562,22 @@ def verify_round_trip(torch, mgr, storages, src, host, dst):
 def box_copy(torch, pkg, src, dst, reps, stream):
     """The box's streaming-copy yardstick: the library's strided kernel over
     one contiguous entry (src -> dst, the same bytes as a gather launch),
-    timed by HIP events around each launch on the stream it runs on, as the
-    block-copy launches are; read + write bytes per second. The copy is
-    checked against its source."""
-    plan = pkg.StridedPlan([pkg.StridedEntry(src.data_ptr(), dst.data_ptr(), src.numel())])
-    t = min(timed_each(torch, lambda: pkg.copy_strided(plan, stream=stream), reps, stream)
-            for _ in range(3))
+    timed by HIP events right around each launch on the stream it runs on,
+    as the block-copy launches are; read + write bytes per second (the best
+    of 3 rounds). The copy is checked against its source."""
+    plan = pkg.StridedPlan([pkg.StridedEntry(src.data_ptr(), dst.data_ptr(), src.numel())],
+                           profile_kernels=True)
+    pkg.copy_strided(plan, stream=stream).Await()
+    plan.kernel_times(reset=True)
+    best = 0.0
+    for _ in range(3):
+        for f in [pkg.copy_strided(plan, stream=stream) for _ in range(reps)]:
+            f.Await()
+        best = max(best, kernel_gbps(plan.kernel_times(reset=True)) or 0.0)
     torch.cuda.synchronize()
     check(torch.equal(dst, src), "box copy")
     plan.close()
-    return 2 * src.numel() / t / 1e9
+    return best
 
 
 def frac_of_box(gbps, box_gbps):

@@ -933,6 +933,15 @@ int kvx_strided_plan_create(int32_t device, const kvx_strided_entry* entries, in
                             kvx_strided_plan** out);
 int kvx_strided_plan_run(kvx_strided_plan* p, void* stream, kvx_future** out);
 void kvx_strided_plan_destroy(kvx_strided_plan* p);
+/* Kernel timing of a plan's runs (no reference counterpart; the manager's
+ * and the weight synchronizer's profile_kernels for plans): with on = 1 each
+ * later run records a pair of HIP timing events right around its launch on
+ * its stream. kernel_times returns the launches, summed duration (ms) and
+ * algorithmic HBM bytes (2 x bytes moved) of the profiled runs so far,
+ * waiting for them; reset = 1 drops them afterwards. */
+int kvx_strided_plan_profile(kvx_strided_plan* p, int32_t on);
+int kvx_strided_plan_kernel_times(kvx_strided_plan* p, int32_t reset, int64_t* out_launches,
+                                  double* out_total_ms, int64_t* out_bytes);
 
 /*
  * Raw device kernels (no manager): gather / scatter block ids of W storages.

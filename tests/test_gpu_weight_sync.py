@@ -108,6 +108,35 @@ def test_strided_plan_matches_oracle_on_every_run(kvx, cuda):
     empty.close()
 
 
+def test_strided_plan_kernel_times(kvx, cuda):
+    """A plan made with profile_kernels times each run's launch: launches,
+    a positive duration and 2 x the bytes its entries move per run, counted
+    while the copies stay byte-exact; reset drops the samples."""
+    src = torch.randint(0, 256, (3 << 20,), dtype=torch.uint8, device=cuda)
+    dst = torch.zeros_like(src)
+    entries = [kvx.StridedEntry(src.data_ptr(), dst.data_ptr(), 1 << 20),
+               kvx.StridedEntry(src.data_ptr() + (1 << 20), dst.data_ptr() + (1 << 20),
+                                4096, 256, 4096, 4096)]
+    per_run = (1 << 20) + 4096 * 256
+    plan = kvx.StridedPlan(entries, profile_kernels=True)
+    assert plan.kernel_times() == {"launches": 0, "total_ms": 0.0, "bytes": 0}
+    s = torch.cuda.Stream(cuda)
+    for _ in range(3):
+        kvx.copy_strided(plan, stream=s, device=0).Await()
+    kt = plan.kernel_times()
+    assert kt["launches"] == 3 and kt["bytes"] == 3 * 2 * per_run and kt["total_ms"] > 0, kt
+    assert plan.kernel_times(reset=True)["launches"] == 3
+    assert plan.kernel_times()["launches"] == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:per_run], src[:per_run])
+    assert not dst[per_run:].any()
+    plain = kvx.StridedPlan(entries)
+    kvx.copy_strided(plain, stream=s, device=0).Await()
+    assert plain.kernel_times()["launches"] == 0
+    plan.close()
+    plain.close()
+
+
 def _tensors(rng, cuda, sizes, dtype=torch.bfloat16):
     out = []
     for n in sizes:

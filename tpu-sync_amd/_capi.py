@@ -378,6 +378,9 @@ PROTOTYPES = {
                                        ctypes.POINTER(_vp)]),
     "kvx_strided_plan_run": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
     "kvx_strided_plan_destroy": (None, [_vp]),
+    "kvx_strided_plan_profile": (_int, [_vp, _i32]),
+    "kvx_strided_plan_kernel_times": (_int, [_vp, _i32, _i64p, ctypes.POINTER(ctypes.c_double),
+                                             _i64p]),
     "kvx_tiled_buffer_elements": (_int, [ctypes.POINTER(TiledLayoutC), ctypes.POINTER(_i64)]),
     "kvx_tile_buffer": (_int, [_i32, ctypes.POINTER(TiledLayoutC), _u64, _u64, _vp,
                                ctypes.POINTER(_vp)]),

@@ -298,4 +298,18 @@ int kvx_strided_plan_run(kvx_strided_plan* p, void* stream, kvx_future** out) {
 
 void kvx_strided_plan_destroy(kvx_strided_plan* p) { delete p; }
 
+int kvx_strided_plan_profile(kvx_strided_plan* p, int32_t on) {
+  if (p == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null handle");
+  p->impl->SetProfiling(on != 0);
+  return KVX_OK;
+}
+
+int kvx_strided_plan_kernel_times(kvx_strided_plan* p, int32_t reset, int64_t* out_launches,
+                                  double* out_total_ms, int64_t* out_bytes) {
+  if (p == nullptr || out_launches == nullptr || out_total_ms == nullptr || out_bytes == nullptr) {
+    return Fail(KVX_INVALID_ARGUMENT, "null handle or output");
+  }
+  return Done(p->impl->KernelTimes(reset != 0, out_launches, out_total_ms, out_bytes));
+}
+
 }  // extern "C"

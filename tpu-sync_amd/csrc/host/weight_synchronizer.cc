@@ -481,6 +481,9 @@ StatusOr<std::unique_ptr<StridedCopyPlan>> StridedCopyPlan::Create(
     }
   }
   p->n_ = static_cast<uint32_t>(table.size());
+  for (const StridedCopy& c : copies) {
+    p->bytes_ += c.size * (c.count <= 0 ? 1 : c.count);
+  }
   if (p->grid_ == 0) return p;
   DeviceGuard g(device);
   if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
@@ -498,7 +501,42 @@ StridedCopyPlan::~StridedCopyPlan() {
     (void)hipEventSynchronize(e);
     (void)hipEventDestroy(e);
   }
+  for (auto& s : samples_) {
+    (void)hipEventSynchronize(s.second);
+    (void)hipEventDestroy(s.first);
+    (void)hipEventDestroy(s.second);
+  }
   if (image_ != nullptr) (void)hipFree(image_);
+}
+
+void StridedCopyPlan::SetProfiling(bool on) {
+  std::lock_guard<std::mutex> l(mu_);
+  profile_ = on;
+}
+
+Status StridedCopyPlan::KernelTimes(bool reset, int64_t* launches, double* ms, int64_t* bytes) {
+  DeviceGuard g(device_);
+  if (!g.ok()) return InvalidArgumentError("cannot select HIP device");
+  std::lock_guard<std::mutex> l(mu_);
+  *launches = 0;
+  *ms = 0;
+  *bytes = 0;
+  for (auto& s : samples_) {
+    KVX_HIP_RETURN_IF_ERROR(hipEventSynchronize(s.second));
+    float t = 0;
+    KVX_HIP_RETURN_IF_ERROR(hipEventElapsedTime(&t, s.first, s.second));
+    ++*launches;
+    *ms += t;
+    *bytes += 2 * bytes_;
+  }
+  if (reset) {
+    for (auto& s : samples_) {
+      (void)hipEventDestroy(s.first);
+      (void)hipEventDestroy(s.second);
+    }
+    samples_.clear();
+  }
+  return OkStatus();
 }
 
 StatusOr<CopyFuture> StridedCopyPlan::Run(hipStream_t stream) {
@@ -524,11 +562,31 @@ StatusOr<CopyFuture> StridedCopyPlan::Run(hipStream_t stream) {
       return ran.status();
     }
     runs_.push_back(ran.value());
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (profile_ && (hipEventCreate(&t0) != hipSuccess || hipEventCreate(&t1) != hipSuccess ||
+                     hipEventRecord(t0, stream) != hipSuccess)) {
+      // Profiling is best effort: this run goes unsampled.
+      (void)hipGetLastError();
+      if (t0 != nullptr) (void)hipEventDestroy(t0);
+      if (t1 != nullptr) (void)hipEventDestroy(t1);
+      t0 = t1 = nullptr;
+    }
     const hipError_t e = LaunchStridedCopy(static_cast<const StridedEntryDev*>(image_), n_,
                                            grid_, vec_, stream);
     if (e != hipSuccess) {
+      if (t0 != nullptr) (void)hipEventDestroy(t0);
+      if (t1 != nullptr) (void)hipEventDestroy(t1);
       (void)hipEventDestroy(done);
       return HipStatus(e, "strided copy launch");
+    }
+    if (t0 != nullptr) {
+      if (hipEventRecord(t1, stream) == hipSuccess) {
+        samples_.emplace_back(t0, t1);
+      } else {
+        (void)hipGetLastError();
+        (void)hipEventDestroy(t0);
+        (void)hipEventDestroy(t1);
+      }
     }
     // The image must outlive the launch: without its event, wait here.
     if (hipEventRecord(ran.value(), stream) != hipSuccess) (void)hipStreamSynchronize(stream);

@@ -33,6 +33,7 @@
 #include <cstdint>
 #include <memory>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "../kernels/strided_copy.h"
@@ -172,6 +173,12 @@ class StridedCopyPlan {
 
   StatusOr<CopyFuture> Run(hipStream_t stream);
   uint32_t workgroups() const { return grid_; }
+  // With profiling on, each later run records a pair of timing events right
+  // around its launch (and nothing else between them) on its stream.
+  void SetProfiling(bool on);
+  // Launches, summed duration and algorithmic HBM bytes (2 x bytes moved)
+  // of the profiled runs so far; waits for them; reset drops them.
+  Status KernelTimes(bool reset, int64_t* launches, double* ms, int64_t* bytes);
 
  private:
   StridedCopyPlan() = default;
@@ -179,9 +186,12 @@ class StridedCopyPlan {
   int vec_ = 16;
   uint32_t n_ = 0;
   uint32_t grid_ = 0;
+  int64_t bytes_ = 0;  // bytes one run moves
   void* image_ = nullptr;
   std::mutex mu_;
   std::vector<hipEvent_t> runs_;  // one per run that may still read the image
+  bool profile_ = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> samples_;  // (start, stop) per profiled run
 };
 
 }  // namespace kvx

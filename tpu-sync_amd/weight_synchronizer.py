@@ -105,9 +105,10 @@ class StridedPlan:
     plan's runs; close() (or garbage collection) frees the device tables
     after the runs in flight."""
 
-    def __init__(self, entries: Sequence[StridedEntry]):
+    def __init__(self, entries: Sequence[StridedEntry], profile_kernels: bool = False):
         import numpy as np
         self.n = len(entries)
+        self._profile = bool(profile_kernels)
         self._arr = (_capi.StridedEntryC * max(self.n, 1))()
         self._device_plans = {}  # device -> kvx_strided_plan handle
         if self.n:
@@ -125,7 +126,21 @@ class StridedPlan:
                                                              ctypes.byref(h)),
                         "StridedPlan")
             self._device_plans[device] = h
+            if self._profile:
+                _capi.check(_capi.load().kvx_strided_plan_profile(h, 1), "StridedPlan profile")
         return h
+
+    def kernel_times(self, reset: bool = False, device: int = 0) -> dict:
+        """With profile_kernels: launches, summed duration (ms, HIP events right
+        around each launch on its stream) and algorithmic HBM bytes (2 x bytes
+        moved) of the plan's runs on `device` so far."""
+        h = self._device_plans.get(device)
+        if h is None:
+            return {"launches": 0, "total_ms": 0.0, "bytes": 0}
+        n, ms, nb = ctypes.c_int64(), ctypes.c_double(), ctypes.c_int64()
+        _capi.check(_capi.load().kvx_strided_plan_kernel_times(
+            h, int(reset), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(nb)), "kernel_times")
+        return {"launches": n.value, "total_ms": ms.value, "bytes": nb.value}
 
     def close(self) -> None:
         plans, self._device_plans = getattr(self, "_device_plans", {}), {}
