@@ -315,8 +315,9 @@ int32_t kvx_manager_lane_dma_engines(kvx_manager* m);
 int kvx_manager_stream_placement(kvx_manager* m, int32_t* out2);
 /* The same probe over a caller's streams (hipStream_t values, n <= 64) of the
  * current device (no reference counterpart): *pairs_out = pairs that ran one
- * after the other, i.e. share a hardware queue. For a framework that wants
- * its own streams off the library's queues. */
+ * after the other, i.e. share a hardware queue; a stream of another device
+ * is refused with INVALID_ARGUMENT. For a framework that wants its own
+ * streams off the library's queues. */
 int kvx_probe_stream_queues(const uint64_t* streams, int32_t n, int32_t* pairs_out);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the

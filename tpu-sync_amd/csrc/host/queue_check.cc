@@ -75,6 +75,18 @@ StatusOr<std::vector<std::pair<int, int>>> SerializedStreamPairs(
   if (n < 2) return pairs;
   int device = 0;
   KVX_HIP_RETURN_IF_ERROR(hipGetDevice(&device));
+  // The probes write this device's buffer: every stream must belong to it.
+  for (hipStream_t st : streams) {
+    hipDevice_t sd = -1;
+    if (hipStreamGetDevice(st, &sd) != hipSuccess) {
+      (void)hipGetLastError();
+      return InvalidArgumentError("stream probe: not a valid stream");
+    }
+    if (sd != device) {
+      return InvalidArgumentError("stream probe: a stream of device " + std::to_string(sd) +
+                                  ", not of the current device " + std::to_string(device));
+    }
+  }
   int khz = 0;
   if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device) != hipSuccess ||
       khz <= 0) {
