@@ -184,6 +184,61 @@ def test_fp8_scale_rows_of_any_width(kvx, oracle, cuda, heads):
     mgr.close()
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_payload_and_side_tables_of_random_shapes(kvx, oracle, cuda, seed):
+    """Random payload block sizes (16-, 4- and 2-byte multiples, so every
+    vector width of the one-launch kernel) with side tables of 1-64 fp32 per
+    block, random ids and small staging chunks that cut payload pieces inside
+    storages: staged offload + reload and device gather + scatter, all
+    against the oracle."""
+    rng = np.random.default_rng(900 + seed)
+    layers = int(rng.integers(1, 4))
+    blocks, n = 40, int(rng.integers(1, 24))
+    bb = int(rng.choice([8192, 12992, 20000, 32768, 10002, 16388]))
+    k = int(rng.integers(1, 65))
+    kv_np = [rng.integers(0, 256, (blocks, bb), dtype=np.uint8) for _ in range(2 * layers)]
+    sc_np = [fp32_scales(rng, blocks, k) for _ in range(layers)]
+    kv = [torch.from_numpy(a).to(cuda) for a in kv_np]
+    sc = [torch.from_numpy(a).to(cuda) for a in sc_np]
+    chunk = int(rng.integers(2, 6)) * bb + int(rng.integers(0, bb))
+    mgr = kvx.KVCacheManager(kv, host_blocks_to_allocate=32, scale_tables=sc,
+                             transfer_mode="staged", staging_chunk_bytes=chunk, staging_chunks=2)
+    dev = [u8(a).copy() for a in kv_np + sc_np]
+    bbs = [bb] * (2 * layers) + [4 * k] * layers
+    host = [np.zeros(32 * b, np.uint8) for b in bbs]
+    ids = rng.choice(blocks, n, replace=False).tolist()
+    slot = rng.permutation(32)[:n].tolist()
+    mgr.d2h(ids, slot).Await()
+    assert oracle.transfer(True, dev, host, bbs, [d.nbytes for d in dev], ids, slot,
+                           [1] * n) == 0
+    for i in range(3 * layers):
+        assert np.array_equal(mgr.host_view(i), host[i]), i
+    back = rng.choice(blocks, n, replace=False).tolist()
+    mgr.h2d(slot, back).Await()
+    assert oracle.transfer(False, dev, host, bbs, [d.nbytes for d in dev], slot, back,
+                           [1] * n) == 0
+    torch.cuda.synchronize()
+    for i, t in enumerate(kv + sc):
+        assert np.array_equal(u8(t.cpu().numpy()), dev[i]), i
+    # Device gather and scatter of the same storages in one launch each.
+    g_ids = rng.choice(blocks, n, replace=False).tolist()
+    staging = torch.zeros(2 * layers * n * bb + layers * n * 4 * k, dtype=torch.uint8,
+                          device=cuda)
+    mgr.gather(g_ids, staging).Await()
+    want = np.concatenate([u8(a.reshape(blocks, -1)[g_ids]) for a in
+                           [d.reshape(blocks, -1) for d in dev]])
+    assert np.array_equal(staging.cpu().numpy(), want)
+    dst = rng.choice(blocks, n, replace=False).tolist()
+    mgr.scatter(dst, staging).Await()
+    torch.cuda.synchronize()
+    for i, t in enumerate(kv + sc):
+        rows = dev[i].reshape(blocks, -1)
+        rows[dst] = staging.cpu().numpy()[
+            sum(n * b for b in bbs[:i]):sum(n * b for b in bbs[:i + 1])].reshape(n, -1)
+        assert np.array_equal(u8(t.cpu().numpy()), dev[i]), i
+    mgr.close()
+
+
 def test_fp8_llama3_8b_pool_full_size_round_trip(kvx, cuda):
     """32 layers x 16384 blocks of fp8 KV (16 GiB) plus 32 scale tables: a
     512-block offload into a host slot and a reload into 512 other random
