@@ -906,6 +906,48 @@ def test_on_ready_callbacks(kvx, cuda):
     qm.close()
 
 
+@pytest.mark.parametrize("bb", [65536, 131072, 100000, 70004, 262144 + 2])
+def test_blocks_split_over_workgroups_match_oracle(kvx, oracle, cuda, bb):
+    """Blocks larger than one workgroup's pass (32 KiB at 16-byte vectors,
+    8 KiB at 4-byte, 2 KiB at 1-byte) go to consecutive workgroups, a pass
+    each, the last one short when the block is not a whole number of passes:
+    device gather and scatter (storage pairs / all storages), staged offload
+    and reload through small staging chunks, and zero-copy (whose capped grid
+    keeps one workgroup per block), all against the oracle."""
+    rng = np.random.default_rng(bb % 1000)
+    layers, P, n = 2, 24, 9
+    host, dev = dev_pools(rng, cuda, layers, 1, P, bb)
+    for mode in ("staged", "zero_copy"):
+        mgr = make_mgr(kvx, dev, 16, transfer_mode=mode, staging_chunk_bytes=3 * bb,
+                       staging_chunks=2)
+        ids = rng.choice(P, n, replace=False).tolist()
+        if mode == "staged":
+            stg = torch.zeros(layers * n * bb, dtype=torch.uint8, device=cuda)
+            mgr.gather(ids, stg).Await()
+            got = dev_np(stg).reshape(layers, n, bb)
+            for l in range(layers):
+                assert np.array_equal(got[l], dev_np(dev[l][0])[ids]), (l, mode)
+            dst = [i for i in range(P) if i not in ids][:n]
+            mgr.scatter(dst, stg).Await()
+            for l in range(layers):
+                assert np.array_equal(dev_np(dev[l][0])[dst], got[l]), (l, mode)
+        cur = [dev_np(dev[l][0]).reshape(-1).copy() for l in range(layers)]
+        hostm = [np.zeros(16 * bb, np.uint8) for _ in range(layers)]
+        slot = rng.permutation(16)[:n].tolist()
+        mgr.d2h(ids, slot).Await()
+        assert oracle.transfer(True, cur, hostm, [bb] * layers, [c.nbytes for c in cur],
+                               ids, slot, [1] * n) == 0
+        for l in range(layers):
+            assert np.array_equal(mgr.host_view(l), hostm[l]), (l, mode)
+        back = rng.choice(P, n, replace=False).tolist()
+        mgr.h2d(slot, back).Await()
+        assert oracle.transfer(False, cur, hostm, [bb] * layers, [c.nbytes for c in cur],
+                               slot, back, [1] * n) == 0
+        for l in range(layers):
+            assert np.array_equal(dev_np(dev[l][0]).reshape(-1), cur[l]), (l, mode)
+        mgr.close()
+
+
 @pytest.mark.parametrize("cap", [0, -1, 1, 8])
 @pytest.mark.parametrize("layers", [3, 4])
 def test_gather_scatter_every_block_of_the_pool(kvx, cuda, layers, cap):

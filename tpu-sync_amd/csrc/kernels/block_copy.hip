@@ -251,13 +251,23 @@ struct FastParams {
   uint32_t elems;
   uint32_t wstorages;  // whole-storage orders: storages in the launch
   uint32_t w0;         // whole-storage orders: first storage (f0 = w0 * n)
+  uint32_t pieces;     // workgroups per block (1, or blocks above kUnroll * kThreads vectors)
+  uint32_t piece_elems;  // vectors per workgroup when pieces > 1
 };
 
 enum FastOrder : int { kStorageMajor = 0, kStoragePairs = 1, kAllStorages = 2 };
 
-// Block g of a fast launch (one workgroup, one whole block).
+// Workgroup g of a fast launch: one whole block, or with pieces > 1 one
+// piece of piece_elems vectors of a block, the pieces of a block on
+// consecutive workgroups (so a large block's writes are in flight together).
 template <typename V, bool kGather, int kUnroll, int kOrder>
 __device__ __forceinline__ void fast_block(const FastParams& P, uint32_t g) {
+  uint32_t piece = 0;
+  if (P.pieces > 1) {
+    const uint32_t b = g / P.pieces;
+    piece = g - b * P.pieces;
+    g = b;
+  }
   uint32_t w, i;
   if (kOrder == kAllStorages) {
     i = g / P.wstorages;
@@ -281,10 +291,14 @@ __device__ __forceinline__ void fast_block(const FastParams& P, uint32_t g) {
   const uint64_t base = uniform_load<uint64_t>(P.storages, w);
   const int64_t id = uniform_load<int64_t>(reinterpret_cast<uint64_t>(P.ids), i);
   const bool bad = bad_id(id, P.pool_blocks);
-  const uint32_t elems = bad ? 0u : P.elems;
-  KVX_GLOBAL V* pool = gptr<V>(base) + static_cast<uint64_t>(bad ? 0 : id) * P.elems;
+  const uint32_t first = piece * P.piece_elems;  // 0 unless the block is split
+  const uint32_t left = P.elems - first;
+  const uint32_t span = P.pieces > 1 && left > P.piece_elems ? P.piece_elems : left;
+  const uint32_t elems = bad ? 0u : span;
+  KVX_GLOBAL V* pool =
+      gptr<V>(base) + static_cast<uint64_t>(bad ? 0 : id) * P.elems + first;
   KVX_GLOBAL V* stg = gptr<V>(P.staging + w * static_cast<uint64_t>(P.stride_w) +
-                              i * static_cast<uint64_t>(P.stride_i));
+                              i * static_cast<uint64_t>(P.stride_i)) + first;
   if (kGather) {
     copy_whole_block<V, kUnroll>(pool, stg, elems);
   } else {
@@ -423,6 +437,8 @@ bool BuildFastParams(const KParams& K, CopyDir dir, FastParams* F, int* order) {
   }
   F->wstorages = W;
   F->w0 = p.f0 / K.n;
+  F->pieces = 1;
+  F->piece_elems = p.elems;
   return true;
 }
 
@@ -452,7 +468,20 @@ hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, int wg_per_cu,
                   bool capped_grid, hipStream_t stream) {
   FastParams F;
   int order = kStorageMajor;
+  // Blocks above one workgroup's pass (kUnroll * kThreads vectors, 32 KiB at
+  // 16-byte vectors) go to consecutive workgroups a pass each, unless the
+  // launch's grid is capped (zero-copy copies keep their few workgroups).
+  auto split = [&](FastParams* f, uint32_t blocks, uint32_t* g) {
+    const uint32_t pass = kUnroll * kThreads;
+    if (capped_grid || f->elems <= pass) return;
+    const uint64_t pieces = (static_cast<uint64_t>(f->elems) + pass - 1) / pass;
+    if (static_cast<uint64_t>(blocks) * pieces + (*g - blocks) > INT32_MAX) return;
+    f->pieces = static_cast<uint32_t>(pieces);
+    f->piece_elems = pass;
+    *g = *g - blocks + blocks * f->pieces;
+  };
   if (BuildFastParams(P, dir, &F, &order)) {
+    split(&F, grid, &grid);
     // Gathers reserve (unused) LDS to cap their workgroups per CU.
     const uint32_t lds = wg_per_cu > 0 ? kLdsPerCu / static_cast<uint32_t>(wg_per_cu) : 0;
     if (dir == CopyDir::kGather && order == kStoragePairs) {
@@ -479,6 +508,7 @@ hipError_t Launch(const KParams& P, uint32_t grid, CopyDir dir, int wg_per_cu,
   KPiece side;
   uint32_t side_wgs = 0;
   if (BuildFastSideParams(P, dir, &F, &side, &side_wgs, &order)) {
+    split(&F, grid - side_wgs, &grid);
     if (dir == CopyDir::kGather && order == kStoragePairs) {
       hipLaunchKernelGGL((block_copy_fast_side_kernel<V, true, kUnroll, kStoragePairs>),
                          dim3(grid), dim3(kThreads), glds, stream, F, side, side_wgs);
