@@ -319,6 +319,20 @@ int kvx_manager_stream_placement(kvx_manager* m, int32_t* out2);
  * is refused with INVALID_ARGUMENT. For a framework that wants its own
  * streams off the library's queues. */
 int kvx_probe_stream_queues(const uint64_t* streams, int32_t n, int32_t* pairs_out);
+/* Pinned-host <-> device copy rates of the current device on the SDMA
+ * engines the pageable lanes use (no reference counterpart: a measurement of
+ * the link for a caller's bounds). Copies of `bytes` (1..16 GiB) between a
+ * device buffer and a pinned host buffer, the best of 3 rounds of `reps`
+ * (1..1000) copies: out3[0] = device-to-host GB/s alone, out3[1] =
+ * host-to-device alone, out3[2] = both at once (bytes of both / time);
+ * *engines_out (may be null) = the device-to-host engine bit << 16 | the
+ * host-to-device engine bit. Allocates 2 x bytes of device and of pinned
+ * host memory for the call; the bytes moved are checked. UNAVAILABLE when
+ * ROCr offers no SDMA engine for host copies. hipMemcpyAsync leaves the
+ * engine to the runtime, which in some processes runs a host-to-device and a
+ * device-to-host copy issued together one after the other on one engine. */
+int kvx_measure_link_peaks(uint64_t bytes, int32_t reps, double* out3,
+                           uint32_t* engines_out);
 /* With profile_kernels set: launches, summed duration (ms, from HIP events
  * on the kernel's stream) and algorithmic HBM bytes (2 x bytes moved) of the
  * gather (gather = 1) or scatter (gather = 0) kernels so far. Waits for the

@@ -187,3 +187,18 @@ def test_weight_sync_layouts_must_match_the_tensors(kvx):
         kvx.WeightSynchronizer([[t], [t]], layouts=[[L]])
     with pytest.raises(RuntimeError, match="layouts must match"):
         kvx.WeightSynchronizer([[t, t]], layouts=[[L]])
+
+
+def test_link_peaks_validate_arguments_before_the_device(kvx):
+    """kvx_measure_link_peaks rejects a null output, zero or more than 16 GiB
+    of bytes and reps outside 1..1000 with INVALID_ARGUMENT before it touches
+    a device."""
+    lib = kvx._capi.load()
+    out = (ctypes.c_double * 3)()
+    for nbytes, reps in [(0, 5), ((16 << 30) + 1, 5), (1 << 20, 0), (1 << 20, 1001),
+                         (1 << 20, -1)]:
+        assert lib.kvx_measure_link_peaks(nbytes, reps, out, None) == 3, (nbytes, reps)
+        assert lib.kvx_last_error()
+    assert lib.kvx_measure_link_peaks(1 << 20, 5, None, None) == 3
+    with pytest.raises(kvx.KvxError):
+        kvx.measure_link_peaks(0, 5)

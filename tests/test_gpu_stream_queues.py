@@ -55,3 +55,18 @@ def test_probe_rejects_more_than_64_streams(kvx, cuda):
     s = torch.cuda.Stream(cuda)
     with pytest.raises(kvx.KvxError):
         kvx.probe_stream_queues([s] * 65)
+
+
+def test_link_peaks_on_the_lanes_engines(kvx, cuda):
+    """Pinned copies on the lanes' fixed SDMA engines, one direction at a
+    time and both at once: rates in a plausible range (the call checks that
+    the bytes landed), both at once never much below one direction alone,
+    and one engine bit per direction."""
+    r = kvx.measure_link_peaks(64 << 20, 3)
+    print(r, flush=True)
+    for k in ("d2h_gbps", "h2d_gbps", "bidir_gbps"):
+        assert 1.0 < r[k] < 1000.0, r
+    assert r["bidir_gbps"] >= 0.9 * max(r["d2h_gbps"], r["h2d_gbps"]), r
+    d2h_bit, h2d_bit = r["engines"] >> 16, r["engines"] & 0xFFFF
+    for bit in (d2h_bit, h2d_bit):
+        assert bit != 0 and bit & (bit - 1) == 0, r

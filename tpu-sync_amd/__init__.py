@@ -7,7 +7,7 @@ this package is a thin ctypes layer that only passes pointers.
 from . import _capi
 from ._capi import KvxError
 from .kv_cache_manager import (KVCacheManager, LogicalBlockManager, RaidenFuture,
-                               probe_stream_queues)
+                               probe_stream_queues, measure_link_peaks)
 from .kv_cache_store import (BlockStatus, KVCacheMetadata, KVCacheMetadataShmRegion,
                              KVCacheStore, LRUCache, RaidenBlockId, RaidenId)
 from . import copy_plan, pool_layout, tiling, transport
@@ -15,7 +15,7 @@ from .pool_layout import PoolSpec, RegionSpec
 from .weight_synchronizer import (StridedEntry, StridedPlan, WeightSynchronizer,
                                   column_split_entries, compute_nd_shard_slices, copy_strided)
 
-__all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError", "probe_stream_queues",
+__all__ = ["KVCacheManager", "LogicalBlockManager", "RaidenFuture", "KvxError", "probe_stream_queues", "measure_link_peaks",
            "KVCacheStore", "RaidenId", "RaidenBlockId", "BlockStatus", "LRUCache",
            "KVCacheMetadata", "KVCacheMetadataShmRegion", "WeightSynchronizer",
            "StridedEntry", "StridedPlan", "copy_strided", "column_split_entries",

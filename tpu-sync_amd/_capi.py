@@ -268,6 +268,8 @@ PROTOTYPES = {
     "kvx_manager_lane_dma_engines": (ctypes.c_int32, [_vp]),
     "kvx_manager_stream_placement": (_int, [_vp, _i32p]),
     "kvx_probe_stream_queues": (_int, [_u64p, _i32, _i32p]),
+    "kvx_measure_link_peaks": (_int, [ctypes.c_uint64, _i32, ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_uint32)]),
     "kvx_manager_kernel_times": (_int, [_vp, _i32, _i32, _i64p,
                                         ctypes.POINTER(ctypes.c_double), _i64p]),
     "kvx_future_is_ready": (_int, [_vp]),

@@ -11,6 +11,7 @@
 #include "../host/device_memory.h"
 #include "../host/hip_util.h"
 #include "../host/kv_cache_store.h"
+#include "../host/link_peaks.h"
 #include "../host/numa.h"
 #include "../host/queue_check.h"
 #include "../host/raiden_env.h"
@@ -548,6 +549,18 @@ int kvx_probe_stream_queues(const uint64_t* streams, int32_t n, int32_t* pairs_o
   auto pairs = kvx::SerializedStreamPairs(ss);
   if (!pairs.ok()) return Fail(pairs.status());
   *pairs_out = static_cast<int32_t>(pairs->size());
+  return KVX_OK;
+}
+
+int kvx_measure_link_peaks(uint64_t bytes, int32_t reps, double* out3,
+                           uint32_t* engines_out) {
+  if (out3 == nullptr) return Fail(KVX_INVALID_ARGUMENT, "null output");
+  auto r = kvx::MeasureLinkPeaks(static_cast<size_t>(bytes), reps);
+  if (!r.ok()) return Fail(r.status());
+  out3[0] = r->d2h_gbps;
+  out3[1] = r->h2d_gbps;
+  out3[2] = r->bidir_gbps;
+  if (engines_out != nullptr) *engines_out = r->engines;
   return KVX_OK;
 }
 

@@ -108,6 +108,21 @@ def probe_stream_queues(streams) -> int:
     return int(out.value)
 
 
+
+def measure_link_peaks(nbytes: int = 1 << 30, reps: int = 5) -> dict:
+    """Pinned-host <-> device copy rates (GB/s) of the current device on the
+    SDMA engines the pageable lanes use: device-to-host and host-to-device
+    alone and both at once, the best of 3 rounds of `reps` copies of `nbytes`
+    (1..16 GiB; 2 x nbytes of device and of pinned host memory are held for
+    the call). `engines`: the device-to-host engine bit << 16 | the
+    host-to-device bit."""
+    out = (ctypes.c_double * 3)()
+    eng = ctypes.c_uint32()
+    _capi.check(_capi.load().kvx_measure_link_peaks(nbytes, reps, out, ctypes.byref(eng)),
+                "kvx_measure_link_peaks")
+    return {"d2h_gbps": out[0], "h2d_gbps": out[1], "bidir_gbps": out[2],
+            "engines": int(eng.value)}
+
 class LogicalBlockManager:
     """Host block allocator (tpu_sync/kv_cache/logical_block_manager.h:35-93)."""
 
