@@ -133,9 +133,10 @@ def parse_args():
     p.add_argument("--zipf-inflight", type=int, default=1,
                    help="requests whose copies may be in flight at once (1: each "
                         "request's load and save finish before the next is issued)")
-    p.add_argument("--zipf-more-inflight", type=int, default=2,
+    p.add_argument("--zipf-more-inflight", default="2,4",
                    help="then continue the churn on the warm tier with this many "
-                        "requests in flight (0 or 1: skip)")
+                        "requests in flight, one run per comma-separated count "
+                        "(counts below 2 are skipped)")
     p.add_argument("--configs-only", action="store_true",
                    help="measure only the --configs workloads (no headline, no CPU "
                         "baseline) and print them; for profiling one of them")
@@ -308,6 +309,27 @@ def pcie_peaks(torch, dev, nbytes=1 << 30, reps=5):
     del h, h2, d, d2
     return out
 
+
+def link_peaks_both_ways(torch, dev, pkg, runtime, nbytes=1 << 30, reps=5):
+    """The pinned peaks by both methods: `runtime` (pcie_peaks: the runtime's
+    hipMemcpyAsync, which picks the DMA engine per copy) and the library's
+    copies on the lanes' fixed SDMA engines (measure_link_peaks). Returns
+    (the best of the two per figure, the figures by method). The runtime has
+    run the two directions of its bidirectional measurement one after the
+    other in some processes (one direction's rate), which the fixed engines
+    do not."""
+    torch.cuda.synchronize()
+    fixed = pkg.measure_link_peaks(nbytes, reps)
+    by = {"runtime_copies": {k: round(v, 2) for k, v in runtime.items()},
+          "fixed_sdma_engines": {"pcie_d2h_gbps": round(fixed["d2h_gbps"], 2),
+                                 "pcie_h2d_gbps": round(fixed["h2d_gbps"], 2),
+                                 "pcie_bidir_gbps": round(fixed["bidir_gbps"], 2),
+                                 "engines": hex(fixed["engines"])}}
+    best = dict(runtime)
+    for k, f in (("pcie_d2h_gbps", "d2h_gbps"), ("pcie_h2d_gbps", "h2d_gbps"),
+                 ("pcie_bidir_gbps", "bidir_gbps")):
+        best[k] = max(best[k], fixed[f])
+    return best, by
 
 def cpu_model():
     try:
@@ -1067,6 +1089,88 @@ def percentiles_ms(xs):
             "p99": round(float(np.percentile(a, 99)), 2), "max": round(float(a[-1]), 2)}
 
 
+def requests_to_keep(window, inflight):
+    """The requests a caller with at most `inflight` in flight may leave in
+    flight after issuing the newest of `window` (oldest first): the newest
+    inflight - 1 of them, or all while there are fewer."""
+    if inflight <= 1:
+        return []
+    return window[max(0, len(window) - (inflight - 1)):]
+
+def pcie_rates(q_load, q_save, peaks):
+    """Bytes/s of the H2D and D2H directions with q_load and q_save bytes
+    queued: a direction alone runs at its pinned peak; both at once share the
+    bidirectional peak in proportion to their queued bytes, each capped at its
+    own peak (the split that drains both queues together)."""
+    h2d, d2h = peaks["pcie_h2d_gbps"] * 1e9, peaks["pcie_d2h_gbps"] * 1e9
+    bidir = peaks["pcie_bidir_gbps"] * 1e9
+    if q_load <= 0 or q_save <= 0:
+        return h2d, d2h
+    rl = bidir * q_load / (q_load + q_save)
+    if rl > h2d:
+        return h2d, min(d2h, bidir - h2d)
+    if bidir - rl > d2h:
+        return min(h2d, bidir - d2h), d2h
+    return rl, bidir - rl
+
+
+def window_bound_gbps(per_request, inflight, peaks, block_bytes):
+    """PCIe bound of a request stream issued as the churn issues it: request
+    j is issued once every request before j - inflight + 1 has finished both
+    copies; its load (H2D) and save (D2H) join their direction's queue at
+    issue and each queue runs in order, at pcie_rates. Host time between
+    requests and per-copy latencies count as zero, so no copy engine can do
+    better under that window. With one in flight this is the per-request
+    bound sum(max(load / H2D, save / D2H, (load + save) / bidir)); with every
+    request issued at once it is the fully overlapped bound."""
+    from collections import deque
+    n = len(per_request)
+    pending = [0] * n  # copies of each request not yet finished
+    loads, saves = deque(), deque()  # [request, bytes left], in issue order
+    q_load = q_save = 0.0
+    t = 0.0
+    issued = oldest = 0  # oldest: first request with a copy unfinished
+    while True:
+        while issued < n and issued - oldest < inflight:
+            nl, ns = per_request[issued]
+            if nl > 0:
+                loads.append([issued, float(nl) * block_bytes])
+                q_load += float(nl) * block_bytes
+                pending[issued] += 1
+            if ns > 0:
+                saves.append([issued, float(ns) * block_bytes])
+                q_save += float(ns) * block_bytes
+                pending[issued] += 1
+            issued += 1
+            while oldest < issued and pending[oldest] == 0:
+                oldest += 1
+        if not loads and not saves:
+            break
+        rl, rs = pcie_rates(q_load, q_save, peaks)
+        dl = loads[0][1] / rl if loads else float("inf")
+        ds = saves[0][1] / rs if saves else float("inf")
+        dt = min(dl, ds)
+        t += dt
+        for q, r, first in ((loads, rl, dl <= ds), (saves, rs, ds <= dl)):
+            if not q:
+                continue
+            q[0][1] = 0.0 if first else q[0][1] - r * dt
+            if q is loads:
+                q_load = max(0.0, q_load - r * dt)
+            else:
+                q_save = max(0.0, q_save - r * dt)
+            if q[0][1] <= 0.0:
+                pending[q.popleft()[0]] -= 1
+        if not loads:
+            q_load = 0.0
+        if not saves:
+            q_save = 0.0
+        while oldest < issued and pending[oldest] == 0:
+            oldest += 1
+    moved = sum(nl + ns for nl, ns in per_request) * block_bytes
+    return moved / t / 1e9 if t > 0 else None
+
+
 def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
     """Llama-3-70B-shaped KV (80 layers, K and V: 160 storages of 12000 x 32
     KiB blocks, 58.6 GiB) with a host LRU tier (default: a /dev/shm segment of
@@ -1201,7 +1305,7 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
             issue.append((time.perf_counter() - t_req, t_load_call, t_save_call))
             # Keep at most `inflight` requests in flight: wait until every
             # copy but those of the newest inflight - 1 requests has landed.
-            keep = window[len(window) - (inflight - 1):] if inflight > 1 else []
+            keep = requests_to_keep(window, inflight)
             poll_until(loaded - sum(x[0] for x in keep), saved - sum(x[1] for x in keep))
             window = keep
             if inflight == 1:
@@ -1286,19 +1390,20 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                                [t for nb, t in latency if nb < 128])}
                           if latency else None),
            "requests_64_to_127_blocks_vs_pcie_bound": small_vs_bound}
-    if args.zipf_more_inflight > 1:
+    more = []
+    for m in (int(x) for x in str(args.zipf_more_inflight).split(",") if x.strip()):
+        if m < 2:
+            continue
         # The same request stream continued on the warm tier with more
-        # requests in flight, as a server with several requests in progress;
-        # it has no per-request PCIe bound (requests overlap).
-        r2 = run(args.zipf_more_inflight, args.zipf_batches)
+        # requests in flight, as a server with several requests in progress.
+        r2 = run(m, args.zipf_batches)
         moved2 = (r2["saved"] + r2["loaded"]) * S * bb
-        out["more_in_flight"] = {
-            "requests_in_flight": args.zipf_more_inflight, "batches": args.zipf_batches,
-            "blocks_saved": r2["saved"], "blocks_loaded": r2["loaded"],
-            "blocks_skipped": r2["skipped"], "device_hits": r2["device_hits"],
-            "hit_rate": round(r2["hits"] / max(r2["asked"], 1), 4),
-            "gbps": round(moved2 / r2["t_run"] / 1e9, 2),
-            "blocks_per_s": round((r2["saved"] + r2["loaded"]) / r2["t_run"], 1)}
+        e = {"requests_in_flight": m, "batches": args.zipf_batches,
+             "blocks_saved": r2["saved"], "blocks_loaded": r2["loaded"],
+             "blocks_skipped": r2["skipped"], "device_hits": r2["device_hits"],
+             "hit_rate": round(r2["hits"] / max(r2["asked"], 1), 4),
+             "gbps": round(moved2 / r2["t_run"] / 1e9, 2),
+             "blocks_per_s": round((r2["saved"] + r2["loaded"]) / r2["t_run"], 1)}
         if peaks:
             # With requests overlapping freely the stream can do no better
             # than all loads on H2D, all saves on D2H and everything on the
@@ -1307,9 +1412,19 @@ def bench_zipf_store(torch, pkg, dev, args, rng, peaks=None):
                        r2["saved"] * S * bb / (peaks["pcie_d2h_gbps"] * 1e9),
                        moved2 / (peaks["pcie_bidir_gbps"] * 1e9))
             if t_lo > 0:
-                out["more_in_flight"]["pcie_bound_overlapped_gbps"] = round(moved2 / t_lo / 1e9, 2)
-                out["more_in_flight"]["frac_of_overlapped_bound"] = round(
-                    moved2 / r2["t_run"] / (moved2 / t_lo), 4)
+                e["pcie_bound_overlapped_gbps"] = round(moved2 / t_lo / 1e9, 2)
+                e["frac_of_overlapped_bound"] = round(moved2 / r2["t_run"] / (moved2 / t_lo), 4)
+            # The bound of this stream under its own window: requests are
+            # issued only as older ones finish, so a direction idles when the
+            # requests in flight have nothing queued for it.
+            wb = window_bound_gbps(r2["per_request"], m, peaks, S * bb)
+            if wb:
+                e["pcie_bound_window_gbps"] = round(wb, 2)
+                e["frac_of_window_bound"] = round(moved2 / r2["t_run"] / 1e9 / wb, 4)
+        more.append(e)
+        log(f"zipf: {m} in flight: {e}")
+    if more:
+        out["more_in_flight"] = more
     # One offload + reload through the same manager and host tier after the
     # churn (its lanes, chunking and /dev/shm tier), checked against torch.
     perm = rng.permutation(P)
@@ -1520,11 +1635,13 @@ def main():
         # no CPU baseline; not the benchmark's result line.
         dev = torch.device("cuda:0")
         # The churn's PCIe bound needs the link's measured peaks.
-        peaks = pcie_peaks(torch, dev) if "zipf" in args.configs.split(",") else None
-        if peaks:
-            log(f"pinned PCIe peaks: {peaks}")
+        peaks = by_method = None
+        if "zipf" in args.configs.split(","):
+            peaks, by_method = link_peaks_both_ways(torch, dev, pkg, pcie_peaks(torch, dev))
+            log(f"pinned PCIe peaks: {by_method}")
         configs = run_configs(torch, pkg, dev, args, np.random.default_rng(1), peaks)
-        print(json.dumps({"configs_only": True, "configs": configs}), flush=True)
+        print(json.dumps({"configs_only": True, "pcie_peaks_by_method": by_method,
+                          "configs": configs}), flush=True)
         return
 
     w = WORKLOADS[args.workload]
@@ -1741,7 +1858,9 @@ def main():
         log("measuring pinned PCIe peaks (after the headline)")
         later = pcie_peaks(torch, dev)
         log(f"pinned PCIe peaks: {later}")
-        measured_peaks = {k: max(v, later[k]) for k, v in measured_peaks.items()}
+        runtime_peaks = {k: max(v, later[k]) for k, v in measured_peaks.items()}
+        measured_peaks, peaks_by_method = link_peaks_both_ways(torch, dev, pkg, runtime_peaks)
+        log(f"pinned PCIe peaks by method: {peaks_by_method}")
         peaks = measured_peaks
         for mode, r in modes.items():
             r["offload_frac_of_pcie_d2h"] = round(r["offload_gbps"] / peaks["pcie_d2h_gbps"], 4)
@@ -1756,6 +1875,7 @@ def main():
             "reload_frac_of_pcie_h2d": modes[args.mode]["reload_frac_of_pcie_h2d"],
             "duplex_frac_of_pcie_bidir": round(value / peaks["pcie_bidir_gbps"], 4),
             **{k: round(v, 2) for k, v in peaks.items()},
+            "pcie_peaks_by_method": peaks_by_method,
             "modes": modes,
         }
         # Short host runs (every host id a run of its own, as a store's
