@@ -124,6 +124,7 @@ _SLICE_DTYPE = np.dtype([("host", "<i4"), ("dev", "<i4"), ("status", "<i4"),
                          ("replica", "<i4"), ("names", "<u8", (3,))])
 assert _SLICE_DTYPE.itemsize == ctypes.sizeof(_capi.BlockSlice)
 _STATUS_BY_VALUE = {int(s): s for s in BlockStatus}
+_STATUS_INT = {s: int(s) for s in BlockStatus}
 
 
 def _c_slices(slices: Sequence):
@@ -131,25 +132,32 @@ def _c_slices(slices: Sequence):
     bare owner): (pointer, count, objects that must outlive the call). Each
     distinct owner's names are encoded once."""
     keep = []
-    owners = {}  # id(RaidenId) -> its three name addresses
-    hosts, devs, stats, reps, names = [], [], [], [], []
+    owners = {}  # id(RaidenId) -> its row in `rows`
+    rows = []  # the three name addresses of each distinct owner
+    hosts, devs, stats, reps, which = [], [], [], [], []
+    last_rid, last_row = None, 0
+    status_int = _STATUS_INT
     for s in slices:
-        if isinstance(s, RaidenId):
+        if type(s) is not RaidenBlockId and isinstance(s, RaidenId):
             s = RaidenBlockId(raiden_id=s)
         rid = s._raiden_id
-        row = owners.get(id(rid))
-        if row is None:
-            encoded = [rid.job_name.encode(), rid.job_replica_id.encode(),
-                       rid.data_name.encode()]
-            keep.extend(encoded)
-            keep.append(rid)  # keeps id(rid) unique while the table is used
-            row = [ctypes.cast(ctypes.c_char_p(b), ctypes.c_void_p).value for b in encoded]
-            owners[id(rid)] = row
+        if rid is not last_rid:
+            row = owners.get(id(rid))
+            if row is None:
+                encoded = [rid.job_name.encode(), rid.job_replica_id.encode(),
+                           rid.data_name.encode()]
+                keep.extend(encoded)
+                keep.append(rid)  # keeps id(rid) unique while the table is used
+                row = len(rows)
+                rows.append([ctypes.cast(ctypes.c_char_p(b), ctypes.c_void_p).value
+                             for b in encoded])
+                owners[id(rid)] = row
+            last_rid, last_row = rid, row
         hosts.append(s._host_block_id)
         devs.append(s._device_block_id)
-        stats.append(s._status)
-        reps.append(rid.data_replica_idx)
-        names.append(row)
+        stats.append(status_int[s._status])
+        reps.append(rid._data_replica_idx)
+        which.append(last_row)
     n = len(hosts)
     raw = np.zeros(max(n, 1), dtype=_SLICE_DTYPE)
     if n:
@@ -157,7 +165,8 @@ def _c_slices(slices: Sequence):
         raw["dev"][:n] = devs
         raw["status"][:n] = stats
         raw["replica"][:n] = reps
-        raw["names"][:n] = names
+        table = np.array([[a or 0 for a in r] for r in rows], dtype=np.uint64)
+        raw["names"][:n] = table[0] if len(rows) == 1 else table[which]
     keep.append(raw)
     return raw.ctypes.data_as(ctypes.POINTER(_capi.BlockSlice)), n, keep
 
@@ -183,25 +192,35 @@ def _take_slices(handle) -> List[Tuple[bytes, RaidenBlockId]]:
                             dtype=_SLICE_DTYPE)
         hosts, devs = raw["host"].tolist(), raw["dev"].tolist()
         stats, reps = raw["status"].tolist(), raw["replica"].tolist()
-        status = [_STATUS_BY_VALUE[v] for v in stats]
-        make = RaidenBlockId._of
+        by_value = _STATUS_BY_VALUE
         names = raw["names"]
         if (names == names[0]).all() and (raw["replica"] == reps[0]).all():
             # One owner (the library shares equal owners' name pointers).
             p = names[0].tolist()
             rid = RaidenId(_c_string(p[0]), _c_string(p[1]), _c_string(p[2]), reps[0])
-            return [(k, make(rid, h, d, st))
-                    for k, h, d, st in zip(keys, hosts, devs, status)]
-        ids = {}  # one RaidenId per distinct owner
+            owners = [rid] * n
+        else:
+            ids = {}  # one RaidenId per distinct owner
+            owners = []
+            for row, rep in zip(names.tolist(), reps):
+                owner = (*row, rep)
+                rid = ids.get(owner)
+                if rid is None:
+                    rid = RaidenId(_c_string(owner[0]), _c_string(owner[1]),
+                                   _c_string(owner[2]), owner[3])
+                    ids[owner] = rid
+                owners.append(rid)
+        # RaidenBlockId._of inlined: the objects of a long list are built
+        # without a call each.
+        new, cls = object.__new__, RaidenBlockId
         out = []
-        for i, row in enumerate(names.tolist()):
-            owner = (*row, reps[i])
-            rid = ids.get(owner)
-            if rid is None:
-                rid = RaidenId(_c_string(owner[0]), _c_string(owner[1]), _c_string(owner[2]),
-                               owner[3])
-                ids[owner] = rid
-            out.append((keys[i], make(rid, hosts[i], devs[i], status[i])))
+        for k, rid, h, d, v in zip(keys, owners, hosts, devs, stats):
+            b = new(cls)
+            b._raiden_id = rid
+            b._host_block_id = h
+            b._device_block_id = d
+            b._status = by_value[v]
+            out.append((k, b))
         return out
     finally:
         lib.kvx_slices_release(handle)
