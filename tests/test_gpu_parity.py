@@ -427,6 +427,64 @@ def test_raw_kernel_bad_id_flag(kvx, cuda):
                                  stream) == 3
 
 
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 7, 8, 33, 510])
+@pytest.mark.parametrize("W,order", [(2, 0), (4, 1), (6, 0)])
+def test_sliced_gather_of_32k_blocks_matches_oracle(kvx, oracle, cuda, n, W, order):
+    """32 KiB blocks at 16-byte vectors over an even number of whole
+    storages take the sliced gather (a quarter of each of 4 consecutive ids
+    per workgroup): any n, so the last group holds 1-4 ids, duplicate ids,
+    layer-major (0) and block-major (1) staging, byte for byte against the
+    oracle's extract."""
+    rng = np.random.default_rng(1000 + 10 * n + W)
+    P, bb = 600, 32768
+    host = [rng.integers(0, 256, (P, bb), dtype=np.uint8) for _ in range(W)]
+    pools = [torch.from_numpy(h).to(cuda) for h in host]
+    table = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64, device=cuda)
+    id_list = rng.integers(0, P, size=n)
+    ids = torch.tensor(id_list, dtype=torch.int64, device=cuda)
+    stg = torch.full((W * n * bb,), 0x3D, dtype=torch.uint8, device=cuda)
+    err = torch.zeros(1, dtype=torch.int32, device=cuda)
+    lib = kvx._capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.kvx_gather_blocks(table.data_ptr(), W, bb, P, ids.data_ptr(), n,
+                                 stg.data_ptr(), order, err.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    rc, want = oracle.extract([h.reshape(-1) for h in host], bb, id_list, order=order)
+    assert rc == 0
+    assert np.array_equal(stg.cpu().numpy(), want)
+
+
+def test_sliced_gather_bad_ids_in_a_group_and_in_the_last(kvx, cuda):
+    """The sliced gather with bad ids: two in the first group of 4, one in
+    the second, one in the last (short) group. Good blocks land, bad ones
+    leave their staging untouched, and the error flag is set."""
+    rng = np.random.default_rng(31)
+    W, P, bb = 2, 20, 32768
+    id_list = [3, 20, 5, -1, 8, 9, 99, 0, 7, -2]
+    n = len(id_list)
+    pools = [torch.from_numpy(rng.integers(0, 256, (P, bb), dtype=np.uint8)).to(cuda)
+             for _ in range(W)]
+    table = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64, device=cuda)
+    ids = torch.tensor(id_list, dtype=torch.int64, device=cuda)
+    stg = torch.full((W, n, bb), 0xAB, dtype=torch.uint8, device=cuda)
+    err = torch.zeros(1, dtype=torch.int32, device=cuda)
+    lib = kvx._capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.kvx_gather_blocks(table.data_ptr(), W, bb, P, ids.data_ptr(), n,
+                                 stg.data_ptr(), 0, err.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    got = stg.cpu().numpy()
+    for w in range(W):
+        ref = pools[w].cpu().numpy()
+        for i, b in enumerate(id_list):
+            if 0 <= b < P:
+                assert np.array_equal(got[w, i], ref[b]), (w, i)
+            else:
+                assert (got[w, i] == 0xAB).all(), (w, i)
+
+
 @pytest.mark.parametrize("bb", [16, 48, 36, 3, 1024])
 @pytest.mark.parametrize("id_list", [[-1, 25, 4, 99, 11], [-5, 30, 21]])
 def test_raw_small_blocks_bad_first_or_all(kvx, cuda, bb, id_list):
