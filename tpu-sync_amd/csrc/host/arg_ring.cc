@@ -104,8 +104,8 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
   if (copies.empty()) return OkStatus();
   const int vec = StridedVectorBytes(copies);
   std::vector<StridedEntryDev> table;
-  uint32_t grid = 0;
-  if (!BuildStridedTable(copies, vec, &table, &grid)) {
+  uint32_t grid = 0, long_tiles = 0;
+  if (!BuildStridedTable(copies, vec, &table, &grid, &long_tiles)) {
     return InvalidArgumentError("strided copy entry out of the kernel's limits");
   }
   const int64_t bytes = StridedImageBytes(table.size(), grid);
@@ -117,7 +117,7 @@ Status LaunchStridedThroughRing(ArgRing& ring, const std::vector<StridedCopy>& c
   if (kernel_start != nullptr) KVX_HIP_RETURN_IF_ERROR(hipEventRecord(kernel_start, stream));
   KVX_HIP_RETURN_IF_ERROR(LaunchStridedCopy(
       reinterpret_cast<const StridedEntryDev*>(ring.dev(off)),
-      static_cast<uint32_t>(table.size()), grid, vec, stream, max_workgroups));
+      static_cast<uint32_t>(table.size()), grid, vec, stream, max_workgroups, long_tiles));
   return keep.Commit();
 }
 

@@ -476,7 +476,7 @@ StatusOr<std::unique_ptr<StridedCopyPlan>> StridedCopyPlan::Create(
   std::vector<StridedEntryDev> table;
   if (!copies.empty()) {
     p->vec_ = StridedVectorBytes(copies);
-    if (!BuildStridedTable(copies, p->vec_, &table, &p->grid_)) {
+    if (!BuildStridedTable(copies, p->vec_, &table, &p->grid_, &p->long_tiles_)) {
       return InvalidArgumentError("strided copy entry out of the kernel's limits");
     }
   }
@@ -572,7 +572,7 @@ StatusOr<CopyFuture> StridedCopyPlan::Run(hipStream_t stream) {
       t0 = t1 = nullptr;
     }
     const hipError_t e = LaunchStridedCopy(static_cast<const StridedEntryDev*>(image_), n_,
-                                           grid_, vec_, stream);
+                                           grid_, vec_, stream, 0, long_tiles_);
     if (e != hipSuccess) {
       if (t0 != nullptr) (void)hipEventDestroy(t0);
       if (t1 != nullptr) (void)hipEventDestroy(t1);

@@ -186,6 +186,7 @@ class StridedCopyPlan {
   int vec_ = 16;
   uint32_t n_ = 0;
   uint32_t grid_ = 0;
+  uint32_t long_tiles_ = 0;  // the first tiles of the grid, long rows (sliced)
   int64_t bytes_ = 0;  // bytes one run moves
   void* image_ = nullptr;
   std::mutex mu_;

@@ -47,22 +47,27 @@ static_assert(sizeof(StridedEntryDev) == 64, "device table layout");
 
 // Builds the device table for `copies` with vector width `vec_bytes`;
 // returns false if an entry violates the kernel's limits. *grid receives the
-// workgroup count.
+// workgroup count. Entries whose rows span more than one tile come first in
+// the table (in the copies' order, then the others in theirs); *long_tiles
+// (if not null) receives their tiles, the first of the grid.
 bool BuildStridedTable(const std::vector<StridedCopy>& copies, int vec_bytes,
-                       std::vector<StridedEntryDev>* table, uint32_t* grid);
+                       std::vector<StridedEntryDev>* table, uint32_t* grid,
+                       uint32_t* long_tiles = nullptr);
 
 // Largest vector width (16, 8, 4, 2 or 1) dividing every address, size and
 // stride of `copies`.
 int StridedVectorBytes(const std::vector<StridedCopy>& copies);
 
 // Launches the copy of a device-resident table of `n` entries (built by
-// BuildStridedTable, `tiles` from its *grid) on `stream`. max_workgroups > 0
-// caps the grid (each workgroup then walks tiles with a stride of the grid),
-// for copies bound by PCIe rather than HBM; otherwise the launch reserves
-// LDS so that at most 2 of its workgroups share a CU.
+// BuildStridedTable, `tiles` from its *grid, `long_tiles` from its
+// *long_tiles) on `stream`. max_workgroups > 0 caps the grid (each workgroup
+// then walks tiles with a stride of the grid), for copies bound by PCIe
+// rather than HBM; otherwise the launch reserves LDS so that at most 2 of
+// its workgroups share a CU, and at 16-byte vectors moves the long-row tiles
+// sliced (0: every tile contiguous).
 hipError_t LaunchStridedCopy(const StridedEntryDev* table_dev, uint32_t n,
                              uint32_t tiles, int vec_bytes, hipStream_t stream,
-                             uint32_t max_workgroups = 0);
+                             uint32_t max_workgroups = 0, uint32_t long_tiles = 0);
 
 }  // namespace kvx
 
