@@ -55,6 +55,53 @@ def test_strided_copy_random_entries_match_oracle(kvx, cuda):
         assert np.array_equal(u8(dst), want), align
 
 
+def test_strided_copy_sliced_tile_groups_match_oracle(kvx, cuda):
+    """At 16-byte vectors tiles move in groups of 32 (a workgroup takes 1 KiB
+    of each tile of its group): long rows whose 32nd tile is partial, long
+    rows with a group and leftover tiles in several strided rows, two
+    groups; short-row entries whose 32nd tile holds fewer rows, one group
+    and leftover tiles, rows that are not a multiple of 1 KiB. Long and
+    short entries interleaved in one launch (long-row tiles are numbered
+    first), through a per-call launch and a plan, against the oracle."""
+    rng = np.random.default_rng(17)
+    n = 64 << 20
+    src_np = rng.integers(0, 256, n, dtype=np.uint8)
+    src = torch.from_numpy(src_np).to(cuda)
+    T = 32768
+    shapes = [  # (size, count, extra source stride, extra destination stride)
+        (3584, 284, 25088, 0),          # short: 9 rows a tile, 32 tiles, the last 5 rows
+        (1024, 1030, 7168, 0),          # short: 32 rows a tile, 33 tiles
+        (2000, 700, 48, 16),            # short: 16 rows a tile, 44 tiles
+        (32 * T - 1600, 1, 0, 0),       # long: 32 tiles, the last partial
+        (41 * T + 48, 3, 4096, 16),     # long: 42 tiles a row, three rows
+        (64 * T, 1, 0, 0),              # long: two groups
+        (T, 40, 16, 0),                 # one tile per row: short entry of 40 tiles
+    ]
+    order = rng.permutation(len(shapes))
+    entries, ora = [], []
+    s_pos = d_pos = 0
+    for k in order:
+        size, count, s_extra, d_extra = shapes[k]
+        s_stride, d_stride = size + s_extra, size + d_extra
+        ora.append((s_pos, d_pos, size, count, s_stride, d_stride))
+        s_pos += ((count - 1) * s_stride + size + 4095) // 4096 * 4096
+        d_pos += ((count - 1) * d_stride + size + 4095) // 4096 * 4096
+    assert s_pos <= n and d_pos <= n
+    want = np.zeros(n, np.uint8)
+    W.apply_entries(src_np, want, ora)
+    for use_plan in (False, True):
+        dst = torch.zeros(n, dtype=torch.uint8, device=cuda)
+        entries = [kvx.StridedEntry(src.data_ptr() + a, dst.data_ptr() + b, sz, c, ss, ds)
+                   for a, b, sz, c, ss, ds in ora]
+        if use_plan:
+            plan = kvx.StridedPlan(entries)
+            kvx.copy_strided(plan, device=0).Await()
+            plan.close()
+        else:
+            kvx.copy_strided(entries, device=0).Await()
+        assert np.array_equal(u8(dst), want), use_plan
+
+
 def test_strided_plan_matches_oracle_on_every_run(kvx, cuda):
     """A StridedPlan's device table (uploaded once) gives the oracle's bytes on
     every run: random entries of each vector width, three runs into cleared

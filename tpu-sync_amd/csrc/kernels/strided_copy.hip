@@ -12,14 +12,16 @@
 // scalar loads; lanes find their row with a multiply-shift instead of a
 // division. Loads and stores are non-temporal (every byte is touched once).
 //
-// Long rows at 16-byte vectors go sliced: their tiles are numbered first,
-// taken in plain workgroup order, and a workgroup moves a 1 KiB piece of
-// each of 32 consecutive tiles of its row instead of one contiguous tile.
-// Measured on MI355X in one process against contiguous tiles in XCD order:
-// a 1 GiB copy 77.6 -> 83.1 % of HBM peak, a 16 GiB copy 80.2 -> 84.2 %,
-// the 291-tensor Llama-3-8B pack 80.5 -> 85.4 %. Short-row tiles (column
-// splits) keep contiguous tiles in XCD order: plain order cost them 12
-// points.
+// At 16-byte vectors with one workgroup per tile, tiles go sliced: in a
+// group of 32 consecutive tiles (of one long row, or of one entry's runs of
+// short rows) the workgroup holding tile j moves the j-th 1 KiB of each of
+// the group's tiles instead of one contiguous tile. Long-row tiles are
+// numbered first and taken in plain workgroup order, short-row tiles after
+// them in XCD order. Measured on MI355X in one process against contiguous
+// tiles in XCD order: a 1 GiB copy 77.6 -> 83.3 % of HBM peak, a 16 GiB copy
+// 80.6 -> 84.4 %, the 291-tensor Llama-3-8B pack 80.4 -> 84.9 %, its 8-way
+// column split 78.4 -> 80.9 %. (Plain order cost the column split 12 points
+// with contiguous tiles and gained it nothing sliced.)
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -56,13 +58,14 @@ struct KArgs {
   const StridedEntryDev* table;
   const uint32_t* tile_entry;  // tile -> entry index
   uint32_t tiles;
-  uint32_t sliced_tiles;  // tiles [0, sliced_tiles) are long-row tiles, sliced
+  uint32_t sliced;        // tiles in whole groups of kSliceTiles go sliced
+  uint32_t sliced_tiles;  // tiles [0, sliced_tiles): long rows, in plain order
 };
 
-// Tiles of a long row taken as groups of kSliceTiles: the workgroup that
-// holds tile j of a group moves the j-th wave-sized slice (64 vectors) of
-// every tile of the group, so each workgroup's bytes are 32 pieces spread
-// over the group's 1 MiB (at 16-byte vectors) instead of one contiguous tile.
+// Tiles taken as groups of kSliceTiles: the workgroup that holds tile j of a
+// group moves the j-th wave-sized slice (64 vectors) of every tile of the
+// group, so each workgroup's bytes are 32 pieces spread over the group (1 MiB
+// of a long row at 16-byte vectors) instead of one contiguous tile.
 constexpr uint32_t kSliceVecs = 64;
 constexpr uint32_t kSliceTiles = kTileVecs / kSliceVecs;
 static_assert(kSliceTiles == kUnroll * (kThreads / 64), "one slice per wave and step");
@@ -93,6 +96,43 @@ __device__ __forceinline__ void copy_sliced(uint64_t src, uint64_t dst, uint32_t
   }
 }
 
+// Slice j of each tile of the group of kSliceTiles tiles from tile tb of an
+// entry of short rows (rows_per_tile rows per tile; only the entry's last
+// tile may hold fewer).
+template <typename V>
+__device__ __forceinline__ void copy_sliced_rows(const KVX_CONST StridedEntryDev& ent,
+                                                 uint32_t tb, uint32_t j) {
+  const uint32_t wave = threadIdx.x / 64;
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t rpt = ent.rows_per_tile;
+  const uint32_t vecs = ent.vecs;
+  const uint64_t magic = ent.div_magic;
+  V r[kUnroll];
+  uint64_t doff[kUnroll];
+  bool valid[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t c = u * (kThreads / 64) + wave;  // tile of the group
+    const uint32_t row0 = (tb + c) * rpt;
+    const uint32_t left = ent.count - row0;
+    const uint32_t total = (left < rpt ? left : rpt) * vecs;
+    const uint32_t k = j * kSliceVecs + lane;
+    valid[u] = k < total;
+    // Lanes past the tile re-read its last vector; only stores are predicated.
+    const uint32_t kk = valid[u] ? k : total - 1;
+    const uint32_t row = static_cast<uint32_t>((kk * magic) >> 32);
+    const uint64_t r_abs = row0 + row;
+    const uint64_t col = static_cast<uint64_t>(kk - row * vecs) * sizeof(V);
+    r[u] = __builtin_nontemporal_load(
+        (const KVX_GLOBAL V*)(ent.src + r_abs * ent.src_stride + col));
+    doff[u] = r_abs * ent.dst_stride + col;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    if (valid[u]) __builtin_nontemporal_store(r[u], (KVX_GLOBAL V*)(ent.dst + doff[u]));
+  }
+}
+
 // Moves tile `wg` (one entry's rows, or one slice of a long row).
 template <typename V>
 __device__ __forceinline__ void copy_tile(const KArgs& a, uint32_t wg) {
@@ -104,7 +144,7 @@ __device__ __forceinline__ void copy_tile(const KArgs& a, uint32_t wg) {
   const uint64_t dstride = ent->dst_stride;
   const uint32_t vecs = ent->vecs;
   const uint32_t t = wg - ent->tile_begin;
-  if (wg < a.sliced_tiles) {
+  if (a.sliced && ent->rows_per_tile == 0) {
     const uint32_t tpr = ent->tiles_per_row;
     const uint32_t row = t / tpr;
     const uint32_t ct = t - row * tpr;
@@ -112,6 +152,16 @@ __device__ __forceinline__ void copy_tile(const KArgs& a, uint32_t wg) {
     // group) stay contiguous.
     if (ct < (tpr & ~(kSliceTiles - 1))) {
       copy_sliced<V>(src + row * sstride, dst + row * dstride, vecs, ct);
+      return;
+    }
+  } else if (a.sliced) {
+    const uint32_t rpt = ent->rows_per_tile;
+    const uint32_t ntiles = (ent->count + rpt - 1) / rpt;
+    const uint32_t tb = t & ~(kSliceTiles - 1);
+    // Runs of short rows: tiles in whole groups of the entry go sliced, the
+    // entry's last tiles (fewer than a group) contiguous.
+    if (tb + kSliceTiles <= ntiles) {
+      copy_sliced_rows<V>(*ent, tb, t - tb);
       return;
     }
   }
@@ -259,7 +309,8 @@ hipError_t LaunchStridedCopy(const StridedEntryDev* table_dev, uint32_t n,
   a.tiles = tiles;
   const uint32_t grid = max_workgroups > 0 && max_workgroups < tiles ? max_workgroups : tiles;
   // Slicing is measured at 16-byte vectors with one workgroup per tile.
-  a.sliced_tiles = vec_bytes == 16 && grid == tiles && long_tiles <= tiles ? long_tiles : 0;
+  a.sliced = vec_bytes == 16 && grid == tiles ? 1u : 0u;
+  a.sliced_tiles = a.sliced && long_tiles <= tiles ? long_tiles : 0;
   // HBM-bound launches take the occupancy cap; PCIe-bound ones (a capped
   // grid) keep their few workgroups spread without it.
   const uint32_t lds = max_workgroups == 0 ? kLdsPerCu / kWorkgroupsPerCu : 0;
