@@ -52,8 +52,8 @@ HBM_PEAK_GBPS = 8000.0
 # 0.50001, WRITE 1.000): profiles/block_copy_llama3_8b_pmc.txt. Keyed by
 # (kernel, algorithmic bytes per launch).
 MEASURED_TRAFFIC = {
-    ("gather", 2 * 512 * 64 * 32768): int((524448.5 / 0.50001 + 1048635.9 / 1.0) * 1024),
-    ("scatter", 2 * 512 * 64 * 32768): int((524337.2 / 0.50001 + 1048594.5 / 1.0) * 1024),
+    ("gather", 2 * 512 * 64 * 32768): int((524452.0 / 0.50001 + 1048621.8 / 1.0) * 1024),
+    ("scatter", 2 * 512 * 64 * 32768): int((524348.2 / 0.50001 + 1048598.9 / 1.0) * 1024),
 }
 
 WORKLOADS = {
@@ -1783,8 +1783,9 @@ def main():
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
                      "frac_of_box_copy": frac_of_box(ach, args.box_copy_gbps),
                      "traffic": MEASURED_TRAFFIC.get((name, per_launch)),
-                     "kernel": f"block_copy_fast_kernel ({name.split('_')[0]}), {n} ids x {S} "
-                               f"storages per launch, {what}",
+                     "kernel": (("block_copy_sliced_gather_kernel (a quarter of each of 4 ids "
+                                 "per workgroup)" if gather else "block_copy_fast_kernel (scatter)")
+                                + f", {n} ids x {S} storages per launch, {what}"),
                      "launches": args.steps, "avg_launch_us": round(avg_s * 1e6, 2),
                      "bytes_per_launch": int(per_launch), "verified": True}
         log(f"{name} alone: {ach:.0f} GB/s ({ach / HBM_PEAK_GBPS:.1%} of HBM peak, "
@@ -1922,7 +1923,8 @@ def main():
         "scatter_roofline": iso["scatter"],
         "scatter_contiguous": iso["scatter_contiguous"],
         "box_copy": {"kernel": "strided_copy_kernel over one contiguous entry of the same "
-                               "bytes (2 workgroups per CU), HIP events on its stream",
+                               "bytes (sliced tile groups, 2 workgroups per CU), HIP events "
+                               "on its stream",
                      "achieved": round(args.box_copy_gbps, 1),
                      "frac": round(args.box_copy_gbps / HBM_PEAK_GBPS, 4), "verified": True},
         "placement": placement,
