@@ -121,12 +121,15 @@ def test_fp8_chunk_with_partial_payload_and_scales_matches_oracle(kvx, oracle, c
     mgr.close()
 
 
-def test_fp8_device_gather_moves_scales_in_the_same_launch(kvx, oracle, cuda):
-    rng = np.random.default_rng(41)
+@pytest.mark.parametrize("n", [20, 21, 23, 1])
+def test_fp8_device_gather_moves_scales_in_the_same_launch(kvx, oracle, cuda, n):
+    """Payload and scales of n ids in one launch (the fast kernel behind
+    the scale piece), n from 1 to 23, byte for byte."""
+    rng = np.random.default_rng(41 + n)
     layers, blocks = 3, 64
     kv_np, sc_np, kv, sc, bb = build(rng, cuda, layers, blocks)
     mgr = kvx.KVCacheManager(kv, host_blocks_to_allocate=4, scale_tables=sc)
-    ids = rng.choice(blocks, 20, replace=False).tolist()
+    ids = rng.choice(blocks, n, replace=False).tolist()
     n = len(ids)
     staging = torch.zeros(2 * layers * n * bb + layers * n * 32, dtype=torch.uint8,
                           device=cuda)

@@ -427,16 +427,17 @@ def test_raw_kernel_bad_id_flag(kvx, cuda):
                                  stream) == 3
 
 
+@pytest.mark.parametrize("bb", [32768, 16384])
 @pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 7, 8, 33, 510])
 @pytest.mark.parametrize("W,order", [(2, 0), (4, 1), (6, 0)])
-def test_sliced_gather_of_32k_blocks_matches_oracle(kvx, oracle, cuda, n, W, order):
+def test_sliced_gather_matches_oracle(kvx, oracle, cuda, n, W, order, bb):
     """32 KiB blocks at 16-byte vectors over an even number of whole
     storages take the sliced gather (a quarter of each of 4 consecutive ids
-    per workgroup): any n, so the last group holds 1-4 ids, duplicate ids,
-    layer-major (0) and block-major (1) staging, byte for byte against the
-    oracle's extract."""
-    rng = np.random.default_rng(1000 + 10 * n + W)
-    P, bb = 600, 32768
+    per workgroup; 16 KiB blocks, the fast kernel, alongside): any n, so the
+    last group holds 1-4 ids, duplicate ids, layer-major (0) and block-major
+    (1) staging, byte for byte against the oracle's extract."""
+    rng = np.random.default_rng(1000 + 10 * n + W + bb)
+    P = 600
     host = [rng.integers(0, 256, (P, bb), dtype=np.uint8) for _ in range(W)]
     pools = [torch.from_numpy(h).to(cuda) for h in host]
     table = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64, device=cuda)
@@ -455,12 +456,14 @@ def test_sliced_gather_of_32k_blocks_matches_oracle(kvx, oracle, cuda, n, W, ord
     assert np.array_equal(stg.cpu().numpy(), want)
 
 
-def test_sliced_gather_bad_ids_in_a_group_and_in_the_last(kvx, cuda):
-    """The sliced gather with bad ids: two in the first group of 4, one in
-    the second, one in the last (short) group. Good blocks land, bad ones
-    leave their staging untouched, and the error flag is set."""
+@pytest.mark.parametrize("bb", [32768, 16384])
+def test_sliced_gather_bad_ids_in_a_group_and_in_the_last(kvx, cuda, bb):
+    """The sliced gather (32 KiB blocks; 16 KiB blocks, the fast kernel,
+    alongside) with bad ids: two in the first group of 4, one in the second,
+    one in the last (short) group. Good blocks land, bad ones leave their
+    staging untouched, and the error flag is set."""
     rng = np.random.default_rng(31)
-    W, P, bb = 2, 20, 32768
+    W, P = 2, 20
     id_list = [3, 20, 5, -1, 8, 9, 99, 0, 7, -2]
     n = len(id_list)
     pools = [torch.from_numpy(rng.integers(0, 256, (P, bb), dtype=np.uint8)).to(cuda)
