@@ -15,7 +15,7 @@ lru_cache.h:260); hashes demoted to candidates and requested again are
 saved again.
 
 The test runs on a pinned tier and on a /dev/shm tier, the second with the
-benchmark's 32 MiB staging chunks, so its copies take the pageable bounce
+benchmark's staging ring (16 chunks of 32 MiB), so its copies take the pageable bounce
 lanes (host threads between the segment and pinned bounce buffers, SDMA
 between those and device staging) that the benchmark's churn measures.
 
@@ -76,7 +76,7 @@ def test_llama70b_prefix_cache_churn_bytes(kvx, cuda, host_alloc):
     tier = {}
     if host_alloc == "shm":
         tier = dict(host_alloc="shm", shm_key=f"kvx_test_churn_{os.getpid()}",
-                    staging_chunk_bytes=32 << 20, staging_chunks=4)
+                    staging_chunk_bytes=32 << 20, staging_chunks=16)
     mgr = kvx.KVCacheManager(pools, host_blocks_to_allocate=HOST_BLOCKS,
                              raiden_controller_address=store.raiden_controller_address,
                              **tier)
