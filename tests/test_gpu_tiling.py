@@ -196,6 +196,31 @@ def test_full_size_mlp_weight(kvx, cuda):
     assert torch.equal(back, w)
 
 
+@pytest.mark.parametrize("itemsize,P,H,W", [(2, 2, 2050, 2048), (1, 4, 1030, 4096),
+                                           (2, 2, 2103, 2048), (1, 4, 1061, 4096)])
+def test_detile_sliced_slot_groups(kvx, cuda, itemsize, P, H, W):
+    """Detiling packed layouts at 16-byte rows takes its slots sliced over
+    groups of 8 workgroups: shapes with whole groups and a last group of 1-7
+    workgroups (and rows past the matrix in the last tile row). The tiled
+    bytes come from the numpy formulation of the tiling; the detiled matrix
+    must equal the original, and tiling it back the numpy bytes."""
+    rng = np.random.default_rng(H + W + P)
+    dt = np.uint16 if itemsize == 2 else np.uint8
+    x = rng.integers(0, 1 << (8 * itemsize), (H, W), dtype=dt)
+    L = kvx.tiling.TiledLayout(itemsize, (H, W), [(8, 128), (P, 1)])
+    tiled_np = numpy_tile_2d(x, 8, 128, P)
+    assert tiled_np.nbytes == L.tiled_bytes
+    til = torch.from_numpy(tiled_np.view(np.uint8).copy()).to(cuda)
+    out = torch.zeros(H * W * itemsize, dtype=torch.uint8, device=cuda)
+    kvx.tiling.detile_buffer(L, til, out).Await()
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(dt).reshape(H, W), x)
+    back = torch.full((L.tiled_bytes,), 0x5A, dtype=torch.uint8, device=cuda)
+    kvx.tiling.tile_buffer(L, out, back).Await()
+    torch.cuda.synchronize()
+    assert np.array_equal(back.cpu().numpy(), tiled_np.view(np.uint8))
+
+
 def _sync_set(kvx, cuda, rng):
     """Mixed weights: tiled (packed bf16, packed int8, f32, general permuted,
     1-D) and row-major; device tensors hold the tiled bytes."""

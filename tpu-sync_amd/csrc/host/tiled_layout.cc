@@ -364,6 +364,7 @@ Status AppendTiledJobs(const TiledPlan& p, uint64_t tiled, uint64_t linear, int6
     j.vec = v;
     j.dev.mode = tile ? kTileStd : kDetileStd;
     j.dev.lanes_per_unit = two_lanes ? 2 : four_lanes ? 4 : 1;
+    j.dev.sliced = two_lanes || four_lanes ? 1u : 0u;
     if (tiled_order) {
       // Whole tile rows (cuts fall on them): units of tile rows [t_lo, t_hi).
       auto tile_row = [&](int64_t x) -> uint64_t {

@@ -112,7 +112,8 @@ struct TiledJobDev {
   FastDivU32 t_nt0;  // tile rows per matrix (nT0)
   uint32_t torder;   // 0: linear order, 1: tiled order
   uint32_t lanes_per_unit;  // packed units: 1, or 2 (P = 2) / 4 (P = 4) detiling at 16-byte rows
-  uint32_t pad0[2];
+  uint32_t sliced;  // detiling with 2 or 4 lanes per unit: slots in whole groups go sliced
+  uint32_t pad0;
   uint32_t h32;         // H (rows per batch matrix)
   uint32_t w32;         // W (columns)
   uint32_t nt0;         // tile rows per matrix = ceil(H / tH)
