@@ -897,8 +897,8 @@ def bench_weight_sync_tiled(torch, pkg, dev, args):
            "verified": True,
            # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE with the
            # same calibration (profiles/tiled_copy_weight_sync_trace.txt).
-           "detile_pack_traffic": int((7844363.6 / 0.50001 + 15688639.4) * 1024),
-           "tile_unpack_traffic": int((7844090.3 / 0.50001 + 15692173.8) * 1024),
+           "detile_pack_traffic": int((7844374.1 / 0.50001 + 15684196.2) * 1024),
+           "tile_unpack_traffic": int((7844090.4 / 0.50001 + 15692041.6) * 1024),
            "d2h_gbps": round(d2h_gbps, 2), "h2d_gbps": round(h2d_gbps, 2),
            "cpu_baseline": {"value": round(cpu[4], 2), "unit": "GB/s", "cores": 4, "kind": "port",
                             "all_threads_gbps": round(cpu[max(cpu)], 2), "all_threads": max(cpu),
@@ -960,8 +960,8 @@ def bench_tiled_int8(torch, pkg, dev, args):
         out[f"{name}_frac_of_box_copy"] = frac_of_box(g, args.box_copy_gbps)
     # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE with the
     # same calibration (profiles/tiled_copy_weight_sync_trace.txt).
-    out["detile_pack_traffic"] = int((458920.9 / 0.50001 + 918353.0) * 1024)
-    out["tile_unpack_traffic"] = int((458925.5 / 0.50001 + 917635.6) * 1024)
+    out["detile_pack_traffic"] = int((458919.1 / 0.50001 + 917621.9) * 1024)
+    out["tile_unpack_traffic"] = int((458925.5 / 0.50001 + 917616.7) * 1024)
     out["verified"] = True
     ws.close()
     del params, staging
