@@ -54,6 +54,10 @@ HBM_PEAK_GBPS = 8000.0
 MEASURED_TRAFFIC = {
     ("gather", 2 * 512 * 64 * 32768): int((524452.0 / 0.50001 + 1048621.8 / 1.0) * 1024),
     ("scatter", 2 * 512 * 64 * 32768): int((524348.2 / 0.50001 + 1048598.9 / 1.0) * 1024),
+    # The ascending and shuffled runs of ids (profiles/hbm_dram_stall_counters.txt,
+    # calibrated by the same run's 1 GiB copy: 0.500011 / 1.0).
+    ("scatter_contiguous", 2 * 512 * 64 * 32768): int((524345.0 / 0.500011 + 1048587.5) * 1024),
+    ("scatter_shuffled", 2 * 512 * 64 * 32768): int((524345.0 / 0.500011 + 1048604.5) * 1024),
 }
 
 WORKLOADS = {
@@ -182,6 +186,30 @@ def rocpd_summary(db_path):
             short = short if len(short) <= 60 else short[:57] + "..."
             print(f"{short:<60} {grid or 0:>9} {counter:>11} {cnt:>6} {avg:>13.1f} "
                   f"{mn:>13.1f} {mx:>13.1f}")
+    # Per dispatch of this library's kernels, each counter. Counters collected
+    # without _sum come back one row per hardware instance (a TCC counter: one
+    # per L2 channel): their spread over instances.
+    q = ("select p.dispatch_id, p.name, k.grid_x, k.end - k.start, p.counter_name, "
+         "count(*), sum(p.counter_value), min(p.counter_value), max(p.counter_value), "
+         "avg(p.counter_value * p.counter_value) from pmc_events p left join kernels k "
+         "on p.dispatch_id = k.dispatch_id where p.name like '%kvx::%' "
+         "group by p.dispatch_id, p.counter_name "
+         "order by p.dispatch_id, p.counter_name")
+    rows = list(cur.execute(q))
+    if rows:
+        print(f"\n{'dispatch':>8} {'kernel (pmc per dispatch)':<48} {'grid':>9} {'dur_us':>8} "
+              f"{'counter':>30} {'inst':>5} {'sum':>13} {'min':>11} {'max':>11} "
+              f"{'cv':>7} {'max/mean':>8}")
+        for did, name, grid, dur, counter, cnt, tot, mn, mx, sq in rows:
+            short = name.replace("void ", "").replace("(anonymous namespace)::", "")
+            if ">(" in short:
+                short = short[:short.index(">(") + 1]
+            short = short if len(short) <= 48 else short[:45] + "..."
+            mean = tot / cnt
+            cv = max(sq - mean * mean, 0.0) ** 0.5 / mean if mean else 0.0
+            print(f"{did:>8} {short:<48} {grid or 0:>9} {(dur or 0) / 1e3:>8.1f} "
+                  f"{counter:>30} {cnt:>5} {tot:>13.0f} {mn:>11.0f} {mx:>11.0f} "
+                  f"{cv:>7.4f} {mx / mean if mean else 0:>8.2f}")
     # Streams and the hardware queues their kernels ran on (memory copies that
     # run on SDMA engines have no compute queue).
     q = ("select stream_id, queue_id, name, count(*) from kernels "
@@ -1751,6 +1779,9 @@ def main():
     id_sets = [batch()[0] for _ in range(16)]
     gen_c = np.random.default_rng(5)
     contig_sets = [list(range(s0, s0 + n)) for s0 in gen_c.integers(0, P - n, 16)]
+    # The same runs of ids in a shuffled order: the same blocks and pages as
+    # the ascending launches, written in random order.
+    shuffled_sets = [gen_c.permutation(ids).tolist() for ids in contig_sets]
 
     def time_kernel(m, gather, idsets, launches):
         fn = m.gather if gather else m.scatter
@@ -1777,14 +1808,16 @@ def main():
 
     iso = {}
     for name, idsets in (("gather", id_sets), ("scatter", id_sets),
-                         ("scatter_contiguous", contig_sets)):
+                         ("scatter_contiguous", contig_sets),
+                         ("scatter_shuffled", shuffled_sets)):
         gather = name == "gather"
         avg_s, last_ids = time_kernel(mgr, gather, idsets, args.steps)
         verify_kernel(pools, gather, last_ids)
         per_launch = 2 * n * S * bb
         ach = per_launch / avg_s / 1e9
-        what = ("a fresh contiguous run of ids per launch" if name == "scatter_contiguous"
-                else "a fresh random id batch per launch")
+        what = {"scatter_contiguous": "a fresh contiguous run of ids per launch, ascending",
+                "scatter_shuffled": "the same contiguous runs of ids, each in a shuffled "
+                                    "order"}.get(name, "a fresh random id batch per launch")
         iso[name] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
                      "frac_of_box_copy": frac_of_box(ach, args.box_copy_gbps),
@@ -1928,6 +1961,7 @@ def main():
         "roofline": iso["gather"],
         "scatter_roofline": iso["scatter"],
         "scatter_contiguous": iso["scatter_contiguous"],
+        "scatter_shuffled": iso["scatter_shuffled"],
         "box_copy": {"kernel": "strided_copy_kernel over one contiguous entry of the same "
                                "bytes (sliced tile groups, 2 workgroups per CU), HIP events "
                                "on its stream",
