@@ -59,7 +59,9 @@ extern "C" {
 #define KVX_HOST_AUTO 3
 
 /* Transfer modes for copies whose runs are short (with a pinned mirror,
- * runs of at least direct_min_bytes always use one hipMemcpyAsync per run):
+ * runs of at least direct_min_bytes use one hipMemcpyAsync per run, except
+ * in KVX_MODE_AUTO while the other direction is idle, when such runs that
+ * average under 32 MiB per storage move in one zero-copy launch):
  *   KVX_MODE_STAGED: gather kernel -> device staging ring -> hipMemcpyAsync
  *     (and H2D -> scatter for reload), pipelined chunk by chunk;
  *   KVX_MODE_ZERO_COPY: one kernel moves the blocks between the pool and the

@@ -95,7 +95,9 @@ def random_spec(rng, blocks, host_blocks, max_entries=8, max_run=3):
 
 
 PATHS = {
-    "direct": dict(direct_min_bytes=1),
+    # Every run moves directly (staged mode: auto mode would move short runs
+    # zero-copy when the other direction is idle).
+    "direct": dict(direct_min_bytes=1, transfer_mode="staged"),
     "staged": dict(direct_min_bytes=1 << 40, staging_chunk_bytes=1 << 16, staging_chunks=2,
                    transfer_mode="staged"),
     "zero_copy": dict(direct_min_bytes=1 << 40, transfer_mode="zero_copy"),
@@ -855,6 +857,54 @@ def test_auto_duplex_short_runs_take_the_lanes(kvx, oracle, cuda):
     assert mir.transfer(True, d1, h1, ones) == 0
     mir.check(mgr, dev)
     assert kinds() == (3, 3)
+    mgr.close()
+
+
+def test_auto_mid_runs_alone_go_zero_copy(kvx, oracle, cuda):
+    """Auto mode on a pinned mirror with runs long enough to move directly
+    (at least 4 MiB) that average under 32 MiB: one zero-copy launch while
+    the other direction is idle, one DMA per run while a copy of the other
+    direction is in flight, and one DMA per run for runs of 32 MiB. Every
+    step's bytes against the oracle."""
+    import time
+    rng = np.random.default_rng(78)
+    layers, blocks, hb, bb = 4, 96, 96, 1 << 20
+    host, dev = dev_pools(rng, cuda, layers, 1, blocks, bb)
+    mgr = make_mgr(kvx, dev, hb)
+    mir = Mirror(host, hb)
+
+    def counts():
+        st = mgr.engine_stats()
+        return st["zero_copy_copies"], st["direct_copies"], st["memcpy_calls"]
+
+    print("lone offload, 8 MiB runs", flush=True)
+    mgr.d2h([0, 40], [0, 8], [8, 8]).Await()
+    assert mir.transfer(True, [0, 40], [0, 8], [8, 8]) == 0
+    mir.check(mgr, dev)
+    assert counts() == (1, 0, 0)
+    print("lone offload, one 32 MiB run", flush=True)
+    mgr.d2h([48], [32], [32]).Await()
+    assert mir.transfer(True, [48], [32], [32]) == 0
+    mir.check(mgr, dev)
+    assert counts() == (1, 1, layers)
+    # A load of 128 MiB (16 MiB runs, zero-copy: it is alone) keeps its
+    # kernel busy while an offload of 8 MiB runs is issued behind it; the
+    # two touch disjoint device and host blocks.
+    print("load of 16 MiB runs, then an offload of 8 MiB runs", flush=True)
+    f1 = mgr.h2d([0, 16], [16, 64], [16, 16])
+    f2 = mgr.d2h([0, 40], [64, 72], [8, 8])
+    f1.Await()
+    f2.Await()
+    assert mir.transfer(False, [0, 16], [16, 64], [16, 16]) == 0
+    assert mir.transfer(True, [0, 40], [64, 72], [8, 8]) == 0
+    mir.check(mgr, dev)
+    assert counts() == (2, 2, 3 * layers), counts()
+    time.sleep(0.4)
+    print("lone reload after a pause", flush=True)
+    mgr.h2d([64], [88], [8]).Await()
+    assert mir.transfer(False, [64], [88], [8]) == 0
+    mir.check(mgr, dev)
+    assert counts() == (3, 2, 3 * layers), counts()
     mgr.close()
 
 

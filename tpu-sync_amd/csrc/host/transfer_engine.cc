@@ -542,7 +542,29 @@ StatusOr<CopyFuture> TransferEngine::CopyPath(
   }
   if ((min_run != INT64_MAX && min_run * min_block >= opts_.direct_min_bytes) ||
       max_block > opts_.staging_chunk_bytes) {
-    // Long runs, or blocks that do not fit a staging chunk: one DMA per run.
+    // Long runs, or blocks that do not fit a staging chunk: one DMA per run;
+    // in auto mode, runs of a pinned mirror that average under
+    // auto_direct_min_run_bytes with the other direction idle: one
+    // zero-copy launch (see EngineOptions::auto_direct_min_run_bytes).
+    if (opts_.mode == TransferMode::kAuto && host_ok && !duplex &&
+        max_block <= (int64_t{1} << 32)) {
+      int64_t runs = 0;
+      for (int64_t s : sizes) runs += s > 0 ? 1 : 0;
+      int64_t sum_block = 0;
+      for (const StorageView& s : storages) sum_block += s.block_bytes;
+      // Mean bytes of a (storage, run): total blocks x the sum of the
+      // storages' block bytes over (runs x storages).
+      const double mean_run = static_cast<double>(total) * static_cast<double>(sum_block) /
+                              (static_cast<double>(runs) * static_cast<double>(storages.size()));
+      if (mean_run < static_cast<double>(opts_.auto_direct_min_run_bytes)) {
+        std::vector<int64_t> cdev, chost;
+        KVX_RETURN_IF_ERROR(PlanPairs(dir, src, dst, sizes, &cdev, &chost));
+        // One launch addresses fewer than 2^32 (block, storage) pairs.
+        if (static_cast<uint64_t>(cdev.size()) * storages.size() <= UINT32_MAX) {
+          return CopyZeroCopy(dir, storages, cdev, chost, dep);
+        }
+      }
+    }
     return CopyDirect(dir, storages, src, dst, sizes, dep);
   }
   std::vector<int64_t> cdev, chost;

@@ -79,7 +79,9 @@ struct ByteExtent {
 //          and a save at once reach the link's duplex rate, where zero-copy
 //          kernels in both directions interfere.
 // Copies whose runs are all at least direct_min_bytes use one
-// hipMemcpyAsync per (storage, run) in every mode.
+// hipMemcpyAsync per (storage, run) in every mode, except that kAuto moves
+// such runs of a pinned mirror zero-copy when they average under
+// auto_direct_min_run_bytes and the other direction is idle.
 enum class TransferMode : int { kAuto = 0, kStaged = 1, kZeroCopy = 2, kLanes = 3 };
 
 struct EngineOptions {
@@ -133,6 +135,18 @@ struct EngineOptions {
   // directions of a load + save pattern on the same path: a zero-copy save
   // next to lane loads is the slowest mix of all (94 ms).
   int64_t auto_duplex_window_us = 250000;
+  // kAuto moves a copy whose runs would go directly (all at least
+  // direct_min_bytes, or blocks larger than a staging chunk) with one
+  // zero-copy launch instead, when the mirror is pinned, the other direction
+  // is idle (as for auto_duplex_window_us) and the runs average under this
+  // many bytes per storage (0: never). A DMA per run pays a fixed cost per
+  // run that one launch does not. Measured on MI355X (16 runs of one block
+  // per storage, each direction alone, in one process alternating): 8 MiB
+  // runs 53.2 / 53.4 GB/s D2H / H2D directly against 55.2 / 55.8 zero-copy,
+  // 16 MiB 55.0 / 55.3 against 55.6 / 56.2, 32 MiB 56.0 / 56.3 against
+  // 55.8 / 56.3. With both directions at work the DMAs stay: zero-copy
+  // kernels in both directions interfere.
+  int64_t auto_direct_min_run_bytes = 32ll << 20;
   // Host regions the GPU cannot map (malloc, /dev/shm) move through pinned
   // bounce buffers that this many host threads fill and drain, one lane per
   // direction with its own streams, staging ring and SDMA engine (0: leave
